@@ -1,0 +1,68 @@
+// Host-side helpers shared by the C-ABI entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define STK_API __attribute__((visibility("default")))
+
+enum { STK_OK = 0, STK_EINVAL = -1, STK_EHIP = -2 };
+
+void stk_set_error(const char* fmt, ...);
+int stk_check_launch(const char* what);
+
+struct StkCheck {
+  bool ok;
+  const char* msg;
+};
+
+// STK_REQUIRE(cond, msg) or STK_REQUIRE(StkCheck)
+#define STK_REQUIRE_2(cond, msg)      \
+  do {                                \
+    if (!(cond)) {                    \
+      stk_set_error("%s", msg);       \
+      return STK_EINVAL;              \
+    }                                 \
+  } while (0)
+#define STK_REQUIRE_1(chk)            \
+  do {                                \
+    StkCheck _c = (chk);              \
+    if (!_c.ok) {                     \
+      stk_set_error("%s", _c.msg);    \
+      return STK_EINVAL;              \
+    }                                 \
+  } while (0)
+#define STK_GET_MACRO(_1, _2, NAME, ...) NAME
+#define STK_REQUIRE(...) STK_GET_MACRO(__VA_ARGS__, STK_REQUIRE_2, STK_REQUIRE_1)(__VA_ARGS__)
+
+StkCheck stk_check_kv(int dtype, int hq, int hkv, int n, int b, int d);
+
+inline size_t stk_align(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Bump allocator over a caller-provided workspace (256-byte aligned pieces).
+struct Carve {
+  char* p;
+  explicit Carve(void* base) : p(static_cast<char*>(base)) {}
+  template <typename T>
+  T* take(size_t count) {
+    T* r = reinterpret_cast<T*>(p);
+    p += stk_align(count * sizeof(T));
+    return r;
+  }
+};
+
+int stk_launch_states(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                      int n, int b, int d, const void* ids, int itype, int s,
+                      const uint8_t* active, int active_kind, const void* pred, int ptype, int sp,
+                      int32_t* slot, float* m, float* l, float* u, bool with_v, hipStream_t st);
+int stk_launch_states_skip(const void* q, const void* k, const void* v, int dtype, int hq,
+                           int hkv, int n, int b, int d, const void* ids, int itype, int s,
+                           const int32_t* slot_in, int slot_shared, float* m, float* l, float* u,
+                           hipStream_t st);
+int stk_launch_merge(const float* m, const float* l, const float* u, const uint8_t* inc, int h,
+                     int s, int d, float* out, hipStream_t st);
+
+extern "C" int stk_fallback(const void* q, const void* k, const void* v, int dtype, int hq,
+                            int hkv, int n, int b, int d, const void* selected, int sel_dtype,
+                            int sa, const uint8_t* flags, float* out, void* stream);

@@ -1,0 +1,155 @@
+// Shared device helpers for the gfx950 strict-topk kernels.
+//
+// Element types are carried as raw 16/32-bit storage and converted to FP32
+// in registers.  All kernels are written for 64-wide wavefronts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#define STK_WAVE 64
+
+namespace stk {
+
+enum DType : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+enum IType : int { IT_I32 = 0, IT_I64 = 1 };
+
+struct bf16s { uint16_t x; };
+struct f16s { uint16_t x; };
+
+__device__ __forceinline__ float cvt(float x) { return x; }
+__device__ __forceinline__ float cvt(bf16s x) { return __uint_as_float(uint32_t(x.x) << 16); }
+__device__ __forceinline__ float cvt(f16s x) {
+  _Float16 h;
+  __builtin_memcpy(&h, &x.x, 2);
+  return (float)h;
+}
+
+// Unpack one 32-bit word holding 2 (16-bit types) or 1 (fp32) elements.
+template <typename T> struct Unpack;
+template <> struct Unpack<float> {
+  static constexpr int per_word = 1;
+  __device__ __forceinline__ static void run(uint32_t w, float* out) { out[0] = __uint_as_float(w); }
+};
+template <> struct Unpack<bf16s> {
+  static constexpr int per_word = 2;
+  __device__ __forceinline__ static void run(uint32_t w, float* out) {
+    out[0] = __uint_as_float(w << 16);
+    out[1] = __uint_as_float(w & 0xffff0000u);
+  }
+};
+template <> struct Unpack<f16s> {
+  static constexpr int per_word = 2;
+  __device__ __forceinline__ static void run(uint32_t w, float* out) {
+    f16s a{uint16_t(w & 0xffffu)}, b{uint16_t(w >> 16)};
+    out[0] = cvt(a);
+    out[1] = cvt(b);
+  }
+};
+
+// Load VEC contiguous elements starting at p (aligned to VEC*sizeof(T) when
+// that is 4, 8 or 16 bytes) and convert to FP32.
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec(const T* p, float* out) {
+  constexpr int bytes = VEC * (int)sizeof(T);
+  if constexpr (bytes == 16) {
+    uint4 w = *reinterpret_cast<const uint4*>(p);
+    constexpr int pw = Unpack<T>::per_word;
+    Unpack<T>::run(w.x, out + 0 * pw);
+    Unpack<T>::run(w.y, out + 1 * pw);
+    Unpack<T>::run(w.z, out + 2 * pw);
+    Unpack<T>::run(w.w, out + 3 * pw);
+  } else if constexpr (bytes == 8) {
+    uint2 w = *reinterpret_cast<const uint2*>(p);
+    constexpr int pw = Unpack<T>::per_word;
+    Unpack<T>::run(w.x, out);
+    Unpack<T>::run(w.y, out + pw);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) out[i] = cvt(p[i]);
+  }
+}
+
+__device__ __forceinline__ int64_t load_id(const void* ids, int itype, int64_t i) {
+  return itype == IT_I64 ? reinterpret_cast<const int64_t*>(ids)[i]
+                         : (int64_t)reinterpret_cast<const int32_t*>(ids)[i];
+}
+__device__ __forceinline__ void store_id(void* ids, int itype, int64_t i, int64_t v) {
+  if (itype == IT_I64) reinterpret_cast<int64_t*>(ids)[i] = v;
+  else reinterpret_cast<int32_t*>(ids)[i] = (int32_t)v;
+}
+
+// ---------------------------------------------------------------- wave ops
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (STK_WAVE - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / STK_WAVE; }
+
+template <typename F>
+__device__ __forceinline__ float xor_reduce(float v, int from, int to, F op) {
+  // combine lanes with xor offsets from, 2*from, ..., to (inclusive)
+  for (int off = from; off <= to; off <<= 1) v = op(v, __shfl_xor(v, off));
+  return v;
+}
+struct OpAdd { __device__ float operator()(float a, float b) const { return a + b; } };
+struct OpMax { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+
+__device__ __forceinline__ float wave_sum(float v) { return xor_reduce(v, 1, 32, OpAdd()); }
+__device__ __forceinline__ float wave_max(float v) { return xor_reduce(v, 1, 32, OpMax()); }
+
+__device__ __forceinline__ int wave_any(bool p) { return __any(p); }
+
+// Block-wide reductions for up to 1024 threads; `red` needs 32 floats.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  int nw = (blockDim.x + STK_WAVE - 1) / STK_WAVE;
+  float r = 0.f;
+  for (int i = 0; i < nw; ++i) r += red[i];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  __syncthreads();
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  int nw = (blockDim.x + STK_WAVE - 1) / STK_WAVE;
+  float r = -INFINITY;
+  for (int i = 0; i < nw; ++i) r = fmaxf(r, red[i]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int block_or(int v, int* red) {
+  int w = __any(v != 0);
+  __syncthreads();
+  if (lane_id() == 0) red[wave_id()] = w;
+  __syncthreads();
+  int nw = (blockDim.x + STK_WAVE - 1) / STK_WAVE;
+  int r = 0;
+  for (int i = 0; i < nw; ++i) r |= red[i];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int block_count(int v, int* red) {
+  int w = __popcll(__ballot(v != 0));
+  __syncthreads();
+  if (lane_id() == 0) red[wave_id()] = w;
+  __syncthreads();
+  int nw = (blockDim.x + STK_WAVE - 1) / STK_WAVE;
+  int r = 0;
+  for (int i = 0; i < nw; ++i) r += red[i];
+  __syncthreads();
+  return r;
+}
+
+// exp(a - b) where an empty state (a == -inf) contributes exactly 0, also
+// when b is -inf.
+__device__ __forceinline__ float wexp(float a, float b) {
+  return a == -INFINITY ? 0.f : expf(a - b);
+}
+
+__device__ __forceinline__ bool is_bad(float x) { return !(fabsf(x) <= 3.402823466e38f); }
+
+}  // namespace stk

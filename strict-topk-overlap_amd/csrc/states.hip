@@ -1,0 +1,555 @@
+// Per-block softmax states, LSE merge, hybrid grouping, compact speculation
+// and the touch_kv checksum.
+//
+// Reference kernels restated (6Mikao9/strict-topk-overlap):
+//   strict_topk/kernels.py:42-71   _partial      -> k_states
+//   strict_topk/gqa.py:29-59       _partial      -> k_states (GQA, slot mode)
+//   strict_topk/kernels.py:74-91   _merge        -> k_merge
+//   strict_topk/kernels.py:94-117  _group        -> k_hybrid_group
+//   strict_topk/kernels.py:263-356 _mass_only / _compact_group / _compact_values
+//   strict_topk/kernels.py:250-260 _touch        -> k_touch
+#include "attn.hpp"
+#include "api.hpp"
+
+namespace stk {
+
+// Map a launch-order workgroup index to a logical index so that every XCD
+// (workgroups are dealt round-robin over 8 XCDs) receives one contiguous
+// range of logical workgroups.  Consecutive logical items share KV heads, so
+// their tiles meet in the same XCD-local L2.
+__device__ __forceinline__ int xcd_remap(int w, int total) {
+  constexpr int X = 8;
+  int xcd = w % X, r = w / X;
+  int base = total / X, extra = total % X;
+  int start = xcd * base + (xcd < extra ? xcd : extra);
+  return start + r;
+}
+
+struct StatesArgs {
+  const void* q; const void* k; const void* v;
+  const void* ids; int itype;
+  int hq, hkv, n, b, d, s;
+  const uint8_t* active; int active_kind;     // 0 none, 1 per head, 2 per slot
+  const void* pred; int ptype; int sp;        // slot mode: predicted rows
+  int32_t* slot;                              // slot mode output [hq, s]
+  float* m; float* l; float* u;               // [hq, s], [hq, s, d]
+  const int32_t* slot_in; int slot_shared;    // hierarchical repair: skip hits
+  int remap;
+};
+
+// One wave per (query head, slot).  SLOT mode restates gqa.py:38-43: the slot
+// is max{p : P[h,p] == A[h,s]} and only missing blocks are computed.
+template <typename T, int VEC, int NC, int U, bool WITH_V, bool SLOT>
+__global__ __launch_bounds__(256) void k_states(StatesArgs a) {
+  const int waves = blockDim.x / STK_WAVE;
+  int wg = a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
+  int64_t item = (int64_t)wg * waves + wave_id();
+  int64_t items = (int64_t)a.hq * a.s;
+  if (item >= items) return;
+  int h = (int)(item / a.s);
+  int j = (int)(item % a.s);
+  int64_t row = item;
+  int64_t bid = load_id(a.ids, a.itype, row);
+  bool enabled = true;
+  if (a.active_kind == 1) enabled = a.active[h] != 0;
+  else if (a.active_kind == 2) enabled = a.active[row] != 0;
+  if (SLOT) {
+    int best = -1;
+    for (int p = lane_id(); p < a.sp; p += STK_WAVE)
+      if (load_id(a.pred, a.ptype, (int64_t)h * a.sp + p) == bid) best = p;
+    for (int off = 1; off < STK_WAVE; off <<= 1) best = max(best, __shfl_xor(best, off));
+    if (lane_id() == 0) a.slot[row] = best;
+    enabled = best < 0;
+  }
+  if (a.slot_in && a.slot_in[(int64_t)(a.slot_shared ? 0 : h) * a.s + j] >= 0) return;
+  if (bid < 0 || bid >= a.n) enabled = false;   // invalid IDs never touch memory
+  Tile<T, VEC, NC> t;
+  t.init(a.d);
+  float m = -INFINITY, l = 0.f, acc[Tile<T, VEC, NC>::R];
+#pragma unroll
+  for (int i = 0; i < Tile<T, VEC, NC>::R; ++i) acc[i] = 0.f;
+  if (enabled) {
+    int g = a.hq / a.hkv;
+    int kv = h / g;
+    float qr[Tile<T, VEC, NC>::R];
+    t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)h * a.d, qr);
+    size_t off = (((size_t)kv * a.n + (size_t)bid) * a.b) * a.d;
+    const T* kb = reinterpret_cast<const T*>(a.k) + off;
+    const T* vb = reinterpret_cast<const T*>(a.v) + off;
+    float scale = 1.0f / sqrtf((float)a.d);
+    t.template accum<U, false, WITH_V>(qr, kb, vb, a.b, scale, m, l, acc);
+    t.finish(l, acc);
+  } else if (SLOT) {
+    return;   // hits keep their prediction state; scratch row left unwritten
+  }
+  if (lane_id() == 0) {
+    a.m[row] = m;
+    a.l[row] = l;
+  }
+  if (WITH_V) t.store(a.u + row * a.d, acc);
+}
+
+// LSE merge of S states per head (kernels.py:74-91).  256 threads arranged as
+// RG row groups x DT dim threads.
+struct MergeArgs {
+  const float* m; const float* l; const float* u; const uint8_t* inc;
+  int h, s, d;
+  float* out;
+};
+
+__global__ __launch_bounds__(256) void k_merge(MergeArgs a) {
+  __shared__ float red[32];
+  __shared__ float part[256 * 4];
+  int h = blockIdx.x;
+  const float* m = a.m + (size_t)h * a.s;
+  const float* l = a.l + (size_t)h * a.s;
+  float mx = -INFINITY;
+  for (int j = threadIdx.x; j < a.s; j += blockDim.x) {
+    bool on = !a.inc || a.inc[(size_t)h * a.s + j];
+    if (on) mx = fmaxf(mx, m[j]);
+  }
+  mx = block_max(mx, red);
+  if (mx == -INFINITY) mx = 0.f;
+  int dt = 1;
+  while (dt < a.d && dt < 256) dt <<= 1;
+  int rg = 256 / dt;
+  int tr = threadIdx.x / dt, td = threadIdx.x % dt;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float z = 0.f;
+  for (int j = tr; j < a.s; j += rg) {
+    bool on = !a.inc || a.inc[(size_t)h * a.s + j];
+    if (!on) continue;
+    float w = wexp(m[j], mx);
+    if (td == 0) z += w * l[j];
+    const float* ur = a.u + ((size_t)h * a.s + j) * a.d;
+    for (int c = 0; c < 4; ++c) {
+      int dd = td + c * dt;
+      if (dd < a.d) acc[c] += w * ur[dd];
+    }
+  }
+  z = block_sum(z, red);
+  for (int c = 0; c < 4; ++c) part[c * 256 + threadIdx.x] = acc[c];
+  __syncthreads();
+  if (tr == 0) {
+    float inv = 1.f / fmaxf(z, 1e-30f);
+    for (int c = 0; c < 4; ++c) {
+      int dd = td + c * dt;
+      if (dd >= a.d) break;
+      float sum = 0.f;
+      for (int r = 0; r < rg; ++r) sum += part[c * 256 + r * dt + td];
+      a.out[(size_t)h * a.d + dd] = sum * inv;
+    }
+  }
+}
+
+// Hybrid grouping (kernels.py:94-117).
+struct GroupArgs {
+  const float* m; const float* l; const float* u;
+  int h, s, d; float tau;
+  uint8_t* high; float* lm; float* ll; float* lu; float* labs;
+};
+
+__global__ __launch_bounds__(256) void k_hybrid_group(GroupArgs a) {
+  __shared__ float red[32];
+  __shared__ float part[2][256 * 4];
+  int h = blockIdx.x;
+  const float* m = a.m + (size_t)h * a.s;
+  const float* l = a.l + (size_t)h * a.s;
+  float gm = -INFINITY;
+  for (int j = threadIdx.x; j < a.s; j += blockDim.x) gm = fmaxf(gm, m[j]);
+  gm = block_max(gm, red);
+  float tot = 0.f;
+  for (int j = threadIdx.x; j < a.s; j += blockDim.x) tot += wexp(m[j], gm) * l[j];
+  tot = block_sum(tot, red);
+  float thr = a.tau * tot;
+  float lmx = -INFINITY;
+  for (int j = threadIdx.x; j < a.s; j += blockDim.x) {
+    bool hi = wexp(m[j], gm) * l[j] >= thr;
+    a.high[(size_t)h * a.s + j] = hi;
+    if (!hi) lmx = fmaxf(lmx, m[j]);
+  }
+  lmx = block_max(lmx, red);
+  if (lmx == -INFINITY) lmx = 0.f;
+  int dt = 1;
+  while (dt < a.d && dt < 256) dt <<= 1;
+  int rg = 256 / dt;
+  int tr = threadIdx.x / dt, td = threadIdx.x % dt;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f}, aab[4] = {0.f, 0.f, 0.f, 0.f};
+  float z = 0.f;
+  for (int j = tr; j < a.s; j += rg) {
+    bool hi = wexp(m[j], gm) * l[j] >= thr;
+    if (hi) continue;
+    float w = wexp(m[j], lmx);
+    if (td == 0) z += w * l[j];
+    const float* ur = a.u + ((size_t)h * a.s + j) * a.d;
+    for (int c = 0; c < 4; ++c) {
+      int dd = td + c * dt;
+      if (dd < a.d) {
+        float x = ur[dd];
+        acc[c] += w * x;
+        aab[c] += w * fabsf(x);
+      }
+    }
+  }
+  z = block_sum(z, red);
+  for (int c = 0; c < 4; ++c) {
+    part[0][c * 256 + threadIdx.x] = acc[c];
+    part[1][c * 256 + threadIdx.x] = aab[c];
+  }
+  __syncthreads();
+  if (tr == 0) {
+    for (int c = 0; c < 4; ++c) {
+      int dd = td + c * dt;
+      if (dd >= a.d) break;
+      float s0 = 0.f, s1 = 0.f;
+      for (int r = 0; r < rg; ++r) {
+        s0 += part[0][c * 256 + r * dt + td];
+        s1 += part[1][c * 256 + r * dt + td];
+      }
+      a.lu[(size_t)h * a.d + dd] = s0;
+      a.labs[(size_t)h * a.d + dd] = s1;
+    }
+  }
+  if (threadIdx.x == 0) {
+    a.lm[h] = lmx;
+    a.ll[h] = z;
+  }
+}
+
+// Compact grouping (kernels.py:281-309): rank high blocks in position order,
+// cap at C, overflow flag, retained IDs padded with -1, low (m, l).
+struct CompactArgs {
+  const void* q; const void* k; const void* v;
+  const void* ids; int itype;
+  int hq, hkv, n, b, d, s, c;
+  float tau;
+  const float* pm; const float* pl;
+  uint8_t* high; void* rids; uint8_t* overflow;
+  float* lm; float* ll; float* lu; float* labs;
+  float* m; float* l; float* u;
+};
+
+constexpr int kCompactMaxS = 32768;
+
+__global__ __launch_bounds__(256) void k_compact_group(CompactArgs a) {
+  __shared__ float red[32];
+  __shared__ int scan[256];
+  __shared__ uint32_t lowbits[kCompactMaxS / 32];
+  int h = blockIdx.x;
+  const float* m = a.pm + (size_t)h * a.s;
+  const float* l = a.pl + (size_t)h * a.s;
+  float gm = -INFINITY;
+  for (int j = threadIdx.x; j < a.s; j += blockDim.x) gm = fmaxf(gm, m[j]);
+  gm = block_max(gm, red);
+  float tot = 0.f;
+  for (int j = threadIdx.x; j < a.s; j += blockDim.x) tot += wexp(m[j], gm) * l[j];
+  tot = block_sum(tot, red);
+  float thr = a.tau * tot;
+  for (int j = threadIdx.x; j < a.c; j += blockDim.x)
+    store_id(a.rids, a.itype, (int64_t)h * a.c + j, -1);
+  for (int j = threadIdx.x; j < (a.s + 31) / 32; j += blockDim.x) lowbits[j] = 0u;
+  __syncthreads();
+  // rank = inclusive prefix count of high blocks in position order
+  int carry = 0;
+  float lmx = -INFINITY;
+  for (int j0 = 0; j0 < a.s; j0 += blockDim.x) {
+    int j = j0 + threadIdx.x;
+    int hi = (j < a.s) && (wexp(m[j], gm) * l[j] >= thr);
+    scan[threadIdx.x] = hi;
+    __syncthreads();
+    for (int off = 1; off < (int)blockDim.x; off <<= 1) {
+      int x = (int)threadIdx.x >= off ? scan[threadIdx.x - off] : 0;
+      __syncthreads();
+      scan[threadIdx.x] += x;
+      __syncthreads();
+    }
+    int rank = carry + scan[threadIdx.x];
+    int total = scan[blockDim.x - 1];
+    __syncthreads();
+    if (j < a.s) {
+      bool keep = hi && rank <= a.c;
+      a.high[(size_t)h * a.s + j] = keep;
+      if (keep) {
+        store_id(a.rids, a.itype, (int64_t)h * a.c + rank - 1,
+                 load_id(a.ids, a.itype, (int64_t)h * a.s + j));
+      } else {
+        lmx = fmaxf(lmx, m[j]);
+        atomicOr(&lowbits[j >> 5], 1u << (j & 31));
+      }
+    }
+    carry += total;
+  }
+  lmx = block_max(lmx, red);
+  if (lmx == -INFINITY) lmx = 0.f;
+  float z = 0.f;
+  for (int j = threadIdx.x; j < a.s; j += blockDim.x)
+    if ((lowbits[j >> 5] >> (j & 31)) & 1u) z += wexp(m[j], lmx) * l[j];
+  z = block_sum(z, red);
+  if (threadIdx.x == 0) {
+    a.overflow[h] = carry > a.c;
+    a.lm[h] = lmx;
+    a.ll[h] = z;
+  }
+}
+
+// Compact values (kernels.py:312-356): workgroup slot 0 walks the low blocks
+// of head h in the low frame (per token, with the abs envelope); slots 1..C
+// compute retained block states.  Low blocks are split over the 4 waves and
+// the wave sums are added in wave order.
+template <typename T, int VEC, int NC, int U>
+__global__ __launch_bounds__(256) void k_compact_values(CompactArgs a) {
+  using TL = Tile<T, VEC, NC>;
+  __shared__ float wl[4];
+  __shared__ float wu[2][4][kMaxD];
+  int h = blockIdx.x;
+  int slot = blockIdx.y;
+  int g = a.hq / a.hkv;
+  int kv = h / g;
+  TL t;
+  t.init(a.d);
+  float qr[TL::R];
+  t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)h * a.d, qr);
+  float scale = 1.0f / sqrtf((float)a.d);
+  const T* K = reinterpret_cast<const T*>(a.k);
+  const T* V = reinterpret_cast<const T*>(a.v);
+  if (slot == 0) {
+    float lmx = a.lm[h];
+    float l = 0.f, acc[TL::R], aab[TL::R];
+#pragma unroll
+    for (int i = 0; i < TL::R; ++i) acc[i] = aab[i] = 0.f;
+    for (int j = wave_id(); j < a.s; j += 4) {
+      if (a.high[(size_t)h * a.s + j]) continue;
+      int64_t bid = load_id(a.ids, a.itype, (int64_t)h * a.s + j);
+      if (bid < 0 || bid >= a.n) continue;
+      size_t off = (((size_t)kv * a.n + bid) * a.b) * a.d;
+      t.template accum_fixed_abs<U>(qr, K + off, V + off, a.b, scale, lmx, l, acc, aab);
+    }
+    t.finish(l, acc);
+    float dummy = 0.f;
+    t.finish(dummy, aab);
+    if (t.tok == 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        int base = (t.part + c * t.lpt) * VEC;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+          if (base + i < a.d) {
+            wu[0][wave_id()][base + i] = acc[c * VEC + i];
+            wu[1][wave_id()][base + i] = aab[c * VEC + i];
+          }
+      }
+    }
+    __syncthreads();
+    for (int dd = threadIdx.x; dd < a.d; dd += blockDim.x) {
+      float s0 = 0.f, s1 = 0.f;
+      for (int w = 0; w < 4; ++w) {
+        s0 += wu[0][w][dd];
+        s1 += wu[1][w][dd];
+      }
+      a.lu[(size_t)h * a.d + dd] = s0;
+      a.labs[(size_t)h * a.d + dd] = s1;
+    }
+    (void)wl;
+    return;
+  }
+  // retained slots: one wave per slot (waves 1..3 idle)
+  if (wave_id() != 0) return;
+  int c = slot - 1;
+  int64_t row = (int64_t)h * a.c + c;
+  int64_t bid = load_id(a.rids, a.itype, row);
+  float m = -INFINITY, l = 0.f, acc[TL::R];
+#pragma unroll
+  for (int i = 0; i < TL::R; ++i) acc[i] = 0.f;
+  if (bid >= 0 && bid < a.n) {
+    size_t off = (((size_t)kv * a.n + bid) * a.b) * a.d;
+    t.template accum<U, false, true>(qr, K + off, V + off, a.b, scale, m, l, acc);
+    t.finish(l, acc);
+  }
+  if (lane_id() == 0) {
+    a.m[row] = m;
+    a.l[row] = l;
+  }
+  t.store(a.u + row * a.d, acc);
+}
+
+// touch_kv checksum (kernels.py:250-260): one wave per (head, slot, tile).
+template <typename T>
+__global__ __launch_bounds__(64) void k_touch(const T* k, const T* v, const void* ids, int itype,
+                                              int h, int n, int b, int d, int s, float* out) {
+  int hh = blockIdx.x, j = blockIdx.y, tile = blockIdx.z;
+  int ntiles = gridDim.z;
+  int64_t bid = load_id(ids, itype, (int64_t)hh * s + j);
+  float sum = 0.f;
+  if (bid >= 0 && bid < n) {
+    size_t base = ((size_t)hh * n + bid) * (size_t)b * d;
+    for (int x = tile * 1024 + threadIdx.x; x < min((tile + 1) * 1024, b * d); x += 64)
+      sum += cvt(k[base + x]) + cvt(v[base + x]);
+  }
+  sum = wave_sum(sum);
+  if (threadIdx.x == 0) out[((size_t)hh * s + j) * ntiles + tile] = sum;
+}
+
+}  // namespace stk
+
+using namespace stk;
+
+// ---------------------------------------------------------------- C ABI
+static int launch_states(StatesArgs& a, int dtype, bool with_v, bool slot, hipStream_t st) {
+  int64_t items = (int64_t)a.hq * a.s;
+  if (items == 0) return STK_OK;
+  int grid = (int)((items + 3) / 4);
+  a.remap = grid >= 8 ? 1 : 0;
+  STK_DISPATCH_TILE(dtype, a.d, {
+    if (slot)
+      hipLaunchKernelGGL((k_states<T, VEC, NC, U, true, true>), dim3(grid), dim3(256), 0, st, a);
+    else if (with_v)
+      hipLaunchKernelGGL((k_states<T, VEC, NC, U, true, false>), dim3(grid), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_states<T, VEC, NC, U, false, false>), dim3(grid), dim3(256), 0, st, a);
+  });
+  return stk_check_launch("k_states");
+}
+
+int stk_launch_states(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                      int n, int b, int d, const void* ids, int itype, int s,
+                      const uint8_t* active, int active_kind, const void* pred, int ptype, int sp,
+                      int32_t* slot, float* m, float* l, float* u, bool with_v, hipStream_t st) {
+  StatesArgs a{};
+  a.q = q; a.k = k; a.v = v; a.ids = ids; a.itype = itype;
+  a.hq = hq; a.hkv = hkv; a.n = n; a.b = b; a.d = d; a.s = s;
+  a.active = active; a.active_kind = active ? active_kind : 0;
+  a.pred = pred; a.ptype = ptype; a.sp = sp; a.slot = slot;
+  a.m = m; a.l = l; a.u = u;
+  return launch_states(a, dtype, with_v, slot != nullptr, st);
+}
+
+int stk_launch_states_skip(const void* q, const void* k, const void* v, int dtype, int hq,
+                           int hkv, int n, int b, int d, const void* ids, int itype, int s,
+                           const int32_t* slot_in, int slot_shared, float* m, float* l, float* u,
+                           hipStream_t st) {
+  StatesArgs a{};
+  a.q = q; a.k = k; a.v = v; a.ids = ids; a.itype = itype;
+  a.hq = hq; a.hkv = hkv; a.n = n; a.b = b; a.d = d; a.s = s;
+  a.m = m; a.l = l; a.u = u;
+  a.slot_in = slot_in; a.slot_shared = slot_shared;
+  return launch_states(a, dtype, true, false, st);
+}
+
+int stk_launch_merge(const float* m, const float* l, const float* u, const uint8_t* inc, int h,
+                     int s, int d, float* out, hipStream_t st) {
+  MergeArgs a{m, l, u, inc, h, s, d, out};
+  hipLaunchKernelGGL(k_merge, dim3(h), dim3(256), 0, st, a);
+  return stk_check_launch("k_merge");
+}
+
+extern "C" {
+
+STK_API int stk_block_partials(const void* q, const void* k, const void* v, int dtype, int hq,
+                               int hkv, int n, int b, int d, const void* ids, int id_dtype, int s,
+                               const uint8_t* active, int active_kind, float* m, float* l, float* u,
+                               void* stream) {
+  STK_REQUIRE(stk_check_kv(dtype, hq, hkv, n, b, d));
+  STK_REQUIRE(q && k && v && ids && m && l && u, "null pointer");
+  STK_REQUIRE(s >= 0 && (id_dtype == IT_I32 || id_dtype == IT_I64), "bad ids");
+  STK_REQUIRE(active_kind >= 0 && active_kind <= 2, "bad active kind");
+  return stk_launch_states(q, k, v, dtype, hq, hkv, n, b, d, ids, id_dtype, s, active, active_kind,
+                           nullptr, 0, 0, nullptr, m, l, u, true, (hipStream_t)stream);
+}
+
+STK_API int stk_merge_partials(const float* m, const float* l, const float* u,
+                               const uint8_t* include, int h, int s, int d, float* out,
+                               void* stream) {
+  STK_REQUIRE(m && l && u && out, "null pointer");
+  STK_REQUIRE(h >= 0 && s > 0 && d > 0 && d <= kMaxD, "bad merge shape");
+  if (h == 0) return STK_OK;
+  return stk_launch_merge(m, l, u, include, h, s, d, out, (hipStream_t)stream);
+}
+
+STK_API size_t stk_exact_workspace_bytes(int hq, int s, int d) {
+  return stk_align((size_t)hq * s * 4) * 2 + stk_align((size_t)hq * s * d * 4);
+}
+
+STK_API int stk_exact_attention(const void* q, const void* k, const void* v, int dtype, int hq,
+                                int hkv, int n, int b, int d, const void* ids, int id_dtype, int s,
+                                float* out, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  STK_REQUIRE(stk_check_kv(dtype, hq, hkv, n, b, d));
+  STK_REQUIRE(q && k && v && ids && out, "null pointer");
+  STK_REQUIRE(s > 0, "ids must be nonempty");
+  STK_REQUIRE(workspace && workspace_bytes >= stk_exact_workspace_bytes(hq, s, d),
+              "workspace too small");
+  Carve w(workspace);
+  float* m = w.take<float>((size_t)hq * s);
+  float* l = w.take<float>((size_t)hq * s);
+  float* u = w.take<float>((size_t)hq * s * d);
+  hipStream_t st = (hipStream_t)stream;
+  int rc = stk_launch_states(q, k, v, dtype, hq, hkv, n, b, d, ids, id_dtype, s, nullptr, 0,
+                             nullptr, 0, 0, nullptr, m, l, u, true, st);
+  if (rc) return rc;
+  return stk_launch_merge(m, l, u, nullptr, hq, s, d, out, st);
+}
+
+STK_API int stk_speculate(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                          int n, int b, int d, const void* pred, int pred_dtype, int s, int mode,
+                          float tau, int capacity, float* m, float* l, float* u, uint8_t* high,
+                          float* low_m, float* low_l, float* low_u, float* low_abs,
+                          void* retained_ids, uint8_t* overflow, float* mass_m, float* mass_l,
+                          void* stream) {
+  STK_REQUIRE(stk_check_kv(dtype, hq, hkv, n, b, d));
+  STK_REQUIRE(q && k && v && pred && m && l && u, "null pointer");
+  STK_REQUIRE(s > 0, "predicted ids must be nonempty");
+  STK_REQUIRE(mode >= 0 && mode <= 2, "mode must be 0 (saved), 1 (hybrid) or 2 (compact)");
+  STK_REQUIRE(tau >= 0.f && tau <= 1.f, "mass_threshold must be in [0,1]");
+  hipStream_t st = (hipStream_t)stream;
+  if (mode != 2) {
+    int rc = stk_launch_states(q, k, v, dtype, hq, hkv, n, b, d, pred, pred_dtype, s, nullptr, 0,
+                               nullptr, 0, 0, nullptr, m, l, u, true, st);
+    if (rc || mode == 0) return rc;
+    STK_REQUIRE(high && low_m && low_l && low_u && low_abs, "null hybrid output");
+    GroupArgs g{m, l, u, hq, s, d, tau, high, low_m, low_l, low_u, low_abs};
+    hipLaunchKernelGGL(k_hybrid_group, dim3(hq), dim3(256), 0, st, g);
+    return stk_check_launch("k_hybrid_group");
+  }
+  STK_REQUIRE(high && low_m && low_l && low_u && low_abs && retained_ids && overflow && mass_m &&
+                  mass_l,
+              "null compact output");
+  STK_REQUIRE(capacity >= 1 && capacity <= s, "bad compact capacity");
+  STK_REQUIRE(s <= kCompactMaxS, "compact speculation supports at most 32768 predicted blocks");
+  int rc = stk_launch_states(q, k, v, dtype, hq, hkv, n, b, d, pred, pred_dtype, s, nullptr, 0,
+                             nullptr, 0, 0, nullptr, mass_m, mass_l, nullptr, false, st);
+  if (rc) return rc;
+  CompactArgs c{};
+  c.q = q; c.k = k; c.v = v; c.ids = pred; c.itype = pred_dtype;
+  c.hq = hq; c.hkv = hkv; c.n = n; c.b = b; c.d = d; c.s = s; c.c = capacity; c.tau = tau;
+  c.pm = mass_m; c.pl = mass_l; c.high = high; c.rids = retained_ids; c.overflow = overflow;
+  c.lm = low_m; c.ll = low_l; c.lu = low_u; c.labs = low_abs; c.m = m; c.l = l; c.u = u;
+  hipLaunchKernelGGL(k_compact_group, dim3(hq), dim3(256), 0, st, c);
+  rc = stk_check_launch("k_compact_group");
+  if (rc) return rc;
+  STK_DISPATCH_TILE(dtype, d, {
+    hipLaunchKernelGGL((k_compact_values<T, VEC, NC, U>), dim3(hq, capacity + 1), dim3(256), 0,
+                       st, c);
+  });
+  return stk_check_launch("k_compact_values");
+}
+
+STK_API int stk_touch_kv(const void* k, const void* v, int dtype, int h, int n, int b, int d,
+                         const void* pred, int pred_dtype, int s, float* out, void* stream) {
+  STK_REQUIRE(stk_check_kv(dtype, h, h, n, b, d));
+  STK_REQUIRE(k && v && pred && out, "null pointer");
+  if (s == 0 || h == 0) return STK_OK;
+  int nt = (b * d + 1023) / 1024;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DT_BF16)
+    hipLaunchKernelGGL(k_touch<bf16s>, dim3(h, s, nt), dim3(64), 0, st, (const bf16s*)k,
+                       (const bf16s*)v, pred, pred_dtype, h, n, b, d, s, out);
+  else if (dtype == DT_F16)
+    hipLaunchKernelGGL(k_touch<f16s>, dim3(h, s, nt), dim3(64), 0, st, (const f16s*)k,
+                       (const f16s*)v, pred, pred_dtype, h, n, b, d, s, out);
+  else
+    hipLaunchKernelGGL(k_touch<float>, dim3(h, s, nt), dim3(64), 0, st, (const float*)k,
+                       (const float*)v, pred, pred_dtype, h, n, b, d, s, out);
+  return stk_check_launch("k_touch");
+}
+
+}  // extern "C"

@@ -1,0 +1,386 @@
+"""GPU parity: the HIP path against the FP64 oracle on identical inputs.
+
+Bars: block IDs bit-exact (ties toward the lower index, canonical order);
+FP32 scores bit-exact to float32(oracle FP64 score); outputs within the
+reference tolerance |err| <= 3e-4 + 3e-4 |ref| (tests/check_correctness.py:22);
+discrete flags exact on the reference's known-answer inputs.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import stk_oracle as O
+from tests import cases as C
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from strict_topk import _lib
+    _lib.lib()   # fail loudly if the HIP library is missing
+
+
+def dev(*ts):
+    return [t.to(DEV) for t in ts]
+
+
+def np_(*ts):
+    return [C.f64(t) if t.is_floating_point() else C.ids_np(t) for t in ts]
+
+
+def check(out, expected, what=""):
+    m = C.error_metrics(C.f64(out), expected)
+    assert m["passed"], (what, m)
+
+
+# --------------------------------------------------------------- selection
+def test_selector_scores_and_ids_bit_exact():
+    from strict_topk.selector import block_scores, select_blocks
+    gen = torch.Generator().manual_seed(C.SEED)
+    q = torch.randn((3, 70), generator=gen).half()
+    keys = torch.randn((3, 37, 7, 70), generator=gen).half()
+    lo, hi = keys.amin(dim=2).float(), keys.amax(dim=2).float()
+    q[0].zero_()
+    ref = O.bound_scores(*np_(q, lo, hi))
+    qd, lod, hid = dev(q, lo, hi)
+    scores = block_scores(qd, lod, hid)
+    assert scores.dtype == torch.float32 and scores.shape == (3, 37)
+    assert np.array_equal(scores.cpu().numpy(), ref.astype(np.float32))
+    for topk in (1, 11, 37):
+        ids = select_blocks(qd, lod, hid, topk)
+        assert ids.shape == (3, topk) and ids.dtype == torch.int32 and ids.is_contiguous()
+        assert ids.cpu().numpy().tolist() == O.topk_ids(ref, topk).tolist()
+    assert select_blocks(qd, lod, hid, 11)[0].cpu().tolist() == list(range(11))
+
+
+def test_gqa_select_ids_bit_exact():
+    from strict_topk import gqa
+    for hq, hkv, n, b, d, topk in [(6, 2, 23, 7, 13, 5), (16, 8, 512, 32, 128, 64),
+                                   (48, 4, 300, 4, 128, 200), (4, 4, 64, 32, 64, 8),
+                                   (2, 1, 5000, 2, 32, 700)]:
+        gen = torch.Generator().manual_seed(hq * 1000 + n)
+        q = torch.randn((hq, d), generator=gen).bfloat16()
+        k = torch.randn((hkv, n, b, d), generator=gen).bfloat16()
+        lo, hi = k.amin(2).float(), k.amax(2).float()
+        q[0].zero_()
+        ref = O.select_blocks(*np_(q, lo, hi), topk)
+        ids = gqa.select_blocks(*dev(q, lo, hi), topk)
+        assert ids.cpu().numpy().tolist() == ref.tolist(), (hq, n, topk)
+
+
+def test_select_rejects_bad_k():
+    from strict_topk import gqa
+    q = torch.randn((4, 8), device=DEV)
+    lo = torch.zeros((2, 10, 8), device=DEV)
+    with pytest.raises(RuntimeError):
+        gqa.select_blocks(q, lo, lo, 11)
+    assert gqa.select_blocks(q, lo, lo, 0).shape == (4, 0)
+
+
+# ----------------------------------------------------------------- kernels
+REPAIRS = ["split", "fused", "signed", "signed_fused"]
+
+
+def _repair_fn(name):
+    from strict_topk import fused, kernels, signed_fused, signed_repair
+    return {"split": kernels.repair, "fused": fused.repair_fused,
+            "signed": signed_repair.repair_signed,
+            "signed_fused": signed_fused.repair_signed_fused}[name]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_kernels_strict_paths(dtype):
+    from strict_topk.kernels import exact_attention, speculate
+    for name, *ts in C.correctness_cases(dtype):
+        expected = O.attention(*np_(ts[0], ts[1], ts[2], ts[4]))
+        q, k, v, p, a = dev(*ts)
+        check(exact_attention(q, k, v, a), expected, (name, "exact"))
+        for mode, thr in [("saved", .1), ("hybrid", .05), ("hybrid", .2), ("hybrid", 1.),
+                          ("compact", .05), ("compact", .2), ("compact", 1.)]:
+            st = speculate(q, k, v, p, mode=mode, mass_threshold=thr)
+            for impl in REPAIRS:
+                res = _repair_fn(impl)(q, k, v, a, p, st)
+                check(res.output, expected, (name, mode, thr, impl))
+                if mode != "saved" and thr == 1. and name in C.EXPECTED_FALLBACK:
+                    assert int(res.fallback.sum()) == C.EXPECTED_FALLBACK[name], (name, mode, impl)
+                if impl in ("signed", "signed_fused"):
+                    assert res.approximate_heads is None
+
+
+def test_block_partials_and_merge_match_oracle():
+    from strict_topk.kernels import block_partials, merge_partials
+    for name, *ts in C.correctness_cases(torch.bfloat16):
+        qn, kn, vn, pn, an = np_(*ts)
+        q, k, v, p, a = dev(*ts)
+        st = block_partials(q, k, v, a)
+        ref = O.block_states(qn, kn, vn, an)
+        np.testing.assert_allclose(st.m.cpu().double().numpy(), ref.m, rtol=1e-5, atol=1e-5)
+        # compare normalised states to be frame-independent
+        lu = st.u.cpu().double().numpy() / st.l.cpu().double().numpy()[..., None]
+        np.testing.assert_allclose(lu, ref.u / ref.l[..., None], rtol=1e-3, atol=3e-4)
+        mask = torch.zeros(a.shape, dtype=torch.bool, device=DEV)
+        mask[:, ::2] = True
+        st2 = block_partials(q, k, v, a, mask)
+        assert torch.isinf(st2.m[:, 1::2]).all() and (st2.l[:, 1::2] == 0).all()
+        inc = mask.clone()
+        check(merge_partials(st, inc), O.attention(qn, kn, vn, an, inc.cpu().numpy()), name)
+        head = torch.zeros(a.shape[0], dtype=torch.bool, device=DEV)
+        head[0] = True
+        st3 = block_partials(q, k, v, a, head)
+        assert torch.isinf(st3.m[1:]).all()
+
+
+def test_speculate_fields_match_oracle():
+    from strict_topk.kernels import speculate
+    gen = torch.Generator().manual_seed(99)
+    h, n, b, d, s = 4, 40, 16, 64, 12
+    q = torch.randn(h, d, generator=gen).half()
+    k = (torch.randn(h, n, b, d, generator=gen) * 2).half()
+    v = torch.randn(h, n, b, d, generator=gen).half()
+    p = torch.stack([torch.randperm(n, generator=gen)[:s] for _ in range(h)]).int()
+    qn, kn, vn, pn = np_(q, k, v, p)
+    qd, kd, vd, pd = dev(q, k, v, p)
+    for mode in ("hybrid", "compact"):
+        for thr in (.05, .1, .3):
+            ref = O.speculate(qn, kn, vn, pn, mode=mode, mass_threshold=thr, keep_mass=True)
+            got = speculate(qd, kd, vd, pd, mode=mode, mass_threshold=thr, keep_mass=True)
+            # decisions are exact unless a mass sits within 1e-5 of the threshold
+            st = O.block_states(qn, kn, vn, pn)
+            mass = np.exp(st.m - st.m.max(1, keepdims=True)) * st.l
+            frac = mass / mass.sum(1, keepdims=True)
+            safe = np.abs(frac - thr) > 1e-5
+            assert (got.high.cpu().numpy() == ref.high)[safe].all(), (mode, thr)
+            if safe.all():
+                assert np.array_equal(got.high.cpu().numpy(), ref.high)
+                if mode == "compact":
+                    assert got.retained_ids.cpu().numpy().tolist() == ref.retained_ids.tolist()
+                    assert got.overflow.cpu().numpy().tolist() == ref.overflow.tolist()
+                    assert got.retained_ids.dtype == pd.dtype
+                np.testing.assert_allclose(got.low.m.cpu().numpy(), ref.low.m, rtol=1e-5, atol=1e-5)
+                np.testing.assert_allclose(got.low.l.cpu().numpy(), ref.low.l, rtol=1e-4)
+                np.testing.assert_allclose(got.low.u.cpu().numpy(), ref.low.u, rtol=1e-3, atol=1e-4)
+                np.testing.assert_allclose(got.low_abs.cpu().numpy(), ref.low_abs, rtol=1e-3, atol=1e-4)
+            np.testing.assert_allclose(got.mass_m.cpu().numpy(), ref.mass_m, rtol=1e-5, atol=1e-5)
+            np.testing.assert_allclose(got.mass_l.cpu().numpy(), ref.mass_l, rtol=1e-4)
+
+
+@pytest.mark.parametrize("mode", ["hybrid", "compact"])
+@pytest.mark.parametrize("impl", ["fused", "signed", "signed_fused"])
+def test_extra_mass_budget(mode, impl):
+    from strict_topk.kernels import speculate
+    q, k, v, p, a, extra_set = C.budget_case()
+    strict = O.attention(*np_(q, k, v, a))
+    with_extra = O.attention(*np_(q, k, v, extra_set))
+    extra_mass = math.exp(-3) / (2 + math.exp(-3))
+    q, k, v, p, a = dev(q, k, v, p, a)
+    fn = _repair_fn(impl)
+    st = speculate(q, k, v, p, mode=mode, mass_threshold=.2, keep_mass=True)
+    low = fn(q, k, v, a, p, st, max_extra_mass=.01)
+    assert not low.approximate_heads.item() and low.extra_mass_bound.item() == 0.
+    check(low.output, strict)
+    high = fn(q, k, v, a, p, st, max_extra_mass=.1)
+    assert high.approximate_heads.item()
+    assert extra_mass <= high.extra_mass_bound.item() <= .1
+    assert abs(high.extra_mass_bound.item() - math.exp(-3) / (1 + math.exp(-3))) < 1e-6
+    check(high.output, with_extra)
+    forced = fn(q, k, v, a, p, st, cancellation_tol=2., max_extra_mass=.1)
+    assert forced.fallback.item() and not forced.approximate_heads.item()
+    assert forced.extra_mass_bound.item() == 0.
+    check(forced.output, strict)
+    if impl != "fused":
+        assert low.positive_jobs.item() == 1 and low.total_jobs.item() == 2
+        assert high.positive_jobs.item() == 1 and high.total_jobs.item() == 1
+        assert low.positive_jobs.dtype == torch.int32
+
+
+def test_budget_requires_keep_mass():
+    from strict_topk.fused import repair_fused
+    from strict_topk.kernels import speculate
+    from strict_topk.signed_fused import repair_signed_fused
+    q, k, v, p, a, _ = dev(*C.budget_case())
+    st = speculate(q, k, v, p, mode="hybrid", mass_threshold=.2)
+    for fn in (repair_fused, repair_signed_fused):
+        with pytest.raises(ValueError):
+            fn(q, k, v, a, p, st, max_extra_mass=.1)
+        with pytest.raises(ValueError):
+            fn(q, k, v, a, p, st, max_extra_mass=1.5)
+
+
+def test_signed_fused_underflow_regression():
+    from strict_topk.kernels import speculate
+    from strict_topk.signed_fused import repair_signed_fused
+    ts = C.underflow_case()
+    expected = O.attention(*np_(ts[0], ts[1], ts[2], ts[4]))
+    q, k, v, p, a = dev(*ts)
+    pred = speculate(q, k, v, p, mode="hybrid", mass_threshold=1.)
+    res = repair_signed_fused(q, k, v, a, p, pred)
+    check(res.output, expected)
+    assert res.fallback.item()
+
+
+def test_schedule_queue_order():
+    """Queue = misses in selected order, then wrong-low blocks in predicted order."""
+    from strict_topk.kernels import speculate
+    from strict_topk.signed_fused import repair_signed_fused
+    for name, *ts in C.correctness_cases(torch.float16):
+        if not name.startswith("random_unordered"):
+            continue
+        qn, kn, vn, pn, an = np_(*ts)
+        q, k, v, p, a = dev(*ts)
+        for mode in ("saved", "hybrid"):
+            st = speculate(q, k, v, p, mode=mode, mass_threshold=.2)
+            res = repair_signed_fused(q, k, v, a, p, st)
+            for h in range(pn.shape[0]):
+                _, miss = O.membership(pn[h], an[h])
+                assert res.positive_jobs[h].item() == int(miss.sum())
+            if mode == "hybrid":
+                high = st.high.cpu().numpy()
+                for h in range(pn.shape[0]):
+                    hit, _ = O.membership(pn[h], an[h])
+                    low_hit = (hit & ~high[h]).any()
+                    wrong = (~hit & ~high[h]) & low_hit
+                    assert res.total_jobs[h].item() == int(res.positive_jobs[h].item() + wrong.sum())
+
+
+# --------------------------------------------------------------------- GQA
+def test_tiny_gqa_known_answers():
+    from strict_topk import gqa, gqa_light
+    q, k, v, p = dev(*C.tiny_gqa())
+    union = (8 * math.e ** 5 - 5) / (math.e ** 5 + 1)
+    st = gqa.partials(q, k, v, p)
+    assert gqa.exact(q, k, v, p).cpu()[:, 0].tolist() == pytest.approx([8., -5.], abs=1e-6)
+    assert gqa.repair_saved(q, k, v, 1 - p, p, st).cpu()[:, 0].tolist() == pytest.approx([-5., 8.], abs=1e-6)
+    assert gqa.repair_union(q, k, v, 1 - p, p, st).cpu()[:, 0].tolist() == pytest.approx([union] * 2, rel=1e-6)
+    assert gqa_light.repair_saved_light(q, k, v, 1 - p, p, st).cpu()[:, 0].tolist() == pytest.approx([-5., 8.], abs=1e-6)
+
+
+@pytest.mark.parametrize("hq", [6, 16])
+def test_gqa_paths(hq):
+    from strict_topk import gqa, gqa_light
+    for name, *ts in C.gqa_cases(hq=hq, hkv=2 if hq == 6 else 4):
+        qn, kn, vn, pn, an = np_(*ts)
+        expected = O.attention(qn, kn, vn, an)
+        hit = (an[:, :, None] == pn[:, None, :]).any(-1)
+        q, k, v, p, a = dev(*ts)
+        st = gqa.partials(q, k, v, p)
+        ref = O.block_states(qn, kn, vn, pn)
+        np.testing.assert_allclose(st.m.cpu().double().numpy(), ref.m, rtol=1e-5, atol=1e-4)
+        check(gqa.exact(q, k, v, a), expected, (name, "exact"))
+        check(gqa.repair_saved(q, k, v, a, p, st), expected, (name, "saved"))
+        union = O.attention(qn, kn, vn, [np.concatenate((pn[h], an[h][~hit[h]]))
+                                         for h in range(len(pn))])
+        check(gqa.repair_union(q, k, v, a, p, st), union, (name, "union"))
+        check(gqa_light.repair_saved_light(q, k, v, a, p, st), expected, (name, "light"))
+        for emf in (0., 1.):
+            check(gqa_light.repair_saved_auto(q, k, v, a, p, st, emf), expected, (name, "auto", emf))
+    with pytest.raises(ValueError):
+        gqa_light.repair_saved_auto(q, k, v, a, p, st, 1.5)
+
+
+def test_gqa_validation_messages():
+    from strict_topk import gqa
+    q = torch.randn((6, 13), device=DEV, dtype=torch.float16)
+    k = torch.randn((4, 23, 7, 13), device=DEV, dtype=torch.float16)
+    ids = torch.zeros((6, 3), device=DEV, dtype=torch.int32)
+    with pytest.raises(ValueError, match="Hq divisible"):
+        gqa.partials(q, k, k, ids)
+    with pytest.raises(ValueError, match="nonempty int32/int64"):
+        gqa.partials(q, k[:2], k[:2], ids.float())
+
+
+# ------------------------------------------------------------ hierarchical
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_hierarchical_paths(dtype):
+    from strict_topk import gqa_hierarchical as impl
+    for (h, hkv, n, b, d, sa), *ts in C.hier_cases(dtype):
+        qn, kn, vn, an = np_(*ts)
+        expected = O.attention(qn, kn, vn, an)
+        q, k, v, a = dev(*ts)
+        check(impl.exact(q, k, v, a), expected, "exact")
+        for hits in [0, sa // 2, sa - 1, sa]:
+            p = C.prediction_rows(a.cpu(), n, sa, hits).to(DEV)
+            st = impl.partials(q, k, v, p)
+            check(impl.repair_saved(q, k, v, a, p, st), expected, ("saved", hits))
+        shared = a[:1].expand(h, -1).contiguous()
+        exp_shared = O.attention(qn, kn, vn, C.ids_np(shared))
+        for hits in (0, sa // 2, sa):
+            pred = C.prediction_rows(shared.cpu(), n, max(1, sa // 2), min(hits, sa // 2)).to(DEV)
+            out = impl.repair_saved_shared(q, k, v, shared, pred, impl.partials(q, k, v, pred))
+            check(out, exp_shared, ("shared", hits))
+
+
+# ----------------------------------------------------------- graph replays
+def _capture(fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    g.replay()
+    torch.cuda.synchronize()
+    return g, out
+
+
+def test_graph_mutation_signed_fused():
+    """tests/check_signed_fused.py:31-49: capture, scale V in place, replay."""
+    from strict_topk.kernels import speculate
+    from strict_topk.signed_fused import repair_signed_fused
+    gen = torch.Generator().manual_seed(817)
+    for dtype in (torch.float16, torch.bfloat16):
+        q = torch.randn((3, 7), generator=gen).to(dtype)
+        k = torch.randn((3, 17, 5, 7), generator=gen).to(dtype)
+        v = torch.randn(k.shape, generator=gen).to(dtype)
+        p = torch.tensor([[0, 1, 2, 3, 4], [3, 4, 5, 6, 7], [8, 9, 10, 11, 12]], dtype=torch.int64)
+        a = torch.tensor([[1, 2, 8], [4, 9, 15], [0, 5, 16]], dtype=torch.int32)
+        q, k, v, p, a = dev(q, k, v, p, a)
+        for mode in ("saved", "hybrid", "compact"):
+            g, res = _capture(lambda: repair_signed_fused(
+                q, k, v, a, p, speculate(q, k, v, p, mode=mode, mass_threshold=.2)))
+            for scale in (1., -.5, 2.):
+                v.mul_(scale)
+                g.replay()
+                torch.cuda.synchronize()
+                check(res.output, O.attention(*np_(q, k, v, a)), (dtype, mode, scale))
+
+
+def test_graph_mutation_hierarchical_ids():
+    """tests/check_gqa_hierarchical.py:28-32: captured IDs change in place."""
+    from strict_topk import gqa_hierarchical as impl
+    gen = torch.Generator().manual_seed(5)
+    h, hkv, n, b, d, sa = 6, 2, 96, 5, 96, 37
+    q = torch.randn((h, d), generator=gen).bfloat16()
+    k = torch.randn((hkv, n, b, d), generator=gen).bfloat16()
+    v = torch.randn(k.shape, generator=gen).bfloat16()
+    a = torch.stack([torch.randperm(n, generator=gen)[:sa] for _ in range(h)]).int()
+    p = C.prediction_rows(a, n, sa, sa // 2)
+    q, k, v, a, p = dev(q, k, v, a, p)
+    g, out = _capture(lambda: impl.repair_saved(q, k, v, a, p, impl.partials(q, k, v, p)))
+    a.copy_((a + 1) % n)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        check(out, O.attention(*np_(q, k, v, a)), "hier graph")
+
+
+def test_touch_kv_checksums():
+    from strict_topk.kernels import touch_kv
+    gen = torch.Generator().manual_seed(4)
+    k = torch.randn((2, 9, 40, 64), generator=gen).half()
+    v = torch.randn(k.shape, generator=gen).half()
+    p = torch.tensor([[0, 3, 8], [1, 2, 7]], dtype=torch.int32)
+    ref = O.touch_kv(*np_(k, v, p))
+    got = touch_kv(*dev(k, v, p))
+    assert got.shape == ref.shape
+    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-4, atol=1e-3)
