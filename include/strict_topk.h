@@ -1,0 +1,203 @@
+/*
+ * strict_topk.h -- C ABI of libstrict_topk_hip.so, the gfx950 HIP kernels of
+ * the speculative block-sparse Top-K decode path.
+ *
+ * Each entry point replaces one host function of the reference's Python
+ * package (6Mikao9/strict-topk-overlap, files under strict_topk/); the
+ * citation above each declaration names it.  The reference binds no C ABI:
+ * its host functions launch Triton kernels.  The binding that takes the
+ * place of those launches is strict_topk/_lib.py (ctypes) in this repository.
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device addresses; every buffer is contiguous, row-major.
+ *     q[Hq,D]; k,v[Hkv,N,B,D] (Hq % Hkv == 0, query head h reads KV head
+ *     h / (Hq/Hkv)); lo,hi[Hkv,N,D] float32; ID rows [Hq,S]; states
+ *     m,l[Hq,S] and u[Hq,S,D] float32; outputs float32.
+ *   - dtype codes: STK_F32, STK_F16, STK_BF16 (elements of q, k, v);
+ *     ID codes: STK_I32, STK_I64.  Boolean arrays are one byte per entry
+ *     (torch.bool layout).
+ *   - `stream` is a hipStream_t.  Every call only enqueues work on it: no
+ *     allocation, no host synchronisation, no copy to the host, so calls can
+ *     be captured into a HIP graph and issued on concurrent streams.
+ *   - Scratch memory beyond inputs and outputs is the caller's `workspace`
+ *     of at least the size the matching *_workspace_bytes() returns.
+ *   - ID values are not validated on the device; an ID outside [0, N)
+ *     contributes an empty state (-inf, 0, 0) and never reads memory.
+ *   - Return value: STK_OK, STK_EINVAL (bad argument; nothing launched) or
+ *     STK_EHIP (launch error).  stk_last_error() gives the calling thread's
+ *     last message.
+ */
+#ifndef STRICT_TOPK_H
+#define STRICT_TOPK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { STK_OK = 0, STK_EINVAL = -1, STK_EHIP = -2 };
+enum { STK_F32 = 0, STK_F16 = 1, STK_BF16 = 2 };
+enum { STK_I32 = 0, STK_I64 = 1 };
+enum { STK_SAVED = 0, STK_HYBRID = 1, STK_COMPACT = 2 };
+
+const char* stk_last_error(void);
+int stk_abi_version(void);
+
+/* ---------------------------------------------------------- selection */
+
+/* strict_topk/selector.py:23-38 block_scores (and gqa.py:15-26 scoring):
+ * scores[h,n] = sum_d q_d * (q_d >= 0 ? hi : lo)[h/G, n, d], evaluated in
+ * float64 in a fixed order, stored as float32. */
+int stk_block_scores(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
+                     int hkv, int n, int d, float* scores, void* stream);
+
+size_t stk_select_workspace_bytes(int hq, int hkv, int n, int d, int topk);
+
+/* strict_topk/selector.py:41-43 select_blocks and gqa.py:145-161
+ * select_blocks (score + torch.topk(sorted=False)): ids[h, 0..topk) are the
+ * topk highest-scoring blocks, ties toward the lower block index, in
+ * (score desc, index asc) order.  `scores` may be NULL. */
+int stk_select_blocks(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
+                      int hkv, int n, int d, int topk, float* scores, int32_t* ids,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------- states and merge */
+
+/* strict_topk/kernels.py:425-434 block_partials and gqa.py:128-137 partials:
+ * per (query head, slot) m = max logit, l = sum exp(logit - m),
+ * u = sum exp(logit - m) V, logits = q.k / sqrt(D).  `active` (may be NULL)
+ * is [Hq] (active_kind 1) or [Hq,S] (active_kind 2); inactive slots get
+ * (-inf, 0, 0). */
+int stk_block_partials(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                       int n, int b, int d, const void* ids, int id_dtype, int s,
+                       const uint8_t* active, int active_kind, float* m, float* l, float* u,
+                       void* stream);
+
+/* strict_topk/kernels.py:437-442 merge_partials: LSE merge of S states per
+ * head, optional include mask [H,S], out = sum e^(m-M) u / max(z, 1e-30). */
+int stk_merge_partials(const float* m, const float* l, const float* u, const uint8_t* include,
+                       int h, int s, int d, float* out, void* stream);
+
+size_t stk_exact_workspace_bytes(int hq, int s, int d);
+
+/* strict_topk/kernels.py:445-447 exact_attention and gqa.py:140-142 exact. */
+int stk_exact_attention(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                        int n, int b, int d, const void* ids, int id_dtype, int s, float* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* strict_topk/kernels.py:450-501 speculate (saved / hybrid / compact).
+ * saved: m,l,u[Hq,s].  hybrid: also high[Hq,s], low_m/low_l[Hq], low_u and
+ * low_abs[Hq,D].  compact (capacity C from kernels.py:485): m,l,u[Hq,C],
+ * retained_ids[Hq,C] (pred_dtype, rank order, -1 padded), overflow[Hq],
+ * mass_m/mass_l[Hq,s] required.  Unused outputs may be NULL. */
+int stk_speculate(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
+                  int b, int d, const void* pred, int pred_dtype, int s, int mode, float tau,
+                  int capacity, float* m, float* l, float* u, uint8_t* high, float* low_m,
+                  float* low_l, float* low_u, float* low_abs, void* retained_ids,
+                  uint8_t* overflow, float* mass_m, float* mass_l, void* stream);
+
+/* strict_topk/kernels.py:553-560 touch_kv: per (head, slot, 1024-element
+ * tile) sum of K + V of the predicted block, out[H,S,ceil(B*D/1024)]. */
+int stk_touch_kv(const void* k, const void* v, int dtype, int h, int n, int b, int d,
+                 const void* pred, int pred_dtype, int s, float* out, void* stream);
+
+/* ------------------------------------------------------------- repairs */
+
+/* strict_topk/kernels.py:223-247 _fallback (as launched by kernels.py:548
+ * and signed_repair.py:231): strict online softmax over the selected set on
+ * heads whose flag is set. */
+int stk_fallback(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
+                 int b, int d, const void* selected, int sel_dtype, int sa, const uint8_t* flags,
+                 float* out, void* stream);
+
+size_t stk_repair_workspace_bytes(int hq, int sa, int sp, int sc, int d, int mode);
+
+/* strict_topk/kernels.py:504-550 repair (split path: membership, miss
+ * states, saved or hybrid merge with guards, fallback).  (pm,pl,pu) is the
+ * prediction state of width sc; high/low_* are required for hybrid and
+ * compact, retained_ids for compact. */
+int stk_repair(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
+               int b, int d, const void* selected, int sel_dtype, int sa, const void* predicted,
+               int pred_dtype, int sp, int mode, int sc, const float* pm, const float* pl,
+               const float* pu, const uint8_t* high, const float* low_m, const float* low_l,
+               const float* low_u, const float* low_abs, const void* retained_ids,
+               float min_remaining, float cancellation_tol, float* out, uint8_t* fallback,
+               float* remaining, void* workspace, size_t workspace_bytes, void* stream);
+
+/* strict_topk/fused.py:176-220 repair_fused: the whole repair in one
+ * workgroup per head, with the extra-mass budget max_extra_mass
+ * (approximate/extra_mass_bound [Hq] required when it is > 0). */
+int stk_repair_fused(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                     int n, int b, int d, const void* selected, int sel_dtype, int sa,
+                     const void* predicted, int pred_dtype, int sp, int mode, int sc,
+                     const float* pm, const float* pl, const float* pu, const uint8_t* high,
+                     const float* low_m, const float* low_l, const float* low_u,
+                     const float* low_abs, const void* retained_ids, const float* mass_m,
+                     const float* mass_l, float min_remaining, float cancellation_tol,
+                     float max_extra_mass, float* out, uint8_t* fallback, float* remaining,
+                     uint8_t* approximate, float* extra_mass_bound, void* stream);
+
+size_t stk_gqa_repair_workspace_bytes(int hq, int sa, int d);
+
+/* strict_topk/gqa.py:164-193 repair_saved (union_mode 0) and repair_union
+ * (union_mode 1) for native GQA. */
+int stk_gqa_repair(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
+                   int b, int d, const void* selected, int sel_dtype, int sa,
+                   const void* predicted, int pred_dtype, int sp, const float* pm,
+                   const float* pl, const float* pu, int union_mode, float* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* strict_topk/gqa_light.py:63-77 repair_saved_light: hits merged from the
+ * saved states, misses streamed with the online softmax, one launch. */
+int stk_repair_light(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                     int n, int b, int d, const void* selected, int sel_dtype, int sa,
+                     const void* predicted, int pred_dtype, int sp, const float* pm,
+                     const float* pl, const float* pu, float* out, void* stream);
+
+size_t stk_signed_workspace_bytes(int hq, int sa, int sp, int sc, int d, int mode);
+
+/* strict_topk/signed_repair.py:175-232 repair_signed (fused 0: schedule,
+ * signed partials, guarded merge, separate fallback) and
+ * strict_topk/signed_fused.py:148-193 repair_signed_fused (fused 1:
+ * schedule, signed corrections, finalize with inline fallback).  queue is
+ * [Hq, sa + sp] (hybrid/compact) or [Hq, sa] (saved) of queue_dtype;
+ * positive_jobs/total_jobs are [Hq] int32. */
+int stk_repair_signed(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                      int n, int b, int d, const void* selected, int sel_dtype, int sa,
+                      const void* predicted, int pred_dtype, int sp, int mode, int sc,
+                      const float* pm, const float* pl, const float* pu, const uint8_t* high,
+                      const float* low_m, const float* low_l, const float* low_u,
+                      const float* low_abs, const void* retained_ids, const float* mass_m,
+                      const float* mass_l, float min_remaining, float cancellation_tol,
+                      float max_extra_mass, int fused, void* queue, int queue_dtype,
+                      int32_t* positive_jobs, int32_t* total_jobs, float* out, uint8_t* fallback,
+                      float* remaining, uint8_t* approximate, float* extra_mass_bound,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------- hierarchical */
+
+size_t stk_hier_exact_workspace_bytes(int hq, int s, int d);
+
+/* strict_topk/gqa_hierarchical.py:111-112 exact: per-block states, level-1
+ * merge of 32 positions, final LSE merge. */
+int stk_hier_exact(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
+                   int b, int d, const void* selected, int sel_dtype, int sa, float* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+size_t stk_hier_repair_workspace_bytes(int hq, int sa, int d, int shared);
+
+/* strict_topk/gqa_hierarchical.py:115-144 repair_saved (shared 0) and
+ * repair_saved_shared (shared 1: row 0's slot table serves every head). */
+int stk_hier_repair(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                    int n, int b, int d, const void* selected, int sel_dtype, int sa,
+                    const void* predicted, int pred_dtype, int sp, const float* pm,
+                    const float* pl, const float* pu, int shared, float* out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRICT_TOPK_H */

@@ -5,9 +5,10 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define STK_API __attribute__((visibility("default")))
+// The public declarations: every exported definition must match them.
+#include "../../include/strict_topk.h"
 
-enum { STK_OK = 0, STK_EINVAL = -1, STK_EHIP = -2 };
+#define STK_API __attribute__((visibility("default")))
 
 void stk_set_error(const char* fmt, ...);
 int stk_check_launch(const char* what);
@@ -63,6 +64,3 @@ int stk_launch_states_skip(const void* q, const void* k, const void* v, int dtyp
 int stk_launch_merge(const float* m, const float* l, const float* u, const uint8_t* inc, int h,
                      int s, int d, float* out, hipStream_t st);
 
-extern "C" int stk_fallback(const void* q, const void* k, const void* v, int dtype, int hq,
-                            int hkv, int n, int b, int d, const void* selected, int sel_dtype,
-                            int sa, const uint8_t* flags, float* out, void* stream);

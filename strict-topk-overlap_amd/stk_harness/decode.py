@@ -1,0 +1,144 @@
+"""Decode-step closures and algorithmic byte counts for the benchmark configs.
+
+Counterpart of the reference's synthetic decode cases
+(``benchmarks/critical_path.py:65-167,170-236``): the full speculative step
+``overlap_run(select, speculate, repair)`` and the same-work serial step
+``exact(select())`` (``benchmarks/critical_path.py:110``).
+
+Byte model (HBM-bound path; every figure counts bytes that must cross HBM
+once per decode step, from the actual IDs of the run):
+  tile      = 2 * B * D * e            K and V of one (KV head, block), e = element bytes
+  U_x       = unique (KV head, block) pairs read by pass x
+  kv_bytes  = (U_spec + U_miss) * tile              (saved repair reads no wrong blocks)
+  meta      = 2 * Hkv * N * D * 4                   lo and hi, read once
+  states    = Hq * SP * (D + 2) * 4                 speculative state write
+            + Hq * hits * (D + 2) * 4               state read of the hits
+  small     = Q + output + ID rows
+The serial step reads meta + U_A * tile + small.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from strict_topk import gqa, gqa_light
+
+from .configs import CONFIGS, make_qkv, perturb
+from .timing import overlap_run
+
+HBM_PEAK = 8.0e12   # MI355X HBM3E bytes/s
+
+
+def unique_pairs(ids, group):
+    """Number of unique (KV head, block) pairs over rows of ``ids`` [Hq, S]."""
+    ids = np.asarray(ids, dtype=np.int64)
+    hq = ids.shape[0]
+    total = 0
+    for kv in range(hq // group):
+        total += len(np.unique(ids[kv * group:(kv + 1) * group]))
+    return total
+
+
+def misses(selected, predicted):
+    """Per-row selected IDs absent from the predicted row (list of arrays)."""
+    out = []
+    for a, p in zip(np.asarray(selected), np.asarray(predicted)):
+        out.append(np.setdiff1d(a, p, assume_unique=True))
+    return out
+
+
+@dataclass
+class Bytes:
+    kv_spec: int
+    kv_miss: int
+    meta: int
+    states: int
+    small: int
+    serial_kv: int
+    kv_select_only: int = 0
+
+    @property
+    def full(self):
+        return self.kv_spec + self.kv_miss + self.meta + self.states + self.small
+
+    @property
+    def kv_full(self):
+        return self.kv_spec + self.kv_miss
+
+    @property
+    def serial(self):
+        return self.meta + self.serial_kv + self.small
+
+
+def byte_model(cfg, selected, predicted, elem_bytes):
+    g = cfg.hq // cfg.hkv
+    tile = 2 * cfg.block * cfg.dim * elem_bytes
+    sel = np.asarray(selected, dtype=np.int64)
+    pred = np.asarray(predicted, dtype=np.int64)
+    miss_rows = misses(sel, pred)
+    hits = sum(sel.shape[1] - len(m) for m in miss_rows)
+    # unique (kv, block) miss pairs per KV group
+    u_miss = 0
+    for kv in range(cfg.hkv):
+        rows = miss_rows[kv * g:(kv + 1) * g]
+        u_miss += len(np.unique(np.concatenate(rows))) if rows else 0
+    st = 4 * (cfg.dim + 2)
+    small = cfg.hq * cfg.dim * elem_bytes + cfg.hq * cfg.dim * 4 + 4 * (sel.size + pred.size)
+    return Bytes(
+        kv_spec=unique_pairs(pred, g) * tile,
+        kv_miss=u_miss * tile,
+        meta=2 * cfg.hkv * cfg.blocks * cfg.dim * 4,
+        states=cfg.hq * pred.shape[1] * st + hits * st,
+        small=small,
+        serial_kv=unique_pairs(sel, g) * tile,
+    )
+
+
+class GqaStep:
+    """c2 / c3: gqa.select_blocks || gqa.partials -> saved repair."""
+
+    def __init__(self, cfg, overlap, seed, device, repair="auto"):
+        self.cfg, self.overlap, self.seed = cfg, overlap, seed
+        q, k, v, lo, hi = make_qkv(cfg.hq, cfg.hkv, cfg.dim, cfg.block, cfg.blocks, cfg.dtype,
+                                   cfg.hot, seed)
+        self.host = (q, k, v, lo, hi)
+        self.q, self.k, self.v, self.lo, self.hi = (t.to(device) for t in (q, k, v, lo, hi))
+        self.selected = gqa.select_blocks(self.q, self.lo, self.hi, cfg.topk)
+        self.predicted = perturb(self.selected.cpu(), cfg.blocks, cfg.sp, overlap, seed).to(device)
+        self.emf = 1.0 - overlap
+        self.repair = repair
+        self.ss = torch.cuda.Stream()
+        self.ps = torch.cuda.Stream()
+        torch.cuda.synchronize()
+
+    # -- phases
+    def select(self):
+        return gqa.select_blocks(self.q, self.lo, self.hi, self.cfg.topk)
+
+    def speculate(self):
+        return gqa.partials(self.q, self.k, self.v, self.predicted)
+
+    def finish(self, a, state):
+        if self.repair == "light":
+            return gqa_light.repair_saved_light(self.q, self.k, self.v, a, self.predicted, state)
+        if self.repair == "saved":
+            return gqa.repair_saved(self.q, self.k, self.v, a, self.predicted, state)
+        return gqa_light.repair_saved_auto(self.q, self.k, self.v, a, self.predicted, state,
+                                           self.emf)
+
+    # -- whole steps
+    def full(self):
+        return overlap_run(self.select, self.speculate, self.finish, self.ss, self.ps)
+
+    def serial(self):
+        return gqa.exact(self.q, self.k, self.v, self.select())
+
+    def bytes(self):
+        e = torch.tensor([], dtype=self.cfg.dtype).element_size()
+        return byte_model(self.cfg, self.selected.cpu().numpy(), self.predicted.cpu().numpy(), e)
+
+
+def gqa_step(name="c3", overlap=0.9, seed=20261103, device="cuda", repair="auto"):
+    return GqaStep(CONFIGS[name], overlap, seed, device, repair)
