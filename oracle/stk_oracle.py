@@ -21,7 +21,7 @@ Selection contract (this build's, stricter than the reference's
     summation order (``SCORE_LANES`` interleaved lane sums, then an xor
     butterfly), so the GPU scorer and this oracle produce identical bits;
   * ``topk_ids`` returns the K entries with the highest score, ties broken
-    toward the lower block index, emitted in (score desc, index asc) order;
+    toward the lower block index, emitted in ascending block index order;
     NaN ranks below -inf.
 
 Pinning: ``tests/test_oracle.py`` checks each function against the
@@ -155,7 +155,7 @@ def bound_scores_plain(q, lo, hi):
 
 
 def topk_ids(scores, k):
-    """Top-k block IDs per row: score desc, ties toward the lower index.
+    """Top-k block IDs per row, ties toward the lower index, ascending IDs.
 
     Restates the reference's ``scores.topk(k, sorted=False)``
     (strict_topk/gqa.py:161, selector.py:43) with the lower-index tie rule of
@@ -172,7 +172,7 @@ def topk_ids(scores, k):
         nan = np.isnan(s)
         primary = np.where(nan, np.inf, -s)
         order = np.lexsort((idx, nan, primary))
-        out[r] = order[:k]
+        out[r] = np.sort(order[:k])
     return out
 
 

@@ -14,9 +14,41 @@
 
 namespace stk {
 
+// VEC consecutive elements of type T held as raw 32-bit words; loaded with
+// one 2/4/8/16-byte access and converted to FP32 on use.
 template <typename T, int VEC>
-struct alignas((VEC * sizeof(T)) >= 16 ? 16 : (VEC * sizeof(T))) Raw {
-  T v[VEC];
+struct Raw {
+  static constexpr int BYTES = VEC * (int)sizeof(T);
+  static constexpr int W = BYTES >= 4 ? BYTES / 4 : 1;
+  uint32_t w[W];
+
+  __device__ __forceinline__ void load(const T* p) {
+    if constexpr (BYTES == 16) {
+      uint4 x = *reinterpret_cast<const uint4*>(p);
+      w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+    } else if constexpr (BYTES == 8) {
+      uint2 x = *reinterpret_cast<const uint2*>(p);
+      w[0] = x.x; w[1] = x.y;
+    } else if constexpr (BYTES == 4) {
+      w[0] = *reinterpret_cast<const uint32_t*>(p);
+    } else {
+      w[0] = *reinterpret_cast<const uint16_t*>(p);
+    }
+  }
+  __device__ __forceinline__ void zero_unless(bool keep) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = keep ? w[i] : 0u;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (sizeof(T) == 4) {
+      return __uint_as_float(w[i]);
+    } else {
+      uint32_t bits = (w[i / 2] >> (16 * (i % 2))) & 0xffffu;
+      T x;
+      __builtin_memcpy(&x, &bits, 2);
+      return cvt(x);
+    }
+  }
 };
 
 template <typename T, int VEC, int NC>
@@ -39,81 +71,101 @@ struct Tile {
 
   __device__ __forceinline__ bool chunk_ok(int c) const { return (part + c * lpt) * VEC < D; }
 
-  // q row (any element type) -> per-lane FP32 registers (0 outside D)
-  template <typename Q>
-  __device__ __forceinline__ void load_q(const Q* q, float* qr) const {
+  // q row -> per-lane FP32 registers (0 outside D).  Every access is issued
+  // unconditionally from a clamped address so that no branch separates the
+  // loads (a branch makes the compiler wait for each load in turn).
+  __device__ __forceinline__ void load_q(const T* q, float* qr) const {
+    Raw<T, VEC> r[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) r[c].load(q + (chunk_ok(c) ? (part + c * lpt) * VEC : 0));
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      int base = (part + c * lpt) * VEC;
+      bool ok = chunk_ok(c);
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) qr[c * VEC + i] = (base + i < D) ? cvt(q[base + i]) : 0.f;
+      for (int i = 0; i < VEC; ++i) qr[c * VEC + i] = ok ? r[c].get(i) : 0.f;
     }
   }
 
+  // One token row: chunks beyond D, and rows with !valid, read a valid
+  // address and are zeroed.
   __device__ __forceinline__ void load_row(const T* row, Raw<T, VEC>* dst, bool valid) const {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      if (valid && chunk_ok(c)) {
-        dst[c] = *reinterpret_cast<const Raw<T, VEC>*>(row + (part + c * lpt) * VEC);
-      } else {
+      bool ok = valid && chunk_ok(c);
+      dst[c].load(row + (ok ? (part + c * lpt) * VEC : 0));
+      dst[c].zero_unless(ok);
+    }
+  }
+
+  // Raw K (and V) rows of one chunk of U * tpw tokens starting at t0.
+  template <int U, bool WITH_V>
+  __device__ __forceinline__ void load_chunk(const T* kb, const T* vb, int t0, int B,
+                                             Raw<T, VEC> (&kr)[U][NC],
+                                             Raw<T, VEC> (&vr)[U][NC]) const {
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) dst[c].v[i] = T{};
+    for (int u = 0; u < U; ++u) {
+      int t = t0 + u * tpw + tok;
+      bool valid = t < B;
+      load_row(kb + (size_t)(valid ? t : 0) * D, kr[u], valid);
+      if constexpr (WITH_V) load_row(vb + (size_t)(valid ? t : 0) * D, vr[u], valid);
+    }
+  }
+
+  // Online-softmax update of (m, l, acc) with one loaded chunk.  FIXED keeps
+  // m as the exponent frame (weights exp(s - m), no rescaling).
+  template <int U, bool FIXED, bool WITH_V>
+  __device__ __forceinline__ void update_chunk(const float* qr, const Raw<T, VEC> (&kr)[U][NC],
+                                               const Raw<T, VEC> (&vr)[U][NC], int t0, int B,
+                                               float scale, float& m, float& l,
+                                               float* acc) const {
+    float s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float dot = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) dot += kr[u][c].get(i) * qr[c * VEC + i];
+      for (int off = 1; off < lpt; off <<= 1) dot += __shfl_xor(dot, off);
+      int t = t0 + u * tpw + tok;
+      s[u] = (t < B) ? dot * scale : -INFINITY;
+    }
+    if constexpr (!FIXED) {
+      float tile = s[0];
+#pragma unroll
+      for (int u = 1; u < U; ++u) tile = fmaxf(tile, s[u]);
+      for (int off = lpt; off < STK_WAVE; off <<= 1) tile = fmaxf(tile, __shfl_xor(tile, off));
+      float nm = fmaxf(m, tile);
+      if (nm > m) {
+        float alpha = (m == -INFINITY) ? 0.f : expf(m - nm);
+        l *= alpha;
+#pragma unroll
+        for (int i = 0; i < R; ++i) acc[i] *= alpha;
+        m = nm;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float w = (s[u] == -INFINITY) ? 0.f : expf(s[u] - m);
+      l += w;
+      if constexpr (WITH_V) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[c * VEC + i] += w * vr[u][c].get(i);
       }
     }
   }
 
-  // Accumulate one block into (m, l, acc).  FIXED keeps m as the exponent
-  // frame (weights exp(s - m), no rescaling).  WITH_V=false skips V.
+  // Accumulate one block into (m, l, acc).  WITH_V=false skips V.
   template <int U, bool FIXED, bool WITH_V>
   __device__ __forceinline__ void accum(const float* qr, const T* kb, const T* vb, int B,
                                         float scale, float& m, float& l, float* acc) const {
     for (int t0 = 0; t0 < B; t0 += U * tpw) {
       Raw<T, VEC> kr[U][NC];
       Raw<T, VEC> vr[U][NC];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        int t = t0 + u * tpw + tok;
-        bool valid = t < B;
-        load_row(kb + (size_t)(valid ? t : 0) * D, kr[u], valid);
-        if constexpr (WITH_V) load_row(vb + (size_t)(valid ? t : 0) * D, vr[u], valid);
-      }
-      float s[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float dot = 0.f;
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) dot += cvt(kr[u][c].v[i]) * qr[c * VEC + i];
-        for (int off = 1; off < lpt; off <<= 1) dot += __shfl_xor(dot, off);
-        int t = t0 + u * tpw + tok;
-        s[u] = (t < B) ? dot * scale : -INFINITY;
-      }
-      if constexpr (!FIXED) {
-        float tile = s[0];
-#pragma unroll
-        for (int u = 1; u < U; ++u) tile = fmaxf(tile, s[u]);
-        for (int off = lpt; off < STK_WAVE; off <<= 1) tile = fmaxf(tile, __shfl_xor(tile, off));
-        float nm = fmaxf(m, tile);
-        if (nm > m) {
-          float alpha = (m == -INFINITY) ? 0.f : expf(m - nm);
-          l *= alpha;
-#pragma unroll
-          for (int i = 0; i < R; ++i) acc[i] *= alpha;
-          m = nm;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float w = (s[u] == -INFINITY) ? 0.f : expf(s[u] - m);
-        l += w;
-        if constexpr (WITH_V) {
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) acc[c * VEC + i] += w * cvt(vr[u][c].v[i]);
-        }
-      }
+      load_chunk<U, WITH_V>(kb, vb, t0, B, kr, vr);
+      update_chunk<U, FIXED, WITH_V>(qr, kr, vr, t0, B, scale, m, l, acc);
     }
   }
 
@@ -138,7 +190,7 @@ struct Tile {
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) dot += cvt(kr[u][c].v[i]) * qr[c * VEC + i];
+          for (int i = 0; i < VEC; ++i) dot += kr[u][c].get(i) * qr[c * VEC + i];
         for (int off = 1; off < lpt; off <<= 1) dot += __shfl_xor(dot, off);
         int t = t0 + u * tpw + tok;
         float w = (t < B) ? expf(dot * scale - m) : 0.f;
@@ -147,7 +199,7 @@ struct Tile {
         for (int c = 0; c < NC; ++c)
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
-            float x = w * cvt(vr[u][c].v[i]);
+            float x = w * vr[u][c].get(i);
             acc[c * VEC + i] += x;
             abs_acc[c * VEC + i] += fabsf(x);
           }

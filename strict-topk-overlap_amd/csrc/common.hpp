@@ -80,6 +80,20 @@ __device__ __forceinline__ void store_id(void* ids, int itype, int64_t i, int64_
   else reinterpret_cast<int32_t*>(ids)[i] = (int32_t)v;
 }
 
+// Branch-free guarded load: the access is always issued (from index 0 when
+// !ok, which callers guarantee to be valid), and the value replaced after.
+// Keeping loads out of branches lets the compiler keep them all in flight.
+template <typename X>
+__device__ __forceinline__ X ld_or(const X* p, int64_t i, bool ok, X other) {
+  X v = p[ok ? i : 0];
+  return ok ? v : other;
+}
+
+template <typename I>
+__device__ __forceinline__ int64_t ld_id(const void* ids, int64_t i) {
+  return (int64_t) reinterpret_cast<const I*>(ids)[i];
+}
+
 // ---------------------------------------------------------------- wave ops
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (STK_WAVE - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / STK_WAVE; }
@@ -148,6 +162,45 @@ __device__ __forceinline__ int block_count(int v, int* red) {
 // when b is -inf.
 __device__ __forceinline__ float wexp(float a, float b) {
   return a == -INFINITY ? 0.f : expf(a - b);
+}
+
+// --------------------------------------------------------------- scans
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int off = 1; off < STK_WAVE; off <<= 1) {
+    T x = __shfl_up(v, off);
+    if (lane >= off) v += x;
+  }
+  return v;
+}
+
+// Exclusive prefix sum over the whole workgroup in thread order; `tmp`
+// holds one int per wave.  Returns the exclusive prefix; *total the sum.
+__device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total) {
+  int inc = wave_incl_scan(v);
+  const int nw = blockDim.x / STK_WAVE;
+  if (lane_id() == STK_WAVE - 1) tmp[wave_id()] = inc;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < nw; ++w) {
+    int x = tmp[w];
+    before += w < wave_id() ? x : 0;
+    all += x;
+  }
+  __syncthreads();
+  *total = all;
+  return before + inc - v;
+}
+
+__device__ __forceinline__ uint64_t wave_or64(uint64_t v) {
+  for (int off = 1; off < STK_WAVE; off <<= 1) v |= __shfl_xor(v, off);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_and64(uint64_t v) {
+  for (int off = 1; off < STK_WAVE; off <<= 1) v &= __shfl_xor(v, off);
+  return v;
 }
 
 __device__ __forceinline__ bool is_bad(float x) { return !(fabsf(x) <= 3.402823466e38f); }

@@ -1,32 +1,38 @@
 // Min/max query-sign bound scorer plus exact top-K selection.
 //
-// Reference: strict_topk/selector.py:8-20,30-50 (_score, block_scores,
-// select_blocks) and strict_topk/gqa.py:15-26,365-381 (_bound_score,
+// Reference: strict_topk/selector.py:8-20,23-43 (_score, block_scores,
+// select_blocks) and strict_topk/gqa.py:15-26,145-161 (_bound_score,
 // select_blocks), which end in torch.topk(sorted=False).
 //
-// Contract: score[h,n] = sum_d q_d * (q_d >= 0 ? hi : lo)[h/G, n, d] in FP64.
-// Products are exact; 16 lanes share a block, lane c summing dims
-// 64*j + 4*c + t (j ascending, t = 0..3) from +0.0, then lanes combine with an
-// xor butterfly (8, 4, 2, 1).  The top K are the K largest (score, -index)
-// pairs, i.e. ties go to the lower block index; IDs are written in
-// (score desc, index asc) order.
+// Score contract: score[h,n] = sum_d q_d * (q_d >= 0 ? hi : lo)[h/G, n, d]
+// in FP64.  Products of a 16/32-bit q and an FP32 bound are exact in FP64;
+// 16 lanes share a block, lane c summing dims 64*j + 4*c + t (j ascending,
+// t = 0..3) from +0.0, then the lanes combine with an xor butterfly
+// (8, 4, 2, 1).  Selection contract: the K largest (score, -index) pairs,
+// so ties go to the lower block index; IDs are written in ascending block
+// order.  NaN scores rank below -inf.
 //
-// Launch structure (MI355X): k_score_sort spreads the HBM-bound metadata
-// stream over (KV head x head subgroup x chunk) workgroups; every workgroup
-// scores CH blocks for GS query heads sharing one KV head (lo/hi read once
-// per subgroup), bitonic-sorts each head's chunk in LDS and keeps its best KP.
-// k_topk_merge then merges the per-chunk sorted lists of a row with a tree of
-// bitonic half-cleaners.
-#include "common.hpp"
+// Launch structure (MI355X):
+//   k_score  -- HBM-bound scan of lo/hi.  One workgroup = 4 waves covers
+//               16 * STEPS consecutive blocks of one KV head for all G query
+//               heads of that head (lo/hi read once per KV head); every lane
+//               issues all its 16-byte loads before any arithmetic.  Writes
+//               an order-preserving 64-bit key per (query head, block).
+//   k_topk   -- one 1024-thread workgroup per query head: MSB-first radix
+//               select over the row's keys held in registers (8-bit digits
+//               from the highest bit where the row's keys differ, stopping
+//               as soon as the threshold digit's bin is taken whole), then a
+//               block-wide scan writes the selected IDs in index order.
+#include "attn.hpp"
 #include "api.hpp"
 
 namespace stk {
 
-constexpr int kSortElems = 4096;   // GS * CHP per scoring workgroup
-constexpr int kMergeElems = 8192;  // elements resident in the merge workgroup
-constexpr int kMaxGS = 16;
-constexpr int kQElems = 4096;      // GS * D query values staged in LDS
+constexpr int kTopkThreads = 256;
+constexpr int kScoreWaves = 4;
 
+// Order-preserving map of a double to an unsigned key; NaN -> 0 (lowest),
+// -0.0 -> +0.0.
 __device__ __forceinline__ uint64_t score_key(double s) {
   if (s != s) return 0ull;
   if (s == 0.0) s = 0.0;
@@ -34,22 +40,13 @@ __device__ __forceinline__ uint64_t score_key(double s) {
   return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
 }
 
-__device__ __forceinline__ bool better(uint64_t ka, uint32_t ia, uint64_t kb, uint32_t ib) {
-  return ka > kb || (ka == kb && ia < ib);
-}
-
 struct ScoreArgs {
   const void* q; int qtype;
   const float* lo; const float* hi;
   int hq, hkv, n, d;
-  int gs;        // heads per workgroup
-  int ch;        // blocks per chunk
-  int chp;       // next pow2 of ch
-  int kp;        // list length kept per chunk (pow2)
-  int nchunks;
-  float* scores;     // optional FP32 [hq, n]
-  uint64_t* wkey;    // optional [hq, nchunks, kp]
-  uint32_t* widx;
+  int chunks;            // workgroups per KV head
+  float* scores;         // optional FP32 [hq, n]
+  uint64_t* keys;        // optional [hq, n]
 };
 
 template <typename Q>
@@ -57,229 +54,321 @@ __device__ __forceinline__ float qval(const void* q, int64_t i) {
   return cvt(reinterpret_cast<const Q*>(q)[i]);
 }
 
-template <typename Q, bool SORT>
-__global__ __launch_bounds__(256) void k_score_sort(ScoreArgs a) {
-  __shared__ float qs[kQElems];   // per-head query rows (FP32 copies)
-  __shared__ uint64_t skey[kSortElems];
-  __shared__ uint32_t sidx[kSortElems];
+// P = 64-dim passes (D <= 64 * P), STEPS = 4-block wave steps per wave,
+// GT = query heads whose rows are held in registers at a time.
+template <typename Q, int P, int STEPS, bool VEC4, int GT>
+__global__ __launch_bounds__(256) void k_score(ScoreArgs a) {
   const int G = a.hq / a.hkv;
-  const int hg = (G + a.gs - 1) / a.gs;
-  const int kv = blockIdx.x / hg;
-  const int g0 = (blockIdx.x % hg) * a.gs;
-  const int gs = min(a.gs, G - g0);
-  const int h0 = kv * G + g0;
-  const int chunk = blockIdx.y;
-  const int n0 = chunk * a.ch;
-  const int nend = min(a.n, n0 + a.ch);
-  for (int i = threadIdx.x; i < gs * a.d; i += blockDim.x)
-    qs[i] = qval<Q>(a.q, (int64_t)h0 * a.d + i);
-  if (SORT)
-    for (int i = threadIdx.x; i < gs * a.chp; i += blockDim.x) {
-      skey[i] = 0ull;
-      sidx[i] = 0xffffffffu;
-    }
-  __syncthreads();
-  const int lane16 = threadIdx.x & 15;
-  const int slot = threadIdx.x >> 4;          // 16 blocks per pass of 256 threads
-  const int passes = (a.d + 63) / 64;
-  const bool vec4 = (a.d & 3) == 0;
-  const int iters = (a.ch + 15) / 16;
-  for (int it = 0; it < iters; ++it) {
-    // every lane of a 16-group takes part in the butterfly, valid or not
-    int nb = n0 + it * 16 + slot;
-    bool valid = nb < nend && it * 16 + slot < a.ch;
-    double acc[kMaxGS];
+  const int kv = blockIdx.x / a.chunks;
+  const int chunk = blockIdx.x % a.chunks;
+  const int h0 = kv * G;
+  const int lane = lane_id();
+  const int lane16 = lane & 15;
+  const int sub = lane >> 4;                  // block within a 4-block step
+  const int wave_base = (chunk * kScoreWaves + wave_id()) * (4 * STEPS);
+  const Q* qrow = reinterpret_cast<const Q*>(a.q) + (size_t)h0 * a.d;
+  // every load of the wave is issued before any arithmetic, with no branch
+  // around a load: out-of-range blocks, dims and heads read a valid address
+  // and are zeroed
+  float4 lv[STEPS][P], hv[STEPS][P];
 #pragma unroll
-    for (int g = 0; g < kMaxGS; ++g) acc[g] = 0.0;
-    if (valid) {
-      const float* lrow = a.lo + ((size_t)kv * a.n + nb) * a.d;
-      const float* hrow = a.hi + ((size_t)kv * a.n + nb) * a.d;
-      for (int j = 0; j < passes; ++j) {
+  for (int s = 0; s < STEPS; ++s) {
+    int nb = wave_base + 4 * s + sub;
+    bool valid = nb < a.n;
+    const float* lrow = a.lo + ((size_t)kv * a.n + (valid ? nb : 0)) * a.d;
+    const float* hrow = a.hi + ((size_t)kv * a.n + (valid ? nb : 0)) * a.d;
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      int d0 = 64 * j + 4 * lane16;
+      if constexpr (VEC4) {
+        bool ok = valid && d0 < a.d;
+        float4 l4 = *reinterpret_cast<const float4*>(lrow + (ok ? d0 : 0));
+        float4 h4 = *reinterpret_cast<const float4*>(hrow + (ok ? d0 : 0));
+        lv[s][j] = ok ? l4 : make_float4(0.f, 0.f, 0.f, 0.f);
+        hv[s][j] = ok ? h4 : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        float l4[4], h4[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          bool ok = valid && d0 + t < a.d;
+          l4[t] = ld_or(lrow, (int64_t)(d0 + t), ok, 0.f);
+          h4[t] = ld_or(hrow, (int64_t)(d0 + t), ok, 0.f);
+        }
+        lv[s][j] = make_float4(l4[0], l4[1], l4[2], l4[3]);
+        hv[s][j] = make_float4(h4[0], h4[1], h4[2], h4[3]);
+      }
+    }
+  }
+  for (int gb = 0; gb < G; gb += GT) {
+    // query values of heads gb .. gb+GT-1 at this lane's dims, as doubles
+    double qd[GT][P][4];
+#pragma unroll
+    for (int gi = 0; gi < GT; ++gi) {
+      const bool hv_ok = gb + gi < G;
+      const Q* qg = qrow + (size_t)(hv_ok ? gb + gi : 0) * a.d;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
         int d0 = 64 * j + 4 * lane16;
-        float lv[4], hv[4];
-        if (vec4 && d0 + 3 < a.d) {
-          float4 l4 = *reinterpret_cast<const float4*>(lrow + d0);
-          float4 h4 = *reinterpret_cast<const float4*>(hrow + d0);
-          lv[0] = l4.x; lv[1] = l4.y; lv[2] = l4.z; lv[3] = l4.w;
-          hv[0] = h4.x; hv[1] = h4.y; hv[2] = h4.z; hv[3] = h4.w;
+        if constexpr (VEC4) {
+          // four consecutive elements in one 8- or 16-byte access
+          bool ok = hv_ok && d0 < a.d;
+          Raw<Q, 4> r;
+          r.load(qg + (ok ? d0 : 0));
+#pragma unroll
+          for (int t = 0; t < 4; ++t) qd[gi][j][t] = ok ? (double)r.get(t) : 0.0;
         } else {
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            lv[t] = d0 + t < a.d ? lrow[d0 + t] : 0.f;
-            hv[t] = d0 + t < a.d ? hrow[d0 + t] : 0.f;
+            bool ok = hv_ok && d0 + t < a.d;
+            float qv = cvt(qg[ok ? d0 + t : 0]);
+            qd[gi][j][t] = ok ? (double)qv : 0.0;
           }
         }
+      }
+    }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          int dd = d0 + t;
-          if (dd < a.d) {
+    for (int s = 0; s < STEPS; ++s) {
+      const int nb = wave_base + 4 * s + sub;
 #pragma unroll
-            for (int g = 0; g < kMaxGS; ++g) {
-              if (g < gs) {
-                float qv = qs[g * a.d + dd];
-                double b = qv >= 0.f ? (double)hv[t] : (double)lv[t];
-                acc[g] = acc[g] + (double)qv * b;   // exact product, one rounding
-              }
-            }
+      for (int gi = 0; gi < GT; ++gi) {
+        double acc = 0.0;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+          const float lvv[4] = {lv[s][j].x, lv[s][j].y, lv[s][j].z, lv[s][j].w};
+          const float hvv[4] = {hv[s][j].x, hv[s][j].y, hv[s][j].z, hv[s][j].w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            // a zero q (out of range) adds +0.0, which leaves the sum unchanged
+            double b = qd[gi][j][t] >= 0.0 ? (double)hvv[t] : (double)lvv[t];
+            acc = fma(qd[gi][j][t], b, acc);   // exact product, one rounding
           }
         }
-      }
-    }
-    for (int g = 0; g < gs; ++g) {
-      double v = acc[g];
-      v = v + __shfl_xor(v, 8);
-      v = v + __shfl_xor(v, 4);
-      v = v + __shfl_xor(v, 2);
-      v = v + __shfl_xor(v, 1);
-      if (valid && lane16 == 0) {
-        if (v == 0.0) v = 0.0;
-        int h = h0 + g;
-        if (a.scores) a.scores[(size_t)h * a.n + nb] = (float)v;
-        if (SORT) {
-          skey[g * a.chp + (nb - n0)] = score_key(v);
-          sidx[g * a.chp + (nb - n0)] = (uint32_t)nb;
+        acc = acc + __shfl_xor(acc, 8);
+        acc = acc + __shfl_xor(acc, 4);
+        acc = acc + __shfl_xor(acc, 2);
+        acc = acc + __shfl_xor(acc, 1);
+        if (lane16 == 0 && nb < a.n && gb + gi < G) {
+          if (acc == 0.0) acc = 0.0;
+          size_t o = (size_t)(h0 + gb + gi) * a.n + nb;
+          if (a.scores) a.scores[o] = (float)acc;
+          if (a.keys) a.keys[o] = score_key(acc);
         }
       }
-    }
-  }
-  if (!SORT) return;
-  __syncthreads();
-  // bitonic sort of each head's chp entries, descending by (key, -idx)
-  const int total = gs * a.chp;
-  for (int k = 2; k <= a.chp; k <<= 1) {
-    for (int jj = k >> 1; jj > 0; jj >>= 1) {
-      for (int i = threadIdx.x; i < total; i += blockDim.x) {
-        int li = i & (a.chp - 1);
-        int p = li ^ jj;
-        if (p > li) {
-          int base = i - li;
-          uint64_t k1 = skey[base + li], k2 = skey[base + p];
-          uint32_t i1 = sidx[base + li], i2 = sidx[base + p];
-          bool desc = (li & k) == 0;
-          bool swap = desc ? better(k2, i2, k1, i1) : better(k1, i1, k2, i2);
-          if (swap) {
-            skey[base + li] = k2; skey[base + p] = k1;
-            sidx[base + li] = i2; sidx[base + p] = i1;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-  for (int i = threadIdx.x; i < gs * a.kp; i += blockDim.x) {
-    int g = i / a.kp, r = i % a.kp;
-    size_t o = ((size_t)(h0 + g) * a.nchunks + chunk) * a.kp + r;
-    if (r < a.chp) {
-      a.wkey[o] = skey[g * a.chp + r];
-      a.widx[o] = sidx[g * a.chp + r];
-    } else {
-      a.wkey[o] = 0ull;
-      a.widx[o] = 0xffffffffu;
     }
   }
 }
 
-struct MergeTopArgs {
-  const uint64_t* wkey; const uint32_t* widx;
-  int nchunks, kp, k;
+struct TopkArgs {
+  const uint64_t* keys;
+  int n, k;
   int32_t* ids;
 };
 
-// Sorted-list tree merge per row.  LDS holds `cap` lists of kp entries; the
-// running best list stays in list 0 between batches.
-__global__ __launch_bounds__(1024) void k_topk_merge(MergeTopArgs a) {
-  __shared__ uint64_t key[kMergeElems];
-  __shared__ uint32_t idx[kMergeElems];
-  const int h = blockIdx.x;
-  const int kp = a.kp;
-  const int cap = kMergeElems / kp;      // lists resident (pow2, >= 2)
-  const uint64_t* rk = a.wkey + (size_t)h * a.nchunks * kp;
-  const uint32_t* ri = a.widx + (size_t)h * a.nchunks * kp;
-  int next = 0;
-  bool have = false;
-  while (next < a.nchunks || !have) {
-    int first = have ? 1 : 0;
-    int take = min(cap - first, a.nchunks - next);
-    int lists = first + take;
-    int lp = 1;
-    while (lp < lists) lp <<= 1;
-    for (int i = threadIdx.x; i < (lp - first) * kp; i += blockDim.x) {
-      int li = first + i / kp, r = i % kp;
-      int src = next + (li - first);
-      if (li < lists) {
-        key[li * kp + r] = rk[(size_t)src * kp + r];
-        idx[li * kp + r] = ri[(size_t)src * kp + r];
-      } else {
-        key[li * kp + r] = 0ull;
-        idx[li * kp + r] = 0xffffffffu;
-      }
+// Thread t owns indices [t*KPT, t*KPT + KPT) so that an exclusive scan in
+// thread order is a scan in index order.  N <= 256 * KPT.
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void k_topk(TopkArgs a) {
+  __shared__ int hist[256];
+  __shared__ int tmp[kTopkThreads / STK_WAVE];
+  __shared__ uint64_t red64[2][kTopkThreads / STK_WAVE];
+  __shared__ int pick[2];
+  const int row = blockIdx.x;
+  const uint64_t* rk = a.keys + (size_t)row * a.n;
+  const int base = threadIdx.x * KPT;
+  uint64_t key[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) key[i] = ld_or(rk, (int64_t)(base + i), base + i < a.n, (uint64_t)0);
+  // bits shared by every key of the row
+  uint64_t vor = 0ull, vand = ~0ull;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i)
+    if (base + i < a.n) {
+      vor |= key[i];
+      vand &= key[i];
     }
-    next += take;
-    have = true;
-    __syncthreads();
-    for (int stride = 1; stride < lp; stride <<= 1) {
-      int pairs = lp / (2 * stride);
-      // half-cleaner: a[i] vs b[kp-1-i]
-      for (int i = threadIdx.x; i < pairs * kp; i += blockDim.x) {
-        int p = i / kp, r = i % kp;
-        int la = (2 * p) * stride, lb = la + stride;
-        int ia = la * kp + r, ib = lb * kp + (kp - 1 - r);
-        if (better(key[ib], idx[ib], key[ia], idx[ia])) {
-          key[ia] = key[ib];
-          idx[ia] = idx[ib];
+  vor = wave_or64(vor);
+  vand = wave_and64(vand);
+  if (lane_id() == 0) {
+    red64[0][wave_id()] = vor;
+    red64[1][wave_id()] = vand;
+  }
+  __syncthreads();
+  vor = 0ull;
+  vand = ~0ull;
+  for (int w = 0; w < kTopkThreads / STK_WAVE; ++w) {
+    vor |= red64[0][w];
+    vand &= red64[1][w];
+  }
+  const uint64_t diff = vor ^ vand;
+  uint64_t mask = ~0ull, prefix = vand;   // when every key is equal
+  int need = a.k;
+  if (diff != 0ull) {
+    int start = 63 - __clzll((long long)diff);
+    mask = start == 63 ? 0ull : ~0ull << (start + 1);
+    prefix = vand & mask;
+    while (true) {
+      const int shift = start >= 7 ? start - 7 : 0;
+      const int width = start - shift + 1;
+      const uint64_t dmask = ((1ull << width) - 1ull);
+      for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < KPT; ++i)
+        if (base + i < a.n && (key[i] & mask) == prefix)
+          atomicAdd(&hist[(key[i] >> shift) & dmask], 1);
+      __syncthreads();
+      if (wave_id() == 0) {
+        // lane l owns bins 255-4l .. 252-4l (descending digit order)
+        int c[4], s = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          c[t] = hist[255 - 4 * lane_id() - t];
+          s += c[t];
+        }
+        int inc = wave_incl_scan(s);
+        int above = inc - s;        // keys in higher bins than this lane's
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (above < need && above + c[t] >= need) {
+            pick[0] = 255 - 4 * lane_id() - t;
+            pick[1] = above;
+          }
+          above += c[t];
         }
       }
       __syncthreads();
-      // bitonic merge of each surviving list into descending order
-      for (int jj = kp >> 1; jj > 0; jj >>= 1) {
-        for (int i = threadIdx.x; i < pairs * kp; i += blockDim.x) {
-          int p = i / kp, r = i % kp;
-          int q = r ^ jj;
-          if (q > r) {
-            int base = (2 * p) * stride * kp;
-            uint64_t k1 = key[base + r], k2 = key[base + q];
-            uint32_t i1 = idx[base + r], i2 = idx[base + q];
-            if (better(k2, i2, k1, i1)) {
-              key[base + r] = k2; key[base + q] = k1;
-              idx[base + r] = i2; idx[base + q] = i1;
-            }
-          }
-        }
-        __syncthreads();
-      }
+      const int bin = pick[0];
+      const int above = pick[1];
+      const int cnt = hist[bin];
+      need -= above;
+      prefix |= (uint64_t)bin << shift;
+      mask |= dmask << shift;
+      __syncthreads();
+      if (cnt == need || shift == 0) break;
+      start = shift - 1;
     }
-    if (next >= a.nchunks) break;
   }
-  for (int i = threadIdx.x; i < a.k; i += blockDim.x) a.ids[(size_t)h * a.k + i] = (int32_t)idx[i];
+  // selected: (key & mask) > prefix, plus the `need` lowest-index keys with
+  // (key & mask) == prefix
+  int eq = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) eq += base + i < a.n && (key[i] & mask) == prefix;
+  int total;
+  int eq_before = block_excl_scan(eq, tmp, &total);
+  bool sel[KPT];
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    bool valid = base + i < a.n;
+    uint64_t km = key[i] & mask;
+    bool e = valid && km == prefix;
+    sel[i] = valid && (km > prefix || (e && eq_before < need));
+    eq_before += e;
+    cnt += sel[i];
+  }
+  int pos = block_excl_scan(cnt, tmp, &total);
+  int32_t* out = a.ids + (size_t)row * a.k;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i)
+    if (sel[i]) out[pos++] = base + i;
 }
 
-static int pow2ceil(int x) {
-  int p = 1;
-  while (p < x) p <<= 1;
-  return p;
-}
-
-struct SelectPlan {
-  int gs, ch, chp, kp, nchunks, hg;
-};
-
-static SelectPlan plan_select(int hq, int hkv, int n, int d, int topk) {
-  SelectPlan p{};
-  int G = hq / hkv;
-  p.kp = pow2ceil(topk < 1 ? 1 : topk);
-  p.ch = p.kp > 64 ? p.kp : 64;
-  if (p.ch > n) p.ch = n;
-  p.chp = pow2ceil(p.ch);
-  if (p.chp < p.kp) p.chp = p.kp;   // keeps the sort length >= kept length
-  int gs = kSortElems / p.chp;
-  if (gs > kMaxGS) gs = kMaxGS;
-  if (gs > kQElems / d) gs = kQElems / d;
-  if (gs > G) gs = G;
-  if (gs < 1) gs = 1;
-  p.gs = gs;
-  p.hg = (G + gs - 1) / gs;
-  p.nchunks = (n + p.ch - 1) / p.ch;
-  return p;
+// Rows longer than 8192 keys: the same selection with keys re-read from
+// global memory in every pass (thread t owns a contiguous index range).
+__global__ __launch_bounds__(kTopkThreads) void k_topk_long(TopkArgs a) {
+  __shared__ int hist[256];
+  __shared__ int tmp[kTopkThreads / STK_WAVE];
+  __shared__ uint64_t red64[2][kTopkThreads / STK_WAVE];
+  __shared__ int pick[2];
+  const int row = blockIdx.x;
+  const uint64_t* rk = a.keys + (size_t)row * a.n;
+  const int per = (a.n + kTopkThreads - 1) / kTopkThreads;
+  const int b0 = threadIdx.x * per;
+  const int b1 = min(a.n, b0 + per);
+  uint64_t vor = 0ull, vand = ~0ull;
+  for (int i = b0; i < b1; ++i) {
+    vor |= rk[i];
+    vand &= rk[i];
+  }
+  vor = wave_or64(vor);
+  vand = wave_and64(vand);
+  if (lane_id() == 0) {
+    red64[0][wave_id()] = vor;
+    red64[1][wave_id()] = vand;
+  }
+  __syncthreads();
+  vor = 0ull;
+  vand = ~0ull;
+  for (int w = 0; w < kTopkThreads / STK_WAVE; ++w) {
+    vor |= red64[0][w];
+    vand &= red64[1][w];
+  }
+  const uint64_t diff = vor ^ vand;
+  uint64_t mask = ~0ull, prefix = vand;
+  int need = a.k;
+  if (diff != 0ull) {
+    int start = 63 - __clzll((long long)diff);
+    mask = start == 63 ? 0ull : ~0ull << (start + 1);
+    prefix = vand & mask;
+    while (true) {
+      const int shift = start >= 7 ? start - 7 : 0;
+      const int width = start - shift + 1;
+      const uint64_t dmask = ((1ull << width) - 1ull);
+      for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
+      __syncthreads();
+      for (int i = b0; i < b1; ++i) {
+        uint64_t kk = rk[i];
+        if ((kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & dmask], 1);
+      }
+      __syncthreads();
+      if (wave_id() == 0) {
+        int c[4], s = 0;
+        for (int t = 0; t < 4; ++t) {
+          c[t] = hist[255 - 4 * lane_id() - t];
+          s += c[t];
+        }
+        int inc = wave_incl_scan(s);
+        int above = inc - s;
+        for (int t = 0; t < 4; ++t) {
+          if (above < need && above + c[t] >= need) {
+            pick[0] = 255 - 4 * lane_id() - t;
+            pick[1] = above;
+          }
+          above += c[t];
+        }
+      }
+      __syncthreads();
+      const int bin = pick[0];
+      const int above = pick[1];
+      const int cnt = hist[bin];
+      need -= above;
+      prefix |= (uint64_t)bin << shift;
+      mask |= dmask << shift;
+      __syncthreads();
+      if (cnt == need || shift == 0) break;
+      start = shift - 1;
+    }
+  }
+  int eq = 0;
+  for (int i = b0; i < b1; ++i) eq += (rk[i] & mask) == prefix;
+  int total;
+  int eq_before = block_excl_scan(eq, tmp, &total);
+  int cnt = 0;
+  for (int i = b0; i < b1; ++i) {
+    uint64_t km = rk[i] & mask;
+    bool e = km == prefix;
+    cnt += km > prefix || (e && eq_before < need);
+    eq_before += e;
+  }
+  eq_before = block_excl_scan(eq, tmp, &total);
+  int pos = block_excl_scan(cnt, tmp, &total);
+  int32_t* out = a.ids + (size_t)row * a.k;
+  for (int i = b0; i < b1; ++i) {
+    uint64_t km = rk[i] & mask;
+    bool e = km == prefix;
+    if (km > prefix || (e && eq_before < need)) out[pos++] = i;
+    eq_before += e;
+  }
 }
 
 }  // namespace stk
@@ -294,14 +383,63 @@ static StkCheck check_select(int q_dtype, int hq, int hkv, int n, int d) {
   return {true, ""};
 }
 
-template <bool SORT>
-static void launch_score(ScoreArgs& a, int qtype, dim3 grid, hipStream_t st) {
-  if (qtype == DT_BF16)
-    hipLaunchKernelGGL((k_score_sort<bf16s, SORT>), grid, dim3(256), 0, st, a);
-  else if (qtype == DT_F16)
-    hipLaunchKernelGGL((k_score_sort<f16s, SORT>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((k_score_sort<float, SORT>), grid, dim3(256), 0, st, a);
+// Launch the scorer: blocks per workgroup = 4 waves * 4 blocks * STEPS.
+template <typename Q>
+static void launch_score_q(ScoreArgs& a, hipStream_t st) {
+  const int passes = (a.d + 63) / 64;
+  const bool vec4 = a.d % 4 == 0 && (reinterpret_cast<uintptr_t>(a.lo) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.hi) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.q) & (4 * sizeof(Q) - 1)) == 0;
+#define STK_SCORE(PP, SS, GG)                                                                  \
+  do {                                                                                         \
+    a.chunks = (a.n + kScoreWaves * 4 * SS - 1) / (kScoreWaves * 4 * SS);                       \
+    if (vec4)                                                                                  \
+      hipLaunchKernelGGL((k_score<Q, PP, SS, true, GG>), dim3(a.hkv * a.chunks), dim3(256), 0, st, a); \
+    else                                                                                       \
+      hipLaunchKernelGGL((k_score<Q, PP, SS, false, GG>), dim3(a.hkv * a.chunks), dim3(256), 0, st, a); \
+  } while (0)
+  const int G = a.hq / a.hkv;
+  if (passes <= 1) {
+    if (G <= 1) STK_SCORE(1, 2, 1);
+    else if (G <= 2) STK_SCORE(1, 2, 2);
+    else STK_SCORE(1, 2, 4);
+  } else if (passes <= 2) {
+    if (G <= 1) STK_SCORE(2, 2, 1);
+    else if (G <= 2) STK_SCORE(2, 2, 2);
+    else STK_SCORE(2, 2, 4);
+  } else if (passes <= 4) {
+    STK_SCORE(4, 1, 2);
+  } else if (passes <= 8) {
+    STK_SCORE(8, 1, 1);
+  } else {
+    STK_SCORE(16, 1, 1);
+  }
+#undef STK_SCORE
+}
+
+int stk_launch_score(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
+                     int hkv, int n, int d, float* scores, uint64_t* keys, hipStream_t st) {
+  ScoreArgs a{};
+  a.q = q; a.qtype = q_dtype; a.lo = lo; a.hi = hi;
+  a.hq = hq; a.hkv = hkv; a.n = n; a.d = d;
+  a.scores = scores; a.keys = keys;
+  if (q_dtype == DT_BF16) launch_score_q<bf16s>(a, st);
+  else if (q_dtype == DT_F16) launch_score_q<f16s>(a, st);
+  else launch_score_q<float>(a, st);
+  return stk_check_launch("k_score");
+}
+
+int stk_launch_topk(const uint64_t* keys, int rows, int n, int k, int32_t* ids, hipStream_t st) {
+  TopkArgs t{keys, n, k, ids};
+  const dim3 grid(rows), block(kTopkThreads);
+  if (n <= 256) hipLaunchKernelGGL(k_topk<1>, grid, block, 0, st, t);
+  else if (n <= 512) hipLaunchKernelGGL(k_topk<2>, grid, block, 0, st, t);
+  else if (n <= 1024) hipLaunchKernelGGL(k_topk<4>, grid, block, 0, st, t);
+  else if (n <= 2048) hipLaunchKernelGGL(k_topk<8>, grid, block, 0, st, t);
+  else if (n <= 4096) hipLaunchKernelGGL(k_topk<16>, grid, block, 0, st, t);
+  else if (n <= 8192) hipLaunchKernelGGL(k_topk<32>, grid, block, 0, st, t);
+  else hipLaunchKernelGGL(k_topk_long, grid, block, 0, st, t);
+  return stk_check_launch("k_topk");
 }
 
 extern "C" {
@@ -310,27 +448,13 @@ STK_API int stk_block_scores(const void* q, int q_dtype, const float* lo, const 
                              int hkv, int n, int d, float* scores, void* stream) {
   STK_REQUIRE(check_select(q_dtype, hq, hkv, n, d));
   STK_REQUIRE(q && lo && hi && scores, "null pointer");
-  SelectPlan p = plan_select(hq, hkv, n, d, 1);
-  int G = hq / hkv;
-  ScoreArgs a{};
-  a.q = q; a.qtype = q_dtype; a.lo = lo; a.hi = hi;
-  a.hq = hq; a.hkv = hkv; a.n = n; a.d = d;
-  a.gs = G < kMaxGS ? G : kMaxGS;
-  if (a.gs > kQElems / d) a.gs = kQElems / d;
-  a.ch = 64; a.chp = 64; a.kp = 1;
-  a.nchunks = (n + 63) / 64;
-  a.scores = scores;
-  int hg = (G + a.gs - 1) / a.gs;
-  (void)p;
-  launch_score<false>(a, q_dtype, dim3(hkv * hg, a.nchunks), (hipStream_t)stream);
-  return stk_check_launch("k_score_sort");
+  return stk_launch_score(q, q_dtype, lo, hi, hq, hkv, n, d, scores, nullptr,
+                          (hipStream_t)stream);
 }
 
 STK_API size_t stk_select_workspace_bytes(int hq, int hkv, int n, int d, int topk) {
   if (hq <= 0 || hkv <= 0 || n <= 0 || d <= 0 || topk <= 0) return 0;
-  SelectPlan p = plan_select(hq, hkv, n, d, topk);
-  size_t elems = (size_t)hq * p.nchunks * p.kp;
-  return stk_align(elems * 8) + stk_align(elems * 4);
+  return stk_align((size_t)hq * n * sizeof(uint64_t));
 }
 
 STK_API int stk_select_blocks(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
@@ -339,26 +463,13 @@ STK_API int stk_select_blocks(const void* q, int q_dtype, const float* lo, const
   STK_REQUIRE(check_select(q_dtype, hq, hkv, n, d));
   STK_REQUIRE(q && lo && hi && ids, "null pointer");
   STK_REQUIRE(topk >= 1 && topk <= n, "selected index k out of range");
-  STK_REQUIRE(pow2ceil(topk) <= kMergeElems / 2, "topk above 4096 is not supported");
   STK_REQUIRE(workspace && workspace_bytes >= stk_select_workspace_bytes(hq, hkv, n, d, topk),
               "workspace too small");
-  SelectPlan p = plan_select(hq, hkv, n, d, topk);
-  Carve w(workspace);
-  size_t elems = (size_t)hq * p.nchunks * p.kp;
-  ScoreArgs a{};
-  a.q = q; a.qtype = q_dtype; a.lo = lo; a.hi = hi;
-  a.hq = hq; a.hkv = hkv; a.n = n; a.d = d;
-  a.gs = p.gs; a.ch = p.ch; a.chp = p.chp; a.kp = p.kp; a.nchunks = p.nchunks;
-  a.scores = scores;
-  a.wkey = w.take<uint64_t>(elems);
-  a.widx = w.take<uint32_t>(elems);
   hipStream_t st = (hipStream_t)stream;
-  launch_score<true>(a, q_dtype, dim3(hkv * p.hg, p.nchunks), st);
-  int rc = stk_check_launch("k_score_sort");
+  uint64_t* keys = static_cast<uint64_t*>(workspace);
+  int rc = stk_launch_score(q, q_dtype, lo, hi, hq, hkv, n, d, scores, keys, st);
   if (rc) return rc;
-  MergeTopArgs m{a.wkey, a.widx, p.nchunks, p.kp, topk, ids};
-  hipLaunchKernelGGL(k_topk_merge, dim3(hq), dim3(1024), 0, st, m);
-  return stk_check_launch("k_topk_merge");
+  return stk_launch_topk(keys, hq, n, topk, ids, st);
 }
 
 }  // extern "C"

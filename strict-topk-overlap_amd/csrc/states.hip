@@ -8,7 +8,7 @@
 //   strict_topk/kernels.py:94-117  _group        -> k_hybrid_group
 //   strict_topk/kernels.py:263-356 _mass_only / _compact_group / _compact_values
 //   strict_topk/kernels.py:250-260 _touch        -> k_touch
-#include "attn.hpp"
+#include "tile2.hpp"
 #include "api.hpp"
 
 namespace stk {
@@ -89,55 +89,380 @@ __global__ __launch_bounds__(256) void k_states(StatesArgs a) {
   if (WITH_V) t.store(a.u + row * a.d, acc);
 }
 
-// LSE merge of S states per head (kernels.py:74-91).  256 threads arranged as
-// RG row groups x DT dim threads.
+constexpr int kGrpHT = 4;   // heads sharing one loaded tile
+
+// Token-tile states (shapes the token tile supports): one wave per
+// (query head, slot).  GROUP: the wave owning block b (no lower head of its
+// KV group lists b) computes the state of every head of the group whose row
+// holds b, reading the K/V tile once; non-owners return.  Otherwise each wave
+// computes its own slot, honouring the optional active mask (inactive slots
+// get (-inf, 0, 0), kernels.py:42-71).
+template <typename T, int NCH, int UP, typename I, bool GROUP>
+__global__ __launch_bounds__(256) void k_states_tok(StatesArgs a) {
+  using TT = TokTile<T, NCH, UP>;
+  constexpr int HT = GROUP ? kGrpHT : 1;
+  const int waves = blockDim.x / STK_WAVE;
+  int wg = a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
+  int64_t item = (int64_t)wg * waves + wave_id();
+  if (item >= (int64_t)a.hq * a.s) return;
+  const I* ids = reinterpret_cast<const I*>(a.ids);
+  const int h = (int)(item / a.s);
+  const int j = (int)(item - (int64_t)h * a.s);
+  const int G = a.hq / a.hkv;
+  const int hl = h % G;
+  const int g0 = h - hl;
+  int64_t bid;
+  uint64_t found = 1ull << hl;
+  uint64_t pmask[HT];
+#pragma unroll
+  for (int i = 0; i < HT; ++i) pmask[i] = 0ull;
+  if constexpr (GROUP) {
+    // rows of the group that list b; G*S <= 256 IDs, 4 per lane, one pass
+    const int total = G * a.s;
+    const I* grp = ids + (int64_t)g0 * a.s;
+    int64_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int x = i * STK_WAVE + lane_id();
+      v[i] = ld_or(grp, (int64_t)x, x < total, (I)-1);
+    }
+    const int xb = hl * a.s + j;
+    const int ib = xb / STK_WAVE, lb = xb % STK_WAVE;
+    int64_t pick = v[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) pick = ib == i ? v[i] : pick;
+    bid = __shfl(pick, lb);
+    found = 0ull;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int x = i * STK_WAVE + lane_id();
+      if (x < total && v[i] == bid) found |= 1ull << (x / a.s);
+    }
+    for (int off = 1; off < STK_WAVE; off <<= 1) found |= __shfl_xor(found, off);
+    if (found & ((1ull << hl) - 1ull)) return;   // a lower head owns this block
+    found &= ~((1ull << hl) - 1ull);
+  } else {
+    bid = ids[item];
+  }
+  bool enabled = bid >= 0 && bid < a.n;
+  if (!GROUP) {
+    if (a.active_kind == 1) enabled = enabled && a.active[h] != 0;
+    else if (a.active_kind == 2) enabled = enabled && a.active[item] != 0;
+  }
+  const int kv = h / G;
+  TT t;
+  t.init();
+  const float scale = 1.0f / sqrtf((float)a.d);
+  const size_t off = (((size_t)kv * a.n + (enabled ? (size_t)bid : 0)) * a.b) * a.d;
+  const T* kb = reinterpret_cast<const T*>(a.k) + off;
+  const T* vb = reinterpret_cast<const T*>(a.v) + off;
+  while (found) {
+    int heads[HT];
+    int nh = 0;
+#pragma unroll
+    for (int i = 0; i < HT; ++i) {
+      heads[i] = hl;
+      if (found) {
+        int gg = __ffsll((long long)found) - 1;
+        found &= found - 1;
+        heads[i] = gg;
+        nh = i + 1;
+      }
+    }
+    uint32_t qw[HT][TT::QW];
+    float m[HT], l[HT], acc[HT][TT::DPL];
+#pragma unroll
+    for (int i = 0; i < HT; ++i) {
+      m[i] = -INFINITY;
+      l[i] = 0.f;
+#pragma unroll
+      for (int e = 0; e < TT::DPL; ++e) acc[i][e] = 0.f;
+      t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)(g0 + heads[i]) * a.d, qw[i]);
+      if constexpr (GROUP) {
+        // rows of at most 64 IDs: positions of b, read with the query
+        bool in = lane_id() < a.s;
+        int64_t x = ld_or(ids, (int64_t)(g0 + heads[i]) * a.s + lane_id(), in, (I)-1);
+        pmask[i] = __ballot(in && x == bid);
+      }
+    }
+    if (enabled) {
+      for (int t0 = 0; t0 < a.b; t0 += TT::CH) {
+        uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
+        t.load(kb, vb, t0, a.b, kw, vw);
+#pragma unroll
+        for (int i = 0; i < HT; ++i)
+          if (i < nh)
+            t.template update<false, false>(qw[i], kw, vw, t0, a.b, scale, m[i], l[i], acc[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < HT; ++i) {
+      if (i >= nh) continue;
+      const int gg = heads[i];
+      if (gg == hl) {
+        if (lane_id() == 0) {
+          a.m[item] = m[i];
+          a.l[item] = l[i];
+        }
+        t.store(a.u + item * a.d, acc[i]);
+        continue;
+      }
+      const int64_t rbase = (int64_t)(g0 + gg) * a.s;
+      for (int p0 = 0; p0 < a.s; p0 += STK_WAVE) {
+        int p = p0 + lane_id();
+        uint64_t hits = pmask[i];
+        if (p0 > 0) {
+          int64_t x = ld_or(ids, rbase + p, p < a.s, (I)-1);
+          hits = __ballot(p < a.s && x == bid);
+        }
+        while (hits) {
+          int bit = __ffsll((long long)hits) - 1;
+          hits &= hits - 1;
+          int64_t row = rbase + p0 + bit;
+          if (lane_id() == 0) {
+            a.m[row] = m[i];
+            a.l[row] = l[i];
+          }
+          t.store(a.u + row * a.d, acc[i]);
+        }
+      }
+    }
+  }
+}
+
+// LSE merge arguments (kernels.py:74-91, merge_partials :437-442).
 struct MergeArgs {
   const float* m; const float* l; const float* u; const uint8_t* inc;
   int h, s, d;
   float* out;
 };
 
-__global__ __launch_bounds__(256) void k_merge(MergeArgs a) {
-  __shared__ float red[32];
-  __shared__ float part[256 * 4];
-  int h = blockIdx.x;
-  const float* m = a.m + (size_t)h * a.s;
-  const float* l = a.l + (size_t)h * a.s;
-  float mx = -INFINITY;
-  for (int j = threadIdx.x; j < a.s; j += blockDim.x) {
-    bool on = !a.inc || a.inc[(size_t)h * a.s + j];
-    if (on) mx = fmaxf(mx, m[j]);
-  }
-  mx = block_max(mx, red);
-  if (mx == -INFINITY) mx = 0.f;
-  int dt = 1;
-  while (dt < a.d && dt < 256) dt <<= 1;
-  int rg = 256 / dt;
-  int tr = threadIdx.x / dt, td = threadIdx.x % dt;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  float z = 0.f;
-  for (int j = tr; j < a.s; j += rg) {
-    bool on = !a.inc || a.inc[(size_t)h * a.s + j];
-    if (!on) continue;
-    float w = wexp(m[j], mx);
-    if (td == 0) z += w * l[j];
-    const float* ur = a.u + ((size_t)h * a.s + j) * a.d;
-    for (int c = 0; c < 4; ++c) {
-      int dd = td + c * dt;
-      if (dd < a.d) acc[c] += w * ur[dd];
+// GQA states with one read of every (KV head, block) tile.  Wave (h, j)
+// owns block b = ids[h, j] when no lower query head of its KV group lists b;
+// the owner loads the K/V tile once and computes the state of every head of
+// the group whose row holds b (writing each such slot), the other waves
+// return.  Heads are processed in batches of HT sharing the loaded chunk.
+
+template <typename T, int VEC, int NC, int U, typename I>
+__global__ __launch_bounds__(256) void k_states_grp(StatesArgs a) {
+  using TL = Tile<T, VEC, NC>;
+  const int waves = blockDim.x / STK_WAVE;
+  int wg = a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
+  int64_t item = (int64_t)wg * waves + wave_id();
+  if (item >= (int64_t)a.hq * a.s) return;
+  const I* ids = reinterpret_cast<const I*>(a.ids);
+  const int h = (int)(item / a.s);
+  const int G = a.hq / a.hkv;
+  const int hl = h % G;
+  const int g0 = h - hl;
+  const int j = (int)(item - (int64_t)h * a.s);
+  // rows of the group that list b (wave-uniform bit mask, G <= 64); the
+  // group's G*S IDs are read 4 per lane at a time, all loads in flight.
+  // When G*S <= 256 the wave's own ID comes out of the same registers.
+  uint64_t found = 0ull;
+  const int total = G * a.s;
+  const I* grp = ids + (int64_t)g0 * a.s;
+  int64_t bid;
+  if (total <= 4 * STK_WAVE) {
+    int64_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int x = i * STK_WAVE + lane_id();
+      v[i] = ld_or(grp, (int64_t)x, x < total, (I)-1);
+    }
+    const int xb = hl * a.s + j;
+    const int ib = xb / STK_WAVE, lb = xb % STK_WAVE;
+    int64_t pick = v[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) pick = ib == i ? v[i] : pick;
+    bid = __shfl(pick, lb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int x = i * STK_WAVE + lane_id();
+      if (x < total && v[i] == bid) found |= 1ull << (x / a.s);
+    }
+  } else {
+    bid = ids[item];
+    for (int x0 = 0; x0 < total; x0 += 4 * STK_WAVE) {
+      int64_t v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int x = x0 + i * STK_WAVE + lane_id();
+        v[i] = ld_or(grp, (int64_t)x, x < total, (I)-1);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int x = x0 + i * STK_WAVE + lane_id();
+        if (x < total && v[i] == bid) found |= 1ull << (x / a.s);
+      }
     }
   }
-  z = block_sum(z, red);
-  for (int c = 0; c < 4; ++c) part[c * 256 + threadIdx.x] = acc[c];
+  for (int off = 1; off < STK_WAVE; off <<= 1) found |= __shfl_xor(found, off);
+  if (found & ((1ull << hl) - 1ull)) return;   // a lower head owns this block
+  found &= ~((1ull << hl) - 1ull);
+  const bool valid = bid >= 0 && bid < a.n;
+  const int kv = h / G;
+  TL t;
+  t.init(a.d);
+  const float scale = 1.0f / sqrtf((float)a.d);
+  const size_t off = (((size_t)kv * a.n + (valid ? (size_t)bid : 0)) * a.b) * a.d;
+  const T* kb = reinterpret_cast<const T*>(a.k) + off;
+  const T* vb = reinterpret_cast<const T*>(a.v) + off;
+  while (found) {
+    int heads[kGrpHT];
+    int nh = 0;
+#pragma unroll
+    for (int i = 0; i < kGrpHT; ++i) {
+      heads[i] = hl;
+      if (found) {
+        int gg = __ffsll((long long)found) - 1;
+        found &= found - 1;
+        heads[i] = gg;
+        nh = i + 1;
+      }
+    }
+    float qr[kGrpHT][TL::R], m[kGrpHT], l[kGrpHT], acc[kGrpHT][TL::R];
+    uint64_t pmask[kGrpHT];   // rows of at most 64 IDs: positions of b, read with q
+#pragma unroll
+    for (int i = 0; i < kGrpHT; ++i) {
+      m[i] = -INFINITY;
+      l[i] = 0.f;
+#pragma unroll
+      for (int r = 0; r < TL::R; ++r) acc[i][r] = 0.f;
+      t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)(g0 + heads[i]) * a.d, qr[i]);
+      bool in = lane_id() < a.s;
+      int64_t x = ld_or(ids, (int64_t)(g0 + heads[i]) * a.s + lane_id(), in, (I)-1);
+      pmask[i] = __ballot(in && x == bid);
+    }
+    if (valid) {
+      for (int t0 = 0; t0 < a.b; t0 += U * t.tpw) {
+        Raw<T, VEC> kr[U][NC];
+        Raw<T, VEC> vr[U][NC];
+        t.template load_chunk<U, true>(kb, vb, t0, a.b, kr, vr);
+#pragma unroll
+        for (int i = 0; i < kGrpHT; ++i)
+          if (i < nh)
+            t.template update_chunk<U, false, true>(qr[i], kr, vr, t0, a.b, scale, m[i], l[i],
+                                                    acc[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < kGrpHT; ++i)
+        if (i < nh) t.finish(l[i], acc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kGrpHT; ++i) {
+      if (i >= nh) continue;
+      const int gg = heads[i];
+      if (gg == hl) {
+        if (lane_id() == 0) {
+          a.m[item] = m[i];
+          a.l[item] = l[i];
+        }
+        t.store(a.u + item * a.d, acc[i]);
+        continue;
+      }
+      const int64_t rbase = (int64_t)(g0 + gg) * a.s;
+      for (int p0 = 0; p0 < a.s; p0 += STK_WAVE) {
+        int p = p0 + lane_id();
+        uint64_t hits = pmask[i];
+        if (p0 > 0) {
+          int64_t x = ld_or(ids, rbase + p, p < a.s, (I)-1);
+          hits = __ballot(p < a.s && x == bid);
+        }
+        while (hits) {
+          int bit = __ffsll((long long)hits) - 1;
+          hits &= hits - 1;
+          int64_t row = rbase + p0 + bit;
+          if (lane_id() == 0) {
+            a.m[row] = m[i];
+            a.l[row] = l[i];
+          }
+          t.store(a.u + row * a.d, acc[i]);
+        }
+      }
+    }
+  }
+}
+
+// LSE merge of S states per head in one pass over memory: every thread keeps
+// an online (max, sum, vector) over the rows it reads, with all loads of a
+// batch in flight, and the row groups are combined at the end.  Grid (heads,
+// column tiles of 8 lanes * VEC dims); 32 row groups of 8 lanes.
+template <int VEC>
+__global__ __launch_bounds__(256) void k_merge2(MergeArgs a) {
+  constexpr int LPR = 8, RG = 256 / LPR, RB = 4;
+  __shared__ float part[RG][LPR * VEC];
+  __shared__ float gm[RG], gz[RG];
+  const int h = blockIdx.x;
+  const int lc = threadIdx.x % LPR, rg = threadIdx.x / LPR;
+  const int col = blockIdx.y * LPR * VEC + lc * VEC;
+  const float* m = a.m + (size_t)h * a.s;
+  const float* l = a.l + (size_t)h * a.s;
+  const uint8_t* inc = a.inc ? a.inc + (size_t)h * a.s : nullptr;
+  float mt = -INFINITY, zt = 0.f, acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) acc[v] = 0.f;
+  for (int j0 = rg; j0 < a.s; j0 += RG * RB) {
+    float mm[RB], ll[RB], uu[RB][VEC];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      int j = j0 + i * RG;
+      bool in = j < a.s;
+      bool on = in && (!inc || ld_or(inc, (int64_t)j, in, (uint8_t)0));
+      float mv = ld_or(m, (int64_t)j, in, -INFINITY);
+      float lv = ld_or(l, (int64_t)j, in, 0.f);
+      const float* ur = a.u + ((size_t)h * a.s + (in ? j : 0)) * a.d;
+      if constexpr (VEC == 4) {
+        float4 x = *reinterpret_cast<const float4*>(ur + (col < a.d ? col : 0));
+        uu[i][0] = x.x; uu[i][1] = x.y; uu[i][2] = x.z; uu[i][3] = x.w;
+      } else {
+        uu[i][0] = ur[col < a.d ? col : 0];
+      }
+      mm[i] = on ? mv : -INFINITY;
+      ll[i] = on ? lv : 0.f;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) uu[i][v] = on ? uu[i][v] : 0.f;
+    }
+    float bm = mm[0];
+#pragma unroll
+    for (int i = 1; i < RB; ++i) bm = fmaxf(bm, mm[i]);
+    float nm = fmaxf(mt, bm);
+    float alpha = wexp(mt, nm);
+    zt *= alpha;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] *= alpha;
+    mt = nm;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      float w = wexp(mm[i], mt);
+      zt += w * ll[i];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] += w * uu[i][v];
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) part[rg][lc * VEC + v] = acc[v];
+  if (lc == 0) {
+    gm[rg] = mt;
+    gz[rg] = zt;
+  }
   __syncthreads();
-  if (tr == 0) {
-    float inv = 1.f / fmaxf(z, 1e-30f);
-    for (int c = 0; c < 4; ++c) {
-      int dd = td + c * dt;
-      if (dd >= a.d) break;
+  if (rg == 0) {
+    // reference frame: the max over included states, 0 when there is none
+    float M = -INFINITY;
+    for (int r = 0; r < RG; ++r) M = fmaxf(M, gm[r]);
+    if (M == -INFINITY) M = 0.f;
+    float zz = 0.f, f[RG];
+    for (int r = 0; r < RG; ++r) {
+      f[r] = wexp(gm[r], M);
+      zz += f[r] * gz[r];
+    }
+    float inv = 1.f / fmaxf(zz, 1e-30f);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
       float sum = 0.f;
-      for (int r = 0; r < rg; ++r) sum += part[c * 256 + r * dt + td];
-      a.out[(size_t)h * a.d + dd] = sum * inv;
+      for (int r = 0; r < RG; ++r) sum += f[r] * part[r][lc * VEC + v];
+      if (col + v < a.d) a.out[(size_t)h * a.d + col + v] = sum * inv;
     }
   }
 }
@@ -399,8 +724,39 @@ static int launch_states(StatesArgs& a, int dtype, bool with_v, bool slot, hipSt
   if (items == 0) return STK_OK;
   int grid = (int)((items + 3) / 4);
   a.remap = grid >= 8 ? 1 : 0;
+  const int G = a.hq / a.hkv;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
+                          reinterpret_cast<uintptr_t>(a.v);
+  const int nch = with_v && !slot && !a.slot_in ? tok_nch(dtype, a.d, align) : 0;
+  if (nch) {
+    // grouped: one tile read per KV group when the group's rows fit one pass
+    const bool group = !a.active && G > 1 && G <= 64 && (int64_t)G * a.s <= 4 * STK_WAVE;
+    const bool i64 = a.itype == IT_I64;
+    const bool one = a.b <= 16;
+#define STK_TOK(UPV)                                                                            \
+    STK_DISPATCH_TOK(dtype, nch, {                                                              \
+      if (group && i64)                                                                         \
+        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int64_t, true>), dim3(grid), dim3(256), 0, st, a); \
+      else if (group)                                                                           \
+        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int32_t, true>), dim3(grid), dim3(256), 0, st, a); \
+      else if (i64)                                                                             \
+        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int64_t, false>), dim3(grid), dim3(256), 0, st, a); \
+      else                                                                                      \
+        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int32_t, false>), dim3(grid), dim3(256), 0, st, a); \
+    })
+    if (one) STK_TOK(1);
+    else STK_TOK(2);
+#undef STK_TOK
+    return stk_check_launch("k_states_tok");
+  }
+  const bool dedupe = with_v && !slot && !a.active && !a.slot_in && G > 1 && G <= 64 &&
+                      (int64_t)G * a.s <= 4096;
   STK_DISPATCH_TILE(dtype, a.d, {
-    if (slot)
+    if (dedupe && a.itype == IT_I64)
+      hipLaunchKernelGGL((k_states_grp<T, VEC, NC, U, int64_t>), dim3(grid), dim3(256), 0, st, a);
+    else if (dedupe)
+      hipLaunchKernelGGL((k_states_grp<T, VEC, NC, U, int32_t>), dim3(grid), dim3(256), 0, st, a);
+    else if (slot)
       hipLaunchKernelGGL((k_states<T, VEC, NC, U, true, true>), dim3(grid), dim3(256), 0, st, a);
     else if (with_v)
       hipLaunchKernelGGL((k_states<T, VEC, NC, U, true, false>), dim3(grid), dim3(256), 0, st, a);
@@ -438,7 +794,12 @@ int stk_launch_states_skip(const void* q, const void* k, const void* v, int dtyp
 int stk_launch_merge(const float* m, const float* l, const float* u, const uint8_t* inc, int h,
                      int s, int d, float* out, hipStream_t st) {
   MergeArgs a{m, l, u, inc, h, s, d, out};
-  hipLaunchKernelGGL(k_merge, dim3(h), dim3(256), 0, st, a);
+  // vector path needs 16-byte aligned rows (d % 4 == 0 and an aligned base)
+  bool vec = d % 4 == 0 && (reinterpret_cast<uintptr_t>(u) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(k_merge2<4>, dim3(h, (d + 31) / 32), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_merge2<1>, dim3(h, (d + 7) / 8), dim3(256), 0, st, a);
   return stk_check_launch("k_merge");
 }
 

@@ -1,0 +1,221 @@
+// Token-parallel softmax tile for one (query head(s), KV block) pair, built
+// for CDNA4 wave64.
+//
+// Q.K: four lanes share a token row.  Lane (slot, p) holds NCH 16-byte chunks
+// of the row, chunk c covering dims (c*4 + p)*EPC .. +EPC-1, so the four
+// lanes of a slot read 64 contiguous bytes per instruction; 16 token slots
+// per pass, UP passes per chunk of tokens.  16-bit inputs use the packed
+// dot2 instruction (bf16 x bf16 and f16 x f16 products are exact in FP32)
+// against the query held as packed pairs; the four partial dots combine with
+// two xor shuffles inside the quad.
+//
+// P.V: lanes own dims (lane*DPL .. +DPL-1, one 2/4/8-byte access per token
+// row, 256 contiguous bytes per wave instruction); each token's weight is
+// broadcast from the lane that computed it (readlane) and accumulated with
+// FP32 FMAs, so no cross-lane reduction of the value vector is needed.  The
+// running state (m, l, acc) is wave-uniform in m and l.
+//
+// Supported shapes: D = 4 * NCH * EPC with D a multiple of 64 (DPL >= 1);
+// every other shape uses the generic Tile.
+#pragma once
+
+#include "attn.hpp"
+
+namespace stk {
+
+template <typename T> struct Elem;
+template <> struct Elem<bf16s> {
+  __device__ __forceinline__ static float dot(uint32_t k, uint32_t q, float acc) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, k), __builtin_bit_cast(v2, q),
+                                           acc, false);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+};
+template <> struct Elem<f16s> {
+  __device__ __forceinline__ static float dot(uint32_t k, uint32_t q, float acc) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, k), __builtin_bit_cast(v2, q), acc,
+                                  false);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) { return cvt(f16s{uint16_t(w & 0xffffu)}); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return cvt(f16s{uint16_t(w >> 16)}); }
+};
+template <> struct Elem<float> {
+  __device__ __forceinline__ static float dot(uint32_t k, uint32_t q, float acc) {
+    return fmaf(__uint_as_float(k), __uint_as_float(q), acc);
+  }
+};
+
+template <typename T, int NCH, int UP>
+struct TokTile {
+  static constexpr int EPC = 16 / (int)sizeof(T);   // elements per 16-byte chunk
+  static constexpr int LPT = 4;                      // lanes per token row (Q.K)
+  static constexpr int TPP = STK_WAVE / LPT;         // token slots per pass
+  static constexpr int D = LPT * NCH * EPC;
+  static constexpr int DPL = D / STK_WAVE;           // P.V dims per lane
+  static constexpr int QW = NCH * 4;                 // query words per lane
+  static constexpr int CH = TPP * UP;                // tokens per chunk
+  static constexpr int VW = (DPL * (int)sizeof(T) + 3) / 4;   // value words per token
+  static_assert(DPL >= 1 && D % STK_WAVE == 0, "D must be a multiple of 64");
+
+  int slot, part;
+  __device__ __forceinline__ void init() {
+    slot = lane_id() / LPT;
+    part = lane_id() % LPT;
+  }
+  __device__ __forceinline__ int kdim(int c) const { return (c * LPT + part) * EPC; }
+
+  // query row in the Q.K lane layout (raw words)
+  __device__ __forceinline__ void load_q(const T* q, uint32_t* qw) const {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      uint4 x = *reinterpret_cast<const uint4*>(q + kdim(c));
+      qw[4 * c + 0] = x.x; qw[4 * c + 1] = x.y; qw[4 * c + 2] = x.z; qw[4 * c + 3] = x.w;
+    }
+  }
+
+  // K rows of one chunk (tokens t0 + slot + TPP*u) and V rows (tokens t0 .. t0+CH-1)
+  // of the block at kb/vb.  Rows at or past B read row 0 of the block.
+  __device__ __forceinline__ void load(const T* kb, const T* vb, int t0, int B,
+                                       uint32_t (&kw)[UP][QW], uint32_t (&vw)[CH][VW]) const {
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      int t = t0 + slot + TPP * u;
+      const T* row = kb + (size_t)(t < B ? t : 0) * D;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        uint4 x = *reinterpret_cast<const uint4*>(row + kdim(c));
+        kw[u][4 * c + 0] = x.x; kw[u][4 * c + 1] = x.y; kw[u][4 * c + 2] = x.z;
+        kw[u][4 * c + 3] = x.w;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      int t = t0 + i;
+      const T* row = vb + (size_t)(t < B ? t : 0) * D + lane_id() * DPL;
+      if constexpr (DPL * sizeof(T) == 2) {
+        vw[i][0] = *reinterpret_cast<const uint16_t*>(row);
+      } else if constexpr (DPL * sizeof(T) == 4) {
+        vw[i][0] = *reinterpret_cast<const uint32_t*>(row);
+      } else if constexpr (DPL * sizeof(T) == 8) {
+        uint2 x = *reinterpret_cast<const uint2*>(row);
+        vw[i][0] = x.x; vw[i][1] = x.y;
+      } else {
+        uint4 x = *reinterpret_cast<const uint4*>(row);
+        vw[i][0] = x.x; vw[i][1] = x.y; vw[i][2] = x.z; vw[i][3] = x.w;
+      }
+    }
+  }
+
+  // value vector of token i of the chunk as FP32 (this lane's DPL dims)
+  __device__ __forceinline__ void vals(const uint32_t (&vw)[CH][VW], int i, float* out) const {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) out[e] = __uint_as_float(vw[i][e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e)
+        out[e] = (e & 1) ? Elem<T>::hi(vw[i][e / 2]) : Elem<T>::lo(vw[i][e / 2]);
+    }
+  }
+
+  // scaled logits of the chunk's tokens in this lane's slot (-inf past B)
+  __device__ __forceinline__ void scores(const uint32_t* qw, const uint32_t (&kw)[UP][QW], int t0,
+                                         int B, float scale, float* s) const {
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < QW; ++w) acc = Elem<T>::dot(kw[u][w], qw[w], acc);
+      acc += __shfl_xor(acc, 1);
+      acc += __shfl_xor(acc, 2);
+      int t = t0 + slot + TPP * u;
+      s[u] = t < B ? acc * scale : -INFINITY;
+    }
+  }
+
+  // Online-softmax update of (m, l, acc) with one chunk.  FIXED keeps m as
+  // the exponent frame (no rescaling; the caller guarantees it).  ABS also
+  // accumulates sum |w * v| (low-group envelope).
+  template <bool FIXED, bool ABS>
+  __device__ __forceinline__ void update(const uint32_t* qw, const uint32_t (&kw)[UP][QW],
+                                         const uint32_t (&vw)[CH][VW], int t0, int B,
+                                         float scale, float& m, float& l, float* acc,
+                                         float* aacc = nullptr) const {
+    float s[UP];
+    scores(qw, kw, t0, B, scale, s);
+    if constexpr (!FIXED) {
+      float cm = s[0];
+#pragma unroll
+      for (int u = 1; u < UP; ++u) cm = fmaxf(cm, s[u]);
+      for (int off = LPT; off < STK_WAVE; off <<= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+      float nm = fmaxf(m, cm);
+      if (nm > m) {
+        float alpha = m == -INFINITY ? 0.f : expf(m - nm);
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
+        m = nm;
+      }
+    }
+    float w[UP];
+#pragma unroll
+    for (int u = 0; u < UP; ++u) w[u] = s[u] == -INFINITY ? 0.f : expf(s[u] - m);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int u = i / TPP, src = (i % TPP) * LPT;
+      float wt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w[u]), src));
+      float v[DPL];
+      vals(vw, i, v);
+      l += wt;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        float x = wt * v[e];
+        acc[e] += x;
+        if constexpr (ABS) aacc[e] += fabsf(x);
+      }
+    }
+  }
+
+  // this lane's DPL dims of a D-vector
+  __device__ __forceinline__ void store(float* dst, const float* acc, float scale = 1.f) const {
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) dst[lane_id() * DPL + e] = acc[e] * scale;
+  }
+};
+
+// Token-tile shape for (dtype, D): NCH chunks per lane; 0 when unsupported.
+inline int tok_nch(int dtype, int d, uintptr_t align_bits) {
+  if ((align_bits & 15) != 0) return 0;
+  int esize = dtype == DT_F32 ? 4 : 2;
+  int epc = 16 / esize;
+  if (d % 64 != 0 || d % (4 * epc) != 0) return 0;
+  int nch = d / (4 * epc);
+  if (esize == 2 && (nch == 2 || nch == 4 || nch == 8)) return nch;
+  if (esize == 4 && (nch == 4 || nch == 8)) return nch;
+  return 0;
+}
+
+}  // namespace stk
+
+// Dispatch: binds T, NCH for EXPR when the token tile supports (dtype, d).
+#define STK_DISPATCH_TOK(dtype, nch, EXPR)                          \
+  do {                                                              \
+    if (dtype == stk::DT_BF16) {                                    \
+      using T = stk::bf16s;                                         \
+      if (nch == 2) { constexpr int NCH = 2; EXPR; }                \
+      else if (nch == 4) { constexpr int NCH = 4; EXPR; }           \
+      else { constexpr int NCH = 8; EXPR; }                         \
+    } else if (dtype == stk::DT_F16) {                              \
+      using T = stk::f16s;                                          \
+      if (nch == 2) { constexpr int NCH = 2; EXPR; }                \
+      else if (nch == 4) { constexpr int NCH = 4; EXPR; }           \
+      else { constexpr int NCH = 8; EXPR; }                         \
+    } else {                                                        \
+      using T = float;                                              \
+      if (nch == 4) { constexpr int NCH = 4; EXPR; }                \
+      else { constexpr int NCH = 8; EXPR; }                         \
+    }                                                               \
+  } while (0)

@@ -75,6 +75,40 @@ def test_gqa_select_ids_bit_exact():
         assert ids.cpu().numpy().tolist() == ref.tolist(), (hq, n, topk)
 
 
+@pytest.mark.parametrize("n,topk", [(7, 7), (1000, 1), (2048, 64), (3000, 3000), (4096, 64),
+                                    (8192, 2048), (16384, 100), (20000, 333)])
+def test_select_ties_and_row_lengths(n, topk):
+    """Many exactly tied scores (small-integer q and bounds), every register
+    tile size of the top-K kernel and the long-row path, k == n."""
+    from strict_topk import gqa
+    gen = torch.Generator().manual_seed(n + topk)
+    hq, hkv, d = 4, 2, 16
+    q = torch.randint(-2, 3, (hq, d), generator=gen).to(torch.bfloat16)
+    lo = torch.randint(-3, 1, (hkv, n, d), generator=gen).float()
+    hi = lo + torch.randint(0, 3, (hkv, n, d), generator=gen).float()
+    q[1].zero_()
+    ref = O.select_blocks(*np_(q, lo, hi), topk)
+    ids = gqa.select_blocks(*dev(q, lo, hi), topk)
+    assert ids.cpu().numpy().tolist() == ref.tolist()
+    assert ids[1].cpu().tolist() == list(range(topk))
+
+
+def test_select_nonfinite_bounds():
+    """-inf/+inf bounds and NaN scores: NaN ranks below -inf."""
+    from strict_topk import gqa
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn((2, 8), generator=gen).half()
+    lo = torch.randn((2, 40, 8), generator=gen)
+    hi = lo + 1
+    lo[0, 3] = float("-inf")
+    hi[1, 5] = float("inf")
+    lo[1, 7, 0] = float("nan")
+    hi[1, 7, 0] = float("nan")
+    ref = O.select_blocks(*np_(q, lo, hi), 39)
+    ids = gqa.select_blocks(*dev(q, lo, hi), 39)
+    assert ids.cpu().numpy().tolist() == ref.tolist()
+
+
 def test_select_rejects_bad_k():
     from strict_topk import gqa
     q = torch.randn((4, 8), device=DEV)
@@ -282,6 +316,51 @@ def test_gqa_paths(hq):
             check(gqa_light.repair_saved_auto(q, k, v, a, p, st, emf), expected, (name, "auto", emf))
     with pytest.raises(ValueError):
         gqa_light.repair_saved_auto(q, k, v, a, p, st, 1.5)
+
+
+@pytest.mark.parametrize("hq,hkv,n,b,d,sa,sp,hits,dtype", [
+    (8, 2, 300, 32, 128, 64, 64, 58, torch.bfloat16),     # grouped rows sharing blocks
+    (8, 2, 300, 64, 128, 40, 40, 0, torch.bfloat16),      # no hits, two-chunk tiles
+    (4, 1, 9000, 8, 256, 100, 120, 100, torch.float16),   # all hits, wide rows, big N
+    (6, 3, 12000, 5, 70, 37, 29, 11, torch.float32),      # odd D and B, brute-force membership
+    (16, 4, 2048, 32, 128, 64, 64, 48, torch.bfloat16),   # c3-like, 16 misses per head
+])
+def test_gqa_states_and_repair_shapes(hq, hkv, n, b, d, sa, sp, hits, dtype):
+    """Deduplicated GQA states (one tile read per KV group) and the
+    single-launch saved / union / light repair against the oracle."""
+    from strict_topk import gqa, gqa_light
+    gen = torch.Generator().manual_seed(hq * 7 + n)
+    q = torch.randn((hq, d), generator=gen).to(dtype)
+    k = torch.randn((hkv, n, b, d), generator=gen).to(dtype)
+    v = torch.randn(k.shape, generator=gen).to(dtype)
+    g = hq // hkv
+    rows_a, rows_p = [], []
+    for kv in range(hkv):
+        pool = torch.randperm(n, generator=gen)[:sa + sp + 8]
+        for _ in range(g):
+            # heads of a group draw from one pool, so their rows overlap
+            a_row = pool[torch.randperm(sa + 8, generator=gen)[:sa]]
+            others = pool[sa + 8:]
+            keep = a_row[torch.randperm(sa, generator=gen)[:hits]]
+            p_row = torch.cat((keep, others[torch.randperm(len(others), generator=gen)[:sp - hits]]))
+            rows_a.append(a_row)
+            rows_p.append(p_row[torch.randperm(sp, generator=gen)])
+    a = torch.stack(rows_a).to(torch.int64)
+    p = torch.stack(rows_p).to(torch.int32)
+    qn, kn, vn, an, pn = np_(q, k, v, a, p)
+    ref = O.block_states(qn, kn, vn, pn)
+    qd, kd, vd, ad, pd = dev(q, k, v, a, p)
+    st = gqa.partials(qd, kd, vd, pd)
+    np.testing.assert_allclose(st.m.cpu().double().numpy(), ref.m, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(st.l.cpu().double().numpy(), ref.l, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(st.u.cpu().double().numpy(), ref.u, rtol=1e-4, atol=1e-4)
+    expected = O.attention(qn, kn, vn, an)
+    check(gqa.exact(qd, kd, vd, ad), expected, "exact")
+    check(gqa.repair_saved(qd, kd, vd, ad, pd, st), expected, "saved")
+    check(gqa_light.repair_saved_light(qd, kd, vd, ad, pd, st), expected, "light")
+    hit = (an[:, :, None] == pn[:, None, :]).any(-1)
+    union = O.attention(qn, kn, vn, [np.concatenate((pn[r], an[r][~hit[r]])) for r in range(hq)])
+    check(gqa.repair_union(qd, kd, vd, ad, pd, st), union, "union")
 
 
 def test_gqa_validation_messages():

@@ -183,7 +183,7 @@ def test_topk_brute_force_with_ties():
         for r in range(2):
             key = [(1 if math.isnan(x) else 0, 0 if math.isnan(x) else -x, i)
                    for i, x in enumerate(s[r])]
-            want = [i for _, _, i in sorted(key)][:k]
+            want = sorted(i for _, _, i in sorted(key)[:k])
             assert got[r].tolist() == want
 
 
