@@ -2,24 +2,35 @@
 """Benchmark: one speculative block-sparse Top-K decode step on one MI355X.
 
 A step is select (fused bound scorer + exact top-K) concurrently with
-speculative GQA attention over the predicted blocks, joined, then the strict
-repair -- the full path of the reference's ``overlap_run``
-(``benchmarks/run_benchmark.py:99-118``), captured once into a HIP graph and
-replayed.  The workload is config c3 (Qwen3-4B-like shape, 64K context, K=64,
-90 % prediction overlap, bf16), the configuration
-the north-star target is stated on.
+speculative GQA attention over the already-known predicted blocks, then the
+strict repair -- the full path of the reference's ``overlap_run``
+(``benchmarks/run_benchmark.py:99-118``).  It runs as ``strict_topk.step``:
+one launch whose workgroups either score blocks or compute the predicted
+blocks' states, then one launch doing the top-K and the repair per query
+head.  The workload is config c3 (Qwen3-4B-like shape, 64K context, K=64,
+90 % prediction overlap, bf16), the configuration the north-star target is
+stated on.
 
-Printed JSON line (rank 0 only, one GPU):
-  value / ms_per_step   microseconds per full decode step (lower is better),
-                        timed over exactly --steps graph replays bracketed by
-                        torch.cuda.synchronize(), inputs resident in HBM;
-  serial_us             the same-work serial step (select, then attention over
-                        the selected blocks), paired ABBA replay timing;
-  roofline              dominant kernel, algorithmic bytes / average launch
-                        duration measured here with HIP events on its stream;
+Timing.  M consecutive decode steps are captured into one HIP graph, step i
+reading the i % M-th of M device copies of the inputs (identical values,
+different addresses), so the touched working set (~45 MB a step) exceeds
+the L2 and Infinity Cache and operands come from HBM, as in a decode loop
+where every layer's KV is touched once per token.  The timed region is
+exactly --steps steps (--steps / M replays) bracketed by
+torch.cuda.synchronize().  The same construction times the same-work serial
+path (select, then attention over the selected blocks) and the drop-in
+two-stream composition; "hot" variants replay all M steps on one input copy
+(the reference's own method, caches warm).
+
+Printed JSON line (one GPU):
+  value / ms_per_step   microseconds per full decode step (lower is better);
+  serial_us             the serial path, paired ABBA replay timing;
+  roofline              dominant kernel (k_front: select || speculate),
+                        algorithmic bytes / average launch time measured here
+                        with HIP events on its stream;
   path_roofline         the whole step's algorithmic bytes against 8 TB/s;
   cpu_baseline          this repository's torch-CPU port of the reference's
-                        serial path on a bounded sample of the same workload.
+                        serial path, timed on a bounded sample.
 """
 from __future__ import annotations
 
@@ -46,14 +57,32 @@ def log(msg):
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=2400)
+    ap.add_argument("--warmup", type=int, default=240)
     ap.add_argument("--config", default="c3", choices=("c2", "c3"))
     ap.add_argument("--overlap", type=float, default=0.9)
     ap.add_argument("--seed", type=int, default=20261103)
+    ap.add_argument("--graph-steps", type=int, default=12,
+                    help="decode steps per captured graph (and input copies)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     return ap.parse_args()
+
+
+def divisor_at_most(k, m):
+    for x in range(min(k, m), 0, -1):
+        if k % x == 0:
+            return x
+    return 1
+
+
+def traffic_record(workload):
+    """HBM bytes per k_front launch from the committed rocprof counter runs."""
+    path = ROOT / "profiles" / "k_front_traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text())
+    return rec.get(workload)
 
 
 def main():
@@ -73,84 +102,109 @@ def main():
     _lib.lib()   # fail loudly if the HIP library is missing
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    log(f"bench: building {args.config} inputs (seed {args.seed}, overlap {args.overlap})")
-    step = decode.gqa_step(args.config, args.overlap, args.seed, dev)
+    M = divisor_at_most(args.steps, args.graph_steps)
+    log(f"bench: {args.config} inputs, {M} device copies (seed {args.seed}, "
+        f"overlap {args.overlap})")
+    step = decode.gqa_step(args.config, args.overlap, args.seed, dev, sets=M)
     cfg = step.cfg
     q, k, v, lo, hi = step.host
 
-    # ---- parity of the measured configuration against the FP64 oracle
+    # ---- parity of every measured path against the FP64 oracle
     log("bench: oracle selection and attention")
     qn, kn, vn = (t.double().numpy() for t in (q, k, v))
     ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), cfg.topk)
     ids_exact = bool(np.array_equal(step.selected.cpu().numpy(), ref_ids))
     expected = O.attention(qn, kn, vn, ref_ids)
 
-    log("bench: capturing graphs")
-    g_full, out_full = timing.capture(step.full)
-    g_serial, out_serial = timing.capture(step.serial)
-    g_select, _ = timing.capture(step.select)
-    g_spec, st_spec = timing.capture(step.speculate)
-    a_fixed = step.selected
-    g_repair, _ = timing.capture(lambda: step.finish(a_fixed, st_spec))
-
     def err(out):
         o = out.double().cpu().numpy()
         d = np.abs(o - expected)
-        return float(d.max()), float((d / np.maximum(np.abs(expected), 1e-30)).max()), \
-            bool((d <= 3e-4 + 3e-4 * np.abs(expected)).all() and np.isfinite(o).all())
+        return (float(d.max()), float((d / np.maximum(np.abs(expected), 1e-30)).max()),
+                bool((d <= 3e-4 + 3e-4 * np.abs(expected)).all() and np.isfinite(o).all()))
 
-    abs_full, rel_full, ok_full = err(out_full)
-    abs_ser, _, ok_ser = err(out_serial)
-    if not (ids_exact and ok_full and ok_ser):
-        sys.exit(f"bench: parity failed (ids exact {ids_exact}, full err {abs_full:.3g}, "
-                 f"serial err {abs_ser:.3g})")
+    def seq(fn, hot):
+        return lambda: [fn(0 if hot else i) for i in range(M)]
 
-    # ---- the timed region: exactly --steps full decode steps
-    log(f"bench: {args.warmup} warm-up + {args.steps} timed full steps")
-    for _ in range(args.warmup):
-        g_full.replay()
+    log("bench: capturing graphs")
+    graphs, outs = {}, {}
+    for name, fn in (("fused", step.fused), ("serial", step.serial), ("composed", step.full)):
+        for hot in (False, True):
+            key = name + ("_hot" if hot else "")
+            graphs[key], outs[key] = timing.capture(seq(fn, hot))
+    parity = {}
+    for key, out in outs.items():
+        worst = max((err(o) for o in out), key=lambda e: e[0])
+        parity[key] = worst
+        if not (ids_exact and worst[2]):
+            sys.exit(f"bench: parity failed for {key} (ids exact {ids_exact}, "
+                     f"max abs err {worst[0]:.3g})")
+
+    # ---- the timed region: exactly --steps fused decode steps (cold)
+    g = graphs["fused"]
+    warm = max(1, args.warmup // M)
+    reps = args.steps // M
+    log(f"bench: {warm * M} warm-up + {reps * M} timed steps ({M} per graph replay)")
+    for _ in range(warm):
+        g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(args.steps):
-        g_full.replay()
+    for _ in range(reps):
+        g.replay()
     e1.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    ms_per_step = e0.elapsed_time(e1) / args.steps
-    # the replay output must still be right after the timed region
-    if not err(out_full)[2]:
-        sys.exit("bench: full-path output changed during timing")
+    ms_per_step = e0.elapsed_time(e1) / (reps * M)
+    if not all(err(o)[2] for o in outs["fused"]):
+        sys.exit("bench: fused-path output changed during timing")
 
-    log("bench: paired ABBA intervals (full, serial, phases)")
-    med, _ = timing.paired({"full": g_full, "serial": g_serial, "select": g_select,
-                            "speculate": g_spec, "repair": g_repair}, replays=100, rounds=5,
-                           seed=args.seed)
+    log("bench: paired ABBA intervals")
+    med, _ = timing.paired(graphs, replays=max(1, 120 // M), rounds=5, seed=args.seed)
+    per_step = {key: round(us / M, 3) for key, us in med.items()}
 
-    # ---- dominant-kernel roofline: speculative states kernel (k_states),
-    # one launch per call of gqa.partials, events on its stream
+    # ---- dominant-kernel roofline: k_front (select || speculate), one launch
+    # per call of stk_step_front, HIP events on its stream, input copies rotated
+    from strict_topk import step as step_mod  # noqa: F401  (loads the symbols)
+    c = cfg
+    st = step.speculate(0)
+    ws = _lib.workspace(_lib.size("stk_step_workspace_bytes", c.hq, c.hkv, c.blocks, c.dim,
+                                  c.topk), dev)
+    L = _lib.lib()
+    state = [0]
+
+    def front():
+        i = state[0] % M
+        state[0] += 1
+        sq, sk, sv, slo, shi = step.sets[i]
+        rc = L.stk_step_front(sq.data_ptr(), sk.data_ptr(), sv.data_ptr(), _lib.dtype_code(sq),
+                              c.hq, c.hkv, c.blocks, c.block, c.dim, slo.data_ptr(),
+                              shi.data_ptr(), c.topk, step.predicted.data_ptr(), 0, c.sp,
+                              st.m.data_ptr(), st.l.data_ptr(), st.u.data_ptr(), ws.data_ptr(),
+                              ws.numel(), _lib.stream(dev))
+        assert rc == 0, L.stk_last_error()
+
+    # the launches are captured (4 per input copy) so the host's call rate
+    # does not bound the measurement; per launch = replay interval / launches
+    nfront = 4 * M
+    g_front, _ = timing.capture(lambda: [front() for _ in range(nfront)])
+    timing.warm([g_front], ms=50.0)
+    front_us = min(timing.interval_us(g_front, 20) for _ in range(5)) / nfront
+    fb = step.front_bytes()
+    achieved = fb / (front_us * 1e-6) / 1e9
+    workload = f"{cfg.name}@{args.overlap}"
+    roofline = {"kernel": "k_front (select || speculate)", "bound": "hbm",
+                "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(achieved / 8000.0, 4), "traffic": traffic_record(workload),
+                "bytes_per_launch": fb, "us_per_launch": round(front_us, 3)}
+
     by = step.bytes()
-    kernels = {}
-    st_us = timing.launch_us(step.speculate, launches=500)
-    spec_bytes = by.kv_spec + cfg.hq * cfg.sp * 4 * (cfg.dim + 2) + cfg.hq * cfg.dim * 2 \
-        + cfg.hq * cfg.sp * 4
-    kernels["k_states(speculate)"] = {"us": st_us, "bytes": spec_bytes}
-    sel_us = timing.launch_us(step.select, launches=500)
-    kernels["select(k_score_sort+k_topk_merge)"] = {"us": sel_us, "bytes": by.meta}
-    dominant = "k_states(speculate)"
-    dk = kernels[dominant]
-    achieved = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
-    roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
-                "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
-                "traffic": None, "bytes_per_launch": dk["bytes"], "us_per_launch": round(dk["us"], 3)}
-
     full_us = ms_per_step * 1e3
     path = {"algorithmic_bytes": by.full, "kv_bytes": by.kv_full,
             "frac": round(by.full / (full_us * 1e-6) / decode.HBM_PEAK, 4),
             "kv_frac": round(by.kv_full / (full_us * 1e-6) / decode.HBM_PEAK, 4),
             "serial_bytes": by.serial,
-            "serial_frac": round(by.serial / (med["serial"] * 1e-6) / decode.HBM_PEAK, 4)}
+            "serial_frac": round(by.serial / (per_step["serial"] * 1e-6) / decode.HBM_PEAK, 4)}
 
     cpu = None
     if not args.no_cpu:
@@ -164,25 +218,25 @@ def main():
 
     line = {
         "metric": "us/decode step full path (select+spec+repair) vs serial; HBM GB/s % of peak",
-        "value": round(full_us, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": False,
+        "value": round(full_us, 3), "unit": "us/step", "n_gpus": 1, "steps": reps * M,
+        "warmup": warm * M, "ms_per_step": round(ms_per_step, 6), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded CPU generator, hot blocks +1.5 along the group-mean query)",
         "config": {"workload": f"{cfg.name}: Hq={cfg.hq} Hkv={cfg.hkv} D={cfg.dim} "
                                f"B={cfg.block} N={cfg.blocks} K={cfg.topk} "
-                               f"overlap={args.overlap} gqa_light auto repair",
+                               f"overlap={args.overlap}, fused select||speculate + "
+                               "top-K/repair, inputs rotated over "
+                               f"{M} HBM copies",
                    "context": cfg.context, "topk": cfg.topk, "overlap": args.overlap,
-                   "seed": args.seed},
-        "serial_us": round(med["serial"], 3),
-        "speedup_vs_serial": round(med["serial"] / med["full"], 4),
-        "paired_us": {k_: round(v_, 3) for k_, v_ in med.items()},
+                   "seed": args.seed, "steps_per_graph": M},
+        "serial_us": per_step["serial"],
+        "speedup_vs_serial": round(per_step["serial"] / per_step["fused"], 4),
+        "paired_us_per_step": per_step,
         "roofline": roofline,
         "path_roofline": path,
-        "kernels": {k_: {"us": round(v_["us"], 3), "bytes": v_["bytes"],
-                         "GB/s": round(v_["bytes"] / (v_["us"] * 1e-6) / 1e9, 1)}
-                    for k_, v_ in kernels.items()},
-        "parity": {"ids_bit_exact": ids_exact, "max_abs_err": abs_full, "max_rel_err": rel_full,
-                   "serial_max_abs_err": abs_ser},
+        "parity": {"ids_bit_exact": ids_exact,
+                   "max_abs_err": {k_: v_[0] for k_, v_ in parity.items()},
+                   "tolerance": "|err| <= 3e-4 + 3e-4 |ref| vs FP64"},
         "wall_ms_timed_region": round(wall_ms, 2),
         "cpu_baseline": cpu,
     }

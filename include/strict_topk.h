@@ -58,7 +58,7 @@ size_t stk_select_workspace_bytes(int hq, int hkv, int n, int d, int topk);
 /* strict_topk/selector.py:41-43 select_blocks and gqa.py:145-161
  * select_blocks (score + torch.topk(sorted=False)): ids[h, 0..topk) are the
  * topk highest-scoring blocks, ties toward the lower block index, in
- * (score desc, index asc) order.  `scores` may be NULL. */
+ * ascending block order.  `scores` may be NULL. */
 int stk_select_blocks(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
                       int hkv, int n, int d, int topk, float* scores, int32_t* ids,
                       void* workspace, size_t workspace_bytes, void* stream);
@@ -195,6 +195,44 @@ int stk_hier_repair(const void* q, const void* k, const void* v, int dtype, int 
                     const void* predicted, int pred_dtype, int sp, const float* pm,
                     const float* pl, const float* pu, int shared, float* out, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------- fused decode step */
+
+size_t stk_step_workspace_bytes(int hq, int hkv, int n, int d, int topk);
+
+/* 1 when stk_speculative_step supports the shape (alignment aside). */
+int stk_step_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
+                       int pred_dtype);
+
+/* The full speculative decode step of benchmarks/run_benchmark.py:99-118
+ * (overlap_run: gqa.select_blocks || gqa.partials on the predicted blocks,
+ * then gqa_light.repair_saved_light / gqa.repair_saved, or gqa.repair_union
+ * with union_mode 1) in two launches on one stream: a grid whose workgroups
+ * either score blocks or compute the predicted blocks' states, then one
+ * workgroup per query head doing the exact top-K and the repair.  Outputs:
+ * selected[Hq,topk] int32 (ascending IDs, as stk_select_blocks), the
+ * prediction state m,l[Hq,sp], u[Hq,sp,D] (as stk_block_partials) and
+ * out[Hq,D].  bf16/fp16 only, int32 predicted IDs, D in {64, 128, 256}. */
+int stk_speculative_step(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                         int n, int b, int d, const float* lo, const float* hi, int topk,
+                         const void* predicted, int pred_dtype, int sp, int union_mode,
+                         int32_t* selected, float* m, float* l, float* u, float* out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* The two launches of stk_speculative_step separately.  stk_step_front
+ * (select || speculate) writes the prediction state and the score keys into
+ * `workspace`; stk_step_tail (top-K + repair) reads them from the same
+ * workspace and writes `selected` and `out`. */
+int stk_step_front(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
+                   int b, int d, const float* lo, const float* hi, int topk,
+                   const void* predicted, int pred_dtype, int sp, float* m, float* l, float* u,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+int stk_step_tail(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
+                  int b, int d, int topk, const void* predicted, int pred_dtype, int sp,
+                  int union_mode, const float* m, const float* l, const float* u,
+                  int32_t* selected, float* out, void* workspace, size_t workspace_bytes,
+                  void* stream);
 
 #ifdef __cplusplus
 }

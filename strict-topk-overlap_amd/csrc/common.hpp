@@ -80,6 +80,12 @@ __device__ __forceinline__ void store_id(void* ids, int itype, int64_t i, int64_
   else reinterpret_cast<int32_t*>(ids)[i] = (int32_t)v;
 }
 
+// Q, K, V of one call: q[hq, d]; k, v[hkv, n, b, d]; head h reads KV head h / (hq / hkv).
+struct KV {
+  const void* q; const void* k; const void* v;
+  int hq, hkv, n, b, d;
+};
+
 // Branch-free guarded load: the access is always issued (from index 0 when
 // !ok, which callers guarantee to be valid), and the value replaced after.
 // Keeping loads out of branches lets the compiler keep them all in flight.

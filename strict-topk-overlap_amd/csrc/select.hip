@@ -23,139 +23,16 @@
 //               from the highest bit where the row's keys differ, stopping
 //               as soon as the threshold digit's bin is taken whole), then a
 //               block-wide scan writes the selected IDs in index order.
-#include "attn.hpp"
+#include "score.hpp"
+#include "topk.hpp"
 #include "api.hpp"
 
 namespace stk {
 
 constexpr int kTopkThreads = 256;
-constexpr int kScoreWaves = 4;
-
-// Order-preserving map of a double to an unsigned key; NaN -> 0 (lowest),
-// -0.0 -> +0.0.
-__device__ __forceinline__ uint64_t score_key(double s) {
-  if (s != s) return 0ull;
-  if (s == 0.0) s = 0.0;
-  uint64_t b = (uint64_t)__double_as_longlong(s);
-  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
-}
-
-struct ScoreArgs {
-  const void* q; int qtype;
-  const float* lo; const float* hi;
-  int hq, hkv, n, d;
-  int chunks;            // workgroups per KV head
-  float* scores;         // optional FP32 [hq, n]
-  uint64_t* keys;        // optional [hq, n]
-};
-
-template <typename Q>
-__device__ __forceinline__ float qval(const void* q, int64_t i) {
-  return cvt(reinterpret_cast<const Q*>(q)[i]);
-}
-
-// P = 64-dim passes (D <= 64 * P), STEPS = 4-block wave steps per wave,
-// GT = query heads whose rows are held in registers at a time.
 template <typename Q, int P, int STEPS, bool VEC4, int GT>
 __global__ __launch_bounds__(256) void k_score(ScoreArgs a) {
-  const int G = a.hq / a.hkv;
-  const int kv = blockIdx.x / a.chunks;
-  const int chunk = blockIdx.x % a.chunks;
-  const int h0 = kv * G;
-  const int lane = lane_id();
-  const int lane16 = lane & 15;
-  const int sub = lane >> 4;                  // block within a 4-block step
-  const int wave_base = (chunk * kScoreWaves + wave_id()) * (4 * STEPS);
-  const Q* qrow = reinterpret_cast<const Q*>(a.q) + (size_t)h0 * a.d;
-  // every load of the wave is issued before any arithmetic, with no branch
-  // around a load: out-of-range blocks, dims and heads read a valid address
-  // and are zeroed
-  float4 lv[STEPS][P], hv[STEPS][P];
-#pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    int nb = wave_base + 4 * s + sub;
-    bool valid = nb < a.n;
-    const float* lrow = a.lo + ((size_t)kv * a.n + (valid ? nb : 0)) * a.d;
-    const float* hrow = a.hi + ((size_t)kv * a.n + (valid ? nb : 0)) * a.d;
-#pragma unroll
-    for (int j = 0; j < P; ++j) {
-      int d0 = 64 * j + 4 * lane16;
-      if constexpr (VEC4) {
-        bool ok = valid && d0 < a.d;
-        float4 l4 = *reinterpret_cast<const float4*>(lrow + (ok ? d0 : 0));
-        float4 h4 = *reinterpret_cast<const float4*>(hrow + (ok ? d0 : 0));
-        lv[s][j] = ok ? l4 : make_float4(0.f, 0.f, 0.f, 0.f);
-        hv[s][j] = ok ? h4 : make_float4(0.f, 0.f, 0.f, 0.f);
-      } else {
-        float l4[4], h4[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          bool ok = valid && d0 + t < a.d;
-          l4[t] = ld_or(lrow, (int64_t)(d0 + t), ok, 0.f);
-          h4[t] = ld_or(hrow, (int64_t)(d0 + t), ok, 0.f);
-        }
-        lv[s][j] = make_float4(l4[0], l4[1], l4[2], l4[3]);
-        hv[s][j] = make_float4(h4[0], h4[1], h4[2], h4[3]);
-      }
-    }
-  }
-  for (int gb = 0; gb < G; gb += GT) {
-    // query values of heads gb .. gb+GT-1 at this lane's dims, as doubles
-    double qd[GT][P][4];
-#pragma unroll
-    for (int gi = 0; gi < GT; ++gi) {
-      const bool hv_ok = gb + gi < G;
-      const Q* qg = qrow + (size_t)(hv_ok ? gb + gi : 0) * a.d;
-#pragma unroll
-      for (int j = 0; j < P; ++j) {
-        int d0 = 64 * j + 4 * lane16;
-        if constexpr (VEC4) {
-          // four consecutive elements in one 8- or 16-byte access
-          bool ok = hv_ok && d0 < a.d;
-          Raw<Q, 4> r;
-          r.load(qg + (ok ? d0 : 0));
-#pragma unroll
-          for (int t = 0; t < 4; ++t) qd[gi][j][t] = ok ? (double)r.get(t) : 0.0;
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            bool ok = hv_ok && d0 + t < a.d;
-            float qv = cvt(qg[ok ? d0 + t : 0]);
-            qd[gi][j][t] = ok ? (double)qv : 0.0;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const int nb = wave_base + 4 * s + sub;
-#pragma unroll
-      for (int gi = 0; gi < GT; ++gi) {
-        double acc = 0.0;
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-          const float lvv[4] = {lv[s][j].x, lv[s][j].y, lv[s][j].z, lv[s][j].w};
-          const float hvv[4] = {hv[s][j].x, hv[s][j].y, hv[s][j].z, hv[s][j].w};
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            // a zero q (out of range) adds +0.0, which leaves the sum unchanged
-            double b = qd[gi][j][t] >= 0.0 ? (double)hvv[t] : (double)lvv[t];
-            acc = fma(qd[gi][j][t], b, acc);   // exact product, one rounding
-          }
-        }
-        acc = acc + __shfl_xor(acc, 8);
-        acc = acc + __shfl_xor(acc, 4);
-        acc = acc + __shfl_xor(acc, 2);
-        acc = acc + __shfl_xor(acc, 1);
-        if (lane16 == 0 && nb < a.n && gb + gi < G) {
-          if (acc == 0.0) acc = 0.0;
-          size_t o = (size_t)(h0 + gb + gi) * a.n + nb;
-          if (a.scores) a.scores[o] = (float)acc;
-          if (a.keys) a.keys[o] = score_key(acc);
-        }
-      }
-    }
-  }
+  score_wg<Q, P, STEPS, VEC4, GT>(a, blockIdx.x);
 }
 
 struct TopkArgs {
@@ -164,113 +41,13 @@ struct TopkArgs {
   int32_t* ids;
 };
 
-// Thread t owns indices [t*KPT, t*KPT + KPT) so that an exclusive scan in
-// thread order is a scan in index order.  N <= 256 * KPT.
+// One workgroup per row (TopkArgs.keys[row, 0..n)), see topk.hpp.
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void k_topk(TopkArgs a) {
-  __shared__ int hist[256];
-  __shared__ int tmp[kTopkThreads / STK_WAVE];
-  __shared__ uint64_t red64[2][kTopkThreads / STK_WAVE];
-  __shared__ int pick[2];
-  const int row = blockIdx.x;
-  const uint64_t* rk = a.keys + (size_t)row * a.n;
-  const int base = threadIdx.x * KPT;
-  uint64_t key[KPT];
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) key[i] = ld_or(rk, (int64_t)(base + i), base + i < a.n, (uint64_t)0);
-  // bits shared by every key of the row
-  uint64_t vor = 0ull, vand = ~0ull;
-#pragma unroll
-  for (int i = 0; i < KPT; ++i)
-    if (base + i < a.n) {
-      vor |= key[i];
-      vand &= key[i];
-    }
-  vor = wave_or64(vor);
-  vand = wave_and64(vand);
-  if (lane_id() == 0) {
-    red64[0][wave_id()] = vor;
-    red64[1][wave_id()] = vand;
-  }
-  __syncthreads();
-  vor = 0ull;
-  vand = ~0ull;
-  for (int w = 0; w < kTopkThreads / STK_WAVE; ++w) {
-    vor |= red64[0][w];
-    vand &= red64[1][w];
-  }
-  const uint64_t diff = vor ^ vand;
-  uint64_t mask = ~0ull, prefix = vand;   // when every key is equal
-  int need = a.k;
-  if (diff != 0ull) {
-    int start = 63 - __clzll((long long)diff);
-    mask = start == 63 ? 0ull : ~0ull << (start + 1);
-    prefix = vand & mask;
-    while (true) {
-      const int shift = start >= 7 ? start - 7 : 0;
-      const int width = start - shift + 1;
-      const uint64_t dmask = ((1ull << width) - 1ull);
-      for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < KPT; ++i)
-        if (base + i < a.n && (key[i] & mask) == prefix)
-          atomicAdd(&hist[(key[i] >> shift) & dmask], 1);
-      __syncthreads();
-      if (wave_id() == 0) {
-        // lane l owns bins 255-4l .. 252-4l (descending digit order)
-        int c[4], s = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          c[t] = hist[255 - 4 * lane_id() - t];
-          s += c[t];
-        }
-        int inc = wave_incl_scan(s);
-        int above = inc - s;        // keys in higher bins than this lane's
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (above < need && above + c[t] >= need) {
-            pick[0] = 255 - 4 * lane_id() - t;
-            pick[1] = above;
-          }
-          above += c[t];
-        }
-      }
-      __syncthreads();
-      const int bin = pick[0];
-      const int above = pick[1];
-      const int cnt = hist[bin];
-      need -= above;
-      prefix |= (uint64_t)bin << shift;
-      mask |= dmask << shift;
-      __syncthreads();
-      if (cnt == need || shift == 0) break;
-      start = shift - 1;
-    }
-  }
-  // selected: (key & mask) > prefix, plus the `need` lowest-index keys with
-  // (key & mask) == prefix
-  int eq = 0;
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) eq += base + i < a.n && (key[i] & mask) == prefix;
-  int total;
-  int eq_before = block_excl_scan(eq, tmp, &total);
-  bool sel[KPT];
-  int cnt = 0;
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    bool valid = base + i < a.n;
-    uint64_t km = key[i] & mask;
-    bool e = valid && km == prefix;
-    sel[i] = valid && (km > prefix || (e && eq_before < need));
-    eq_before += e;
-    cnt += sel[i];
-  }
-  int pos = block_excl_scan(cnt, tmp, &total);
-  int32_t* out = a.ids + (size_t)row * a.k;
-#pragma unroll
-  for (int i = 0; i < KPT; ++i)
-    if (sel[i]) out[pos++] = base + i;
+  __shared__ TopkLds s;
+  int32_t* out = a.ids + (size_t)blockIdx.x * a.k;
+  topk_select<KPT>(a.keys + (size_t)blockIdx.x * a.n, a.n, a.k, s,
+                   [&](int pos, int idx) { out[pos] = idx; });
 }
 
 // Rows longer than 8192 keys: the same selection with keys re-read from

@@ -1,0 +1,236 @@
+// The speculative decode step in two launches on one stream.
+//
+// The reference runs select and speculate on two streams and joins them
+// before the repair (benchmarks/run_benchmark.py:99-118, overlap_run).  On
+// MI355X a captured two-stream fork/join costs more than the kernels it
+// overlaps, so this file gives the same step as:
+//   k_front        one grid whose workgroups are either scoring workgroups
+//                  (bound score of a chunk of blocks -> 64-bit keys) or
+//                  speculation workgroups (per-block softmax states of the
+//                  predicted blocks, one K/V read per KV group), the two
+//                  roles interleaved evenly over the launch order so both
+//                  streams of HBM traffic run side by side;
+//   k_topk_repair  one workgroup per query head: exact top-K of the head's
+//                  keys (written out as the selected IDs, ascending) feeding
+//                  the single-workgroup saved / union repair directly from LDS.
+// The arithmetic is that of stk_select_blocks, stk_block_partials and
+// stk_gqa_repair; results are identical up to FP32 reduction order.
+#include "score.hpp"
+#include "topk.hpp"
+#include "states_tok.hpp"
+#include "gqa_repair.hpp"
+#include "api.hpp"
+
+namespace stk {
+
+struct FrontArgs {
+  ScoreArgs sc;
+  StatesArgs st;
+  int score_wgs, total_wgs;
+};
+
+template <typename T, int NCH, int UP, int P, int STEPS, int GT, bool GROUP>
+__global__ __launch_bounds__(256) void k_front(FrontArgs a) {
+  const int i = blockIdx.x;
+  // score workgroups among launch indices [0, i) and [0, i]
+  const int before = (int)(((int64_t)i * a.score_wgs) / a.total_wgs);
+  const int upto = (int)(((int64_t)(i + 1) * a.score_wgs) / a.total_wgs);
+  if (upto > before)
+    score_wg<T, P, STEPS, true, GT>(a.sc, before);
+  else
+    states_tok_wg<T, NCH, UP, int32_t, GROUP>(a.st, i - upto);
+}
+
+struct TailArgs {
+  GqaRepairArgs r;
+  const uint64_t* keys;
+  int n, k;
+  int32_t* ids;
+};
+
+template <class Stream, int CHUNKS, int KPT>
+__global__ __launch_bounds__(kRepairThreads) void k_topk_repair(TailArgs a) {
+  extern __shared__ int lds_i[];
+  __shared__ TopkLds tl;
+  __shared__ int tmp[kRepairWaves];
+  __shared__ float wm[kRepairWaves], wl[kRepairWaves];
+  const int h = blockIdx.x;
+  const bool use_map = a.r.kv.n <= kRepairMapN;
+  int* ids = lds_i + (use_map ? a.r.kv.n : a.r.sp);
+  int32_t* out = a.ids + (size_t)h * a.k;
+  topk_select<KPT>(a.keys + (size_t)h * a.n, a.n, a.k, tl, [&](int pos, int idx) {
+    ids[pos] = idx;
+    out[pos] = idx;
+  });
+  gqa_repair_head<Stream, CHUNKS, true>(a.r, h, lds_i, tmp, wm, wl, true);
+}
+
+}  // namespace stk
+
+using namespace stk;
+
+namespace {
+
+struct StepShape {
+  int nch, passes, steps, gt, kpt, up;
+  bool group;
+};
+
+// Shape plan of the fused step, or a message saying why it is not supported.
+const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
+                      int pred_dtype, uintptr_t align, StepShape* s) {
+  if (dtype != DT_BF16 && dtype != DT_F16) return "the fused step takes bf16 or fp16 Q/K/V";
+  if (pred_dtype != IT_I32) return "the fused step takes int32 predicted IDs";
+  s->nch = tok_nch(dtype, d, align);
+  if (!s->nch) return "the fused step needs D in {64, 128, 256} and 16-byte aligned Q/K/V";
+  if (n > 8192) return "the fused step supports at most 8192 blocks";
+  if (topk < 1 || topk > n || topk > kMaxIds || sp < 1 || sp > kMaxIds)
+    return "bad topk or predicted width";
+  const int G = hq / hkv;
+  if (G > 64 || (G > 1 && G * sp > 4 * STK_WAVE))
+    return "the fused step needs (Hq/Hkv) * SP <= 256";
+  s->passes = d / 64;
+  s->steps = s->passes <= 2 ? 2 : 1;
+  s->group = G > 1;
+  s->gt = G == 1 ? 1 : (G == 2 ? 2 : (s->passes <= 2 ? 4 : 2));
+  if (s->passes > 2 && s->gt > 2) s->gt = 2;
+  s->kpt = n <= kRepairThreads * 4 ? 4 : 16;
+  s->up = b <= 16 ? 1 : 2;
+  if (gqa_repair_lds(n, topk, sp, d) > 64 * 1024) return "repair scratch exceeds 64 KiB of LDS";
+  return nullptr;
+}
+
+template <typename T, int NCH, int UP, int P, int STEPS>
+int launch_front_gt(const FrontArgs& f, const StepShape& s, hipStream_t st) {
+  const dim3 grid(f.total_wgs), block(256);
+  if (!s.group)
+    hipLaunchKernelGGL((k_front<T, NCH, UP, P, STEPS, 1, false>), grid, block, 0, st, f);
+  else if (s.gt == 2)
+    hipLaunchKernelGGL((k_front<T, NCH, UP, P, STEPS, 2, true>), grid, block, 0, st, f);
+  else
+    hipLaunchKernelGGL((k_front<T, NCH, UP, P, STEPS, 4, true>), grid, block, 0, st, f);
+  return stk_check_launch("k_front");
+}
+
+template <typename T, int NCH, int UP>
+int launch_tail(const TailArgs& t, const StepShape& s, size_t lds, hipStream_t st) {
+  const dim3 grid(t.r.kv.hq), block(kRepairThreads);
+  constexpr int CH = NCH * 16 / (int)sizeof(T) * 4 <= 128 ? 1 : 2;   // D <= 128 ?
+  if (s.kpt == 4)
+    hipLaunchKernelGGL((k_topk_repair<TokStream<T, NCH, UP>, CH, 4>), grid, block, lds, st, t);
+  else
+    hipLaunchKernelGGL((k_topk_repair<TokStream<T, NCH, UP>, CH, 16>), grid, block, lds, st, t);
+  return stk_check_launch("k_topk_repair");
+}
+
+template <typename T, int NCH>
+int launch_step(const FrontArgs& f, const TailArgs& t, const StepShape& s, size_t lds,
+                hipStream_t st, bool front, bool tail) {
+  constexpr int P = NCH * 16 / (int)sizeof(T) * 4 / 64;   // D / 64
+  constexpr int STEPS = P <= 2 ? 2 : 1;
+  if (front) {
+    int rc = s.up == 1 ? launch_front_gt<T, NCH, 1, P, STEPS>(f, s, st)
+                       : launch_front_gt<T, NCH, 2, P, STEPS>(f, s, st);
+    if (rc) return rc;
+  }
+  if (!tail) return STK_OK;
+  return s.up == 1 ? launch_tail<T, NCH, 1>(t, s, lds, st) : launch_tail<T, NCH, 2>(t, s, lds, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+STK_API size_t stk_step_workspace_bytes(int hq, int hkv, int n, int d, int topk) {
+  (void)hkv; (void)d; (void)topk;
+  if (hq <= 0 || n <= 0) return 0;
+  return stk_align((size_t)hq * n * sizeof(uint64_t));
+}
+
+STK_API int stk_step_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
+                               int pred_dtype) {
+  StepShape s{};
+  if (hq <= 0 || hkv <= 0 || hq % hkv) return 0;
+  return plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, 0, &s) == nullptr;
+}
+
+static int step_call(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                     int n, int b, int d, const float* lo, const float* hi, int topk,
+                     const void* predicted, int pred_dtype, int sp, int union_mode,
+                     int32_t* selected, float* m, float* l, float* u, float* out,
+                     void* workspace, size_t workspace_bytes, void* stream, bool front,
+                     bool tail) {
+  STK_REQUIRE(stk_check_kv(dtype, hq, hkv, n, b, d));
+  STK_REQUIRE(q && k && v && predicted && m && l && u, "null pointer");
+  STK_REQUIRE(!front || (lo && hi), "null pointer");
+  STK_REQUIRE(!tail || (selected && out), "null pointer");
+  STK_REQUIRE(workspace && workspace_bytes >= stk_step_workspace_bytes(hq, hkv, n, d, topk),
+              "workspace too small");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(u) |
+                          (front ? reinterpret_cast<uintptr_t>(lo) | reinterpret_cast<uintptr_t>(hi)
+                                 : 0);
+  StepShape s{};
+  const char* why = plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, align, &s);
+  STK_REQUIRE(why == nullptr, why ? why : "");
+  uint64_t* keys = static_cast<uint64_t*>(workspace);
+  FrontArgs f{};
+  f.sc.q = q; f.sc.qtype = dtype; f.sc.lo = lo; f.sc.hi = hi;
+  f.sc.hq = hq; f.sc.hkv = hkv; f.sc.n = n; f.sc.d = d;
+  f.sc.scores = nullptr; f.sc.keys = keys;
+  f.sc.chunks = (n + kScoreWaves * 4 * s.steps - 1) / (kScoreWaves * 4 * s.steps);
+  f.st.q = q; f.st.k = k; f.st.v = v; f.st.ids = predicted; f.st.itype = IT_I32;
+  f.st.hq = hq; f.st.hkv = hkv; f.st.n = n; f.st.b = b; f.st.d = d; f.st.s = sp;
+  f.st.m = m; f.st.l = l; f.st.u = u;
+  f.score_wgs = hkv * f.sc.chunks;
+  f.total_wgs = f.score_wgs + (int)(((int64_t)hq * sp + 3) / 4);
+  TailArgs t{};
+  t.r.kv = KV{q, k, v, hq, hkv, n, b, d};
+  t.r.a = selected; t.r.atype = IT_I32; t.r.sa = topk;
+  t.r.p = predicted; t.r.ptype = IT_I32; t.r.sp = sp;
+  t.r.pm = m; t.r.pl = l; t.r.pu = u; t.r.uni = union_mode ? 1 : 0; t.r.out = out;
+  t.keys = keys; t.n = n; t.k = topk; t.ids = selected;
+  const size_t lds = gqa_repair_lds(n, topk, sp, d);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DT_BF16) {
+    if (s.nch == 2) return launch_step<bf16s, 2>(f, t, s, lds, st, front, tail);
+    if (s.nch == 4) return launch_step<bf16s, 4>(f, t, s, lds, st, front, tail);
+    return launch_step<bf16s, 8>(f, t, s, lds, st, front, tail);
+  }
+  if (s.nch == 2) return launch_step<f16s, 2>(f, t, s, lds, st, front, tail);
+  if (s.nch == 4) return launch_step<f16s, 4>(f, t, s, lds, st, front, tail);
+  return launch_step<f16s, 8>(f, t, s, lds, st, front, tail);
+}
+
+STK_API int stk_speculative_step(const void* q, const void* k, const void* v, int dtype, int hq,
+                                 int hkv, int n, int b, int d, const float* lo, const float* hi,
+                                 int topk, const void* predicted, int pred_dtype, int sp,
+                                 int union_mode, int32_t* selected, float* m, float* l, float* u,
+                                 float* out, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, topk, predicted, pred_dtype, sp,
+                   union_mode, selected, m, l, u, out, workspace, workspace_bytes, stream, true,
+                   true);
+}
+
+STK_API int stk_step_front(const void* q, const void* k, const void* v, int dtype, int hq,
+                           int hkv, int n, int b, int d, const float* lo, const float* hi,
+                           int topk, const void* predicted, int pred_dtype, int sp, float* m,
+                           float* l, float* u, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, topk, predicted, pred_dtype, sp, 0,
+                   nullptr, m, l, u, nullptr, workspace, workspace_bytes, stream, true, false);
+}
+
+STK_API int stk_step_tail(const void* q, const void* k, const void* v, int dtype, int hq,
+                          int hkv, int n, int b, int d, int topk, const void* predicted,
+                          int pred_dtype, int sp, int union_mode, const float* m, const float* l,
+                          const float* u, int32_t* selected, float* out, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  return step_call(q, k, v, dtype, hq, hkv, n, b, d, nullptr, nullptr, topk, predicted,
+                   pred_dtype, sp, union_mode, selected, const_cast<float*>(m),
+                   const_cast<float*>(l), const_cast<float*>(u), out, workspace,
+                   workspace_bytes, stream, false, true);
+}
+
+}  // extern "C"

@@ -24,6 +24,7 @@ import numpy as np
 import torch
 
 from strict_topk import gqa, gqa_light
+from strict_topk import step as step_mod
 
 from .configs import CONFIGS, make_qkv, perturb
 from .timing import overlap_run
@@ -97,14 +98,22 @@ def byte_model(cfg, selected, predicted, elem_bytes):
 
 
 class GqaStep:
-    """c2 / c3: gqa.select_blocks || gqa.partials -> saved repair."""
+    """c2 / c3: gqa.select_blocks || gqa.partials -> saved repair.
 
-    def __init__(self, cfg, overlap, seed, device, repair="auto"):
+    ``sets`` device copies of (q, k, v, lo, hi) hold identical values at
+    different addresses; step i of a captured sequence uses copy i % sets, so
+    that a sequence larger than the caches (MI355X: 4 MB L2 per XCD, 256 MB
+    Infinity Cache) reads its operands from HBM as a real decode loop does.
+    """
+
+    def __init__(self, cfg, overlap, seed, device, repair="auto", sets=1):
         self.cfg, self.overlap, self.seed = cfg, overlap, seed
         q, k, v, lo, hi = make_qkv(cfg.hq, cfg.hkv, cfg.dim, cfg.block, cfg.blocks, cfg.dtype,
                                    cfg.hot, seed)
         self.host = (q, k, v, lo, hi)
-        self.q, self.k, self.v, self.lo, self.hi = (t.to(device) for t in (q, k, v, lo, hi))
+        first = tuple(t.to(device) for t in (q, k, v, lo, hi))
+        self.sets = [first] + [tuple(t.clone() for t in first) for _ in range(sets - 1)]
+        self.q, self.k, self.v, self.lo, self.hi = first
         self.selected = gqa.select_blocks(self.q, self.lo, self.hi, cfg.topk)
         self.predicted = perturb(self.selected.cpu(), cfg.blocks, cfg.sp, overlap, seed).to(device)
         self.emf = 1.0 - overlap
@@ -113,32 +122,50 @@ class GqaStep:
         self.ps = torch.cuda.Stream()
         torch.cuda.synchronize()
 
-    # -- phases
-    def select(self):
-        return gqa.select_blocks(self.q, self.lo, self.hi, self.cfg.topk)
+    # -- phases on input copy i
+    def select(self, i=0):
+        q, k, v, lo, hi = self.sets[i % len(self.sets)]
+        return gqa.select_blocks(q, lo, hi, self.cfg.topk)
 
-    def speculate(self):
-        return gqa.partials(self.q, self.k, self.v, self.predicted)
+    def speculate(self, i=0):
+        q, k, v, lo, hi = self.sets[i % len(self.sets)]
+        return gqa.partials(q, k, v, self.predicted)
 
-    def finish(self, a, state):
+    def finish(self, a, state, i=0):
+        q, k, v, lo, hi = self.sets[i % len(self.sets)]
         if self.repair == "light":
-            return gqa_light.repair_saved_light(self.q, self.k, self.v, a, self.predicted, state)
+            return gqa_light.repair_saved_light(q, k, v, a, self.predicted, state)
         if self.repair == "saved":
-            return gqa.repair_saved(self.q, self.k, self.v, a, self.predicted, state)
-        return gqa_light.repair_saved_auto(self.q, self.k, self.v, a, self.predicted, state,
-                                           self.emf)
+            return gqa.repair_saved(q, k, v, a, self.predicted, state)
+        return gqa_light.repair_saved_auto(q, k, v, a, self.predicted, state, self.emf)
 
-    # -- whole steps
-    def full(self):
-        return overlap_run(self.select, self.speculate, self.finish, self.ss, self.ps)
+    # -- whole steps on input copy i
+    def full(self, i=0):
+        """The drop-in composition: overlap_run over two side streams."""
+        return overlap_run(lambda: self.select(i), lambda: self.speculate(i),
+                           lambda a, st: self.finish(a, st, i), self.ss, self.ps)
 
-    def serial(self):
-        return gqa.exact(self.q, self.k, self.v, self.select())
+    def fused(self, i=0):
+        """The same step in two launches on one stream (strict_topk.step)."""
+        q, k, v, lo, hi = self.sets[i % len(self.sets)]
+        return step_mod.speculative_step(q, k, v, lo, hi, self.predicted, self.cfg.topk).output
+
+    def serial(self, i=0):
+        q, k, v, lo, hi = self.sets[i % len(self.sets)]
+        return gqa.exact(q, k, v, self.select(i))
 
     def bytes(self):
         e = torch.tensor([], dtype=self.cfg.dtype).element_size()
         return byte_model(self.cfg, self.selected.cpu().numpy(), self.predicted.cpu().numpy(), e)
 
+    def front_bytes(self):
+        """Algorithmic bytes of the select || speculate launch (k_front)."""
+        by = self.bytes()
+        c = self.cfg
+        e = torch.tensor([], dtype=c.dtype).element_size()
+        return (by.meta + by.kv_spec + c.hq * c.sp * 4 * (c.dim + 2) + c.hq * c.blocks * 8
+                + c.hq * c.dim * e + c.hq * c.sp * 4)
 
-def gqa_step(name="c3", overlap=0.9, seed=20261103, device="cuda", repair="auto"):
-    return GqaStep(CONFIGS[name], overlap, seed, device, repair)
+
+def gqa_step(name="c3", overlap=0.9, seed=20261103, device="cuda", repair="auto", sets=1):
+    return GqaStep(CONFIGS[name], overlap, seed, device, repair, sets)

@@ -55,6 +55,12 @@ _SIGS = {
     "stk_hier_exact": (I, [P, P, P, I, I, I, I, I, I, P, I, I, P, P, Z, P]),
     "stk_hier_repair_workspace_bytes": (Z, [I, I, I, I]),
     "stk_hier_repair": (I, [P, P, P, I, I, I, I, I, I, P, I, I, P, I, I, P, P, P, I, P, P, Z, P]),
+    "stk_step_workspace_bytes": (Z, [I, I, I, I, I]),
+    "stk_step_supported": (I, [I, I, I, I, I, I, I, I, I]),
+    "stk_speculative_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I,
+                                 P, P, P, P, P, P, Z, P]),
+    "stk_step_front": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, P, P, P, P, Z, P]),
+    "stk_step_tail": (I, [P, P, P, I, I, I, I, I, I, I, P, I, I, I, P, P, P, P, P, P, Z, P]),
 }
 
 EXPORTS = tuple(_SIGS)

@@ -3,8 +3,8 @@
 Drop-in for the reference ``strict_topk/selector.py`` (same names, argument
 meaning and ValueError messages, :23-43).  Scores are evaluated in FP64 on the
 GPU (exact products, fixed summation order) and returned as FP32; selection
-is exact top-K with ties toward the lower block index, emitted in
-(score desc, index asc) order — one valid instance of the reference's
+is exact top-K with ties toward the lower block index, emitted in ascending
+block order -- one valid instance of the reference's
 ``torch.topk(sorted=False)`` result, whose order is unspecified.
 """
 import torch

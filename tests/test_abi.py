@@ -1,0 +1,61 @@
+"""The C ABI: every function declared in include/strict_topk.h is exported by
+the built library and bound by strict_topk/_lib.py with the same arity.
+No GPU is needed (only symbol lookup and host-only queries are called)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "strict_topk.h"
+
+
+def _declarations():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(?:const\s+)?[a-z_0-9]+\s*\*?\s*(stk_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        args = m.group(2).strip()
+        decls[m.group(1)] = 0 if args in ("", "void") else len(args.split(","))
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from strict_topk import _lib
+    if not _lib._PATH.exists():
+        import build_lib
+        build_lib.build()
+    return _lib
+
+
+def test_header_declares_the_abi():
+    decls = _declarations()
+    assert len(decls) >= 25
+    assert "stk_speculative_step" in decls and "stk_select_blocks" in decls
+
+
+def test_every_declared_symbol_is_exported(lib):
+    handle = ctypes.CDLL(str(lib._PATH))
+    missing = [name for name in _declarations() if not hasattr(handle, name)]
+    assert not missing, missing
+
+
+def test_binding_matches_header(lib):
+    decls = _declarations()
+    assert set(lib._SIGS) == set(decls)
+    for name, nargs in decls.items():
+        assert len(lib._SIGS[name][1]) == nargs, name
+
+
+def test_host_only_queries(lib):
+    L = lib.lib()
+    assert L.stk_abi_version() == 1
+    assert L.stk_step_supported(2, 32, 8, 2048, 32, 128, 64, 64, 0) == 1
+    assert L.stk_step_supported(0, 32, 8, 2048, 32, 128, 64, 64, 0) == 0   # fp32
+    assert L.stk_step_supported(2, 32, 8, 2048, 32, 96, 64, 64, 0) == 0    # D = 96
+    assert lib.size("stk_select_workspace_bytes", 32, 8, 2048, 128, 64) >= 32 * 2048 * 8
+    # argument errors are reported without touching a device
+    rc = L.stk_block_scores(None, 2, None, None, 4, 3, 10, 8, None, None)
+    assert rc == -1 and b"divisible" in L.stk_last_error()

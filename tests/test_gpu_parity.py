@@ -463,3 +463,55 @@ def test_touch_kv_checksums():
     got = touch_kv(*dev(k, v, p))
     assert got.shape == ref.shape
     np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-4, atol=1e-3)
+
+
+# ------------------------------------------------------- fused decode step
+@pytest.mark.parametrize("hq,hkv,n,b,d,topk,overlap,dtype,union", [
+    (32, 8, 2048, 32, 128, 64, 0.9, torch.bfloat16, False),   # c3 shape
+    (16, 8, 512, 32, 128, 64, 0.9, torch.bfloat16, True),     # c2 shape, union repair
+    (4, 4, 64, 32, 64, 8, 0.75, torch.float16, False),        # c1 shape (G = 1)
+    (8, 4, 300, 16, 256, 40, 0.5, torch.bfloat16, False),     # D = 256, one-pass tiles
+    (6, 3, 5000, 32, 128, 80, 1.0, torch.float16, False),     # long rows, all hits
+    (12, 1, 700, 8, 64, 20, 0.0, torch.bfloat16, False),      # G = 12, no hits
+])
+def test_speculative_step(hq, hkv, n, b, d, topk, overlap, dtype, union):
+    """speculative_step: selected IDs bit-exact, prediction states and the
+    strict (or union) output against the oracle on the same inputs."""
+    from stk_harness.configs import make_qkv, perturb
+    from strict_topk import step
+    q, k, v, lo, hi = make_qkv(hq, hkv, d, b, n, dtype, True, 20261103 + n)
+    qn, kn, vn = np_(q, k, v)
+    ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), topk)
+    p = perturb(torch.from_numpy(ref_ids), n, topk, overlap, 7)
+    pn = p.numpy().astype(np.int64)
+    qd, kd, vd, lod, hid, pd = dev(q, k, v, lo, hi, p)
+    assert step.supported(qd, kd, lod, topk, pd)
+    res = step.speculative_step(qd, kd, vd, lod, hid, pd, topk, union=union)
+    assert res.selected.cpu().numpy().tolist() == ref_ids.tolist()
+    st = O.block_states(qn, kn, vn, pn)
+    np.testing.assert_allclose(res.state.m.cpu().double().numpy(), st.m, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(res.state.l.cpu().double().numpy(), st.l, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(res.state.u.cpu().double().numpy(), st.u, rtol=1e-4, atol=1e-4)
+    if union:
+        expected = O.gqa_repair(qn, kn, vn, ref_ids, pn, st, union=True)
+    else:
+        expected = O.attention(qn, kn, vn, ref_ids)
+    check(res.output, expected, ("step", hq, n, union))
+
+
+def test_speculative_step_composed_fallback():
+    """fp32 inputs and int64 predictions run through the individual kernels."""
+    from strict_topk import step
+    gen = torch.Generator().manual_seed(9)
+    q = torch.randn((4, 48), generator=gen)
+    k = torch.randn((2, 30, 8, 48), generator=gen)
+    v = torch.randn(k.shape, generator=gen)
+    lo, hi = k.amin(2), k.amax(2)
+    p = torch.stack([torch.randperm(30, generator=gen)[:6] for _ in range(4)])
+    qn, kn, vn = np_(q, k, v)
+    ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), 6)
+    qd, kd, vd, lod, hid, pd = dev(q, k, v, lo, hi, p)
+    assert not step.supported(qd, kd, lod, 6, pd)
+    res = step.speculative_step(qd, kd, vd, lod, hid, pd, 6)
+    assert res.selected.cpu().numpy().tolist() == ref_ids.tolist()
+    check(res.output, O.attention(qn, kn, vn, ref_ids), "composed step")
