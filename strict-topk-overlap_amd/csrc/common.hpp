@@ -100,6 +100,58 @@ __device__ __forceinline__ int64_t ld_id(const void* ids, int64_t i) {
   return (int64_t) reinterpret_cast<const I*>(ids)[i];
 }
 
+// ------------------------------------------------------ DPP lane exchange
+// Cross-lane moves through the VALU's data-parallel-primitive modifier
+// (no LDS round trip).  Controls (GFX9 encoding): quad_perm [1,0,3,2] =
+// 0xB1 (xor 1), [2,3,0,1] = 0x4E (xor 2), row_ror:r = 0x120 + r (rotate
+// inside each 16-lane row), row_half_mirror = 0x141 (within 8 lanes,
+// i <-> 7-i), row_mirror = 0x140 (within 16 lanes, i <-> 15-i),
+// row_bcast15 = 0x142, row_bcast31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, v), CTRL,
+                                                               ROW_MASK, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  uint64_t b = (uint64_t)__double_as_longlong(v);
+  int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xf, 0xf, false);
+  int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
+  return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
+// Sum over the 4 lanes of a quad, result in all 4 lanes.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp<0xB1>(0.f, v);
+  v += dpp<0x4E>(0.f, v);
+  return v;
+}
+
+// Maximum over the whole wave, returned wave-uniform.  (Quads, half rows and
+// rows by permutation; rows 1 and 3, then 2 and 3, by row broadcast; lane 63
+// ends with the total.)
+__device__ __forceinline__ float wave_max_u(float v) {
+  v = fmaxf(v, dpp<0xB1>(v, v));
+  v = fmaxf(v, dpp<0x4E>(v, v));
+  v = fmaxf(v, dpp<0x141>(v, v));
+  v = fmaxf(v, dpp<0x140>(v, v));
+  v = fmaxf(v, dpp<0x142, 0xa>(v, v));
+  v = fmaxf(v, dpp<0x143, 0xc>(v, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Sum over the whole wave, returned wave-uniform (same pattern).
+__device__ __forceinline__ float wave_sum_u(float v) {
+  v += dpp<0xB1>(0.f, v);
+  v += dpp<0x4E>(0.f, v);
+  v += dpp<0x141>(0.f, v);
+  v += dpp<0x140>(0.f, v);
+  v += dpp<0x142, 0xa>(0.f, v);
+  v += dpp<0x143, 0xc>(0.f, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // ---------------------------------------------------------------- wave ops
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (STK_WAVE - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / STK_WAVE; }

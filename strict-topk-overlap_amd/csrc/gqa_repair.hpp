@@ -179,7 +179,7 @@ struct TokStream {
     int cur_id = x < count ? list[x] : 0;
     {
       size_t off = (((size_t)kv * n + cur_id) * B) * d;
-      t.load(K + off, V + off, 0, B, kw, vw);
+      t.load(K + off, V + off, 0, kw, vw);
     }
     for (int t0 = 0; x < count;) {
       int nt0 = t0 + TT::CH;
@@ -193,7 +193,7 @@ struct TokStream {
       const int lt0 = have_next ? nt0 : t0;
       size_t noff = (((size_t)kv * n + nid) * B) * d;
       uint32_t kn[UP][TT::QW], vn[TT::CH][TT::VW];
-      t.load(K + noff, V + noff, lt0, B, kn, vn);
+      t.load(K + noff, V + noff, lt0, kn, vn);
       t.template update<false, false>(qw, kw, vw, t0, B, scale, m, l, acc);
 #pragma unroll
       for (int u = 0; u < UP; ++u)

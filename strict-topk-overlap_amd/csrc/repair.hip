@@ -554,11 +554,11 @@ static int launch_gqa_repair(const GqaRepairArgs& g, int dtype, hipStream_t st) 
   const bool vrow = d % 8 == 0 && (reinterpret_cast<uintptr_t>(g.pu) & 15) == 0;
   const uintptr_t align = reinterpret_cast<uintptr_t>(g.kv.q) | reinterpret_cast<uintptr_t>(g.kv.k) |
                           reinterpret_cast<uintptr_t>(g.kv.v);
-  const int nch = tok_nch(dtype, d, align);
+  const int nch = tok_nch(dtype, d, g.kv.b, align);
   const dim3 grid(g.kv.hq), block(kRepairThreads);
   if (nch) {
     // d is 64, 128 or 256 here
-    const bool one = g.kv.b <= 16;
+    const bool one = tok_up(g.kv.b) == 1;
 #define STK_REPAIR_TOK(UPV)                                                                           \
     STK_DISPATCH_TOK(dtype, nch, {                                                                    \
       if (d <= 128 && vrow)                                                                           \

@@ -3,10 +3,26 @@
 // Reference: strict_topk/selector.py:8-20 (_score) and strict_topk/gqa.py:15-26
 // (_bound_score): score[h,n] = sum_d q_d * (q_d >= 0 ? hi : lo)[h/G, n, d].
 // Evaluated in FP64: products of a 16/32-bit q and an FP32 bound are exact;
-// 16 lanes share a block, lane c summing dims 64*j + 4*c + t (j ascending,
-// t = 0..3) from +0.0, then an xor butterfly (8, 4, 2, 1) combines the lanes.
-// A workgroup (4 waves) covers 16 * STEPS consecutive blocks of one KV head
-// for all G query heads of that head, so lo/hi are read once per KV head.
+// 16 logical lanes share a block, lane c summing dims 64*j + 4*c + t
+// (j ascending, t = 0..3) from +0.0, then an xor butterfly (8, 4, 2, 1)
+// combines the lanes.  A workgroup (4 waves) covers 16 * STEPS consecutive
+// blocks of one KV head for all G query heads of that head, so lo/hi are
+// read once per KV head.
+//
+// Instruction budget (the scorer is VALU-limited once lo/hi arrive):
+//   * the query heads' values are converted to FP64 once per workgroup and
+//     staged in LDS with a select mask (all ones where q < 0 or q is NaN);
+//   * each (head, dim, block) costs one bit-select of lo/hi, one FP32->FP64
+//     conversion and one FP64 FMA;
+//   * the 16-lane sums of all C = GT * STEPS (head, block) pairs of a wave
+//     share one transposed reduction: at each of the first log2(C) levels a
+//     lane keeps half of its pairs and adds its partner's copy of that half,
+//     so the exchanges fall from 4 * C to about C.  Every exchange is a
+//     single DPP move: physical lanes are permuted (score_lane) so that the
+//     half-row mirror (physical xor 7) is logical xor 4; rotation by 8
+//     inside a row is xor 8; quad permutations are xor 2 and xor 1.  Each
+//     partial is the sum of the same two operands as in the butterfly, so
+//     the bits are those of the contract.
 #pragma once
 
 #include "attn.hpp"
@@ -33,48 +49,98 @@ struct ScoreArgs {
   uint64_t* keys;        // optional [hq, n]
 };
 
-template <typename Q>
-__device__ __forceinline__ float qval(const void* q, int64_t i) {
-  return cvt(reinterpret_cast<const Q*>(q)[i]);
+// Physical lane (0..15 inside a row) -> logical lane of the summation order.
+__device__ __forceinline__ int score_lane(int l16) { return l16 ^ ((l16 & 4) ? 3 : 0); }
+
+// A DPP move of a double whose pattern reads a valid lane for every lane.
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_d(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)b, CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
+  return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
+// One halving level: keep values [0, N/2) (up = false) or [N/2, N) (up =
+// true) in slots [0, N/2), adding the partner's copy of the same half.
+template <int N, int CTRL>
+__device__ __forceinline__ void score_halve(double* v, bool up) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const double keep = up ? v[N / 2 + i] : v[i];
+    const double send = up ? v[i] : v[N / 2 + i];
+    v[i] = keep + dpp_mov_d<CTRL>(send);
+  }
+}
+
+// Sums over the 16 lanes of each row of C values per lane (C in 1, 2, 4, 8).
+// Returns, in physical lane l16, the total of value index l16 >> (4 - log2 C).
+template <int C>
+__device__ __forceinline__ double score_rowsum(double (&v)[C], int l16) {
+  static_assert(C == 1 || C == 2 || C == 4 || C == 8, "1, 2, 4 or 8 sums per lane");
+  if constexpr (C == 8) {
+    score_halve<8, 0x128>(v, l16 & 8);
+    score_halve<4, 0x141>(v, l16 & 4);
+    score_halve<2, 0x4E>(v, l16 & 2);
+    return v[0] + dpp_mov_d<0xB1>(v[0]);
+  } else if constexpr (C == 4) {
+    score_halve<4, 0x128>(v, l16 & 8);
+    score_halve<2, 0x141>(v, l16 & 4);
+    double r = v[0] + dpp_mov_d<0x4E>(v[0]);
+    return r + dpp_mov_d<0xB1>(r);
+  } else if constexpr (C == 2) {
+    score_halve<2, 0x128>(v, l16 & 8);
+    double r = v[0] + dpp_mov_d<0x141>(v[0]);
+    r = r + dpp_mov_d<0x4E>(r);
+    return r + dpp_mov_d<0xB1>(r);
+  } else {
+    double r = v[0] + dpp_mov_d<0x128>(v[0]);
+    r = r + dpp_mov_d<0x141>(r);
+    r = r + dpp_mov_d<0x4E>(r);
+    return r + dpp_mov_d<0xB1>(r);
+  }
 }
 
 // P = 64-dim passes (D <= 64 * P), STEPS = 4-block wave steps per wave,
-// GT = query heads whose rows are held in registers at a time.
-template <typename Q, int P, int STEPS, bool VEC4, int GT>
+// GT = query heads per LDS stage.  FULL: D % 64 == 0 and q, lo, hi 16-byte
+// aligned (whole passes, vector loads); otherwise dims past D are zeroed
+// element by element.
+template <typename Q, int P, int STEPS, bool FULL, int GT>
 __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg) {
+  constexpr int C = GT * STEPS;           // (head, block) sums per wave
+  constexpr int QN = GT * 64 * P;         // staged query values
+  __shared__ __align__(16) double s_q[QN];
+  __shared__ __align__(16) uint32_t s_m[QN];
   const int G = a.hq / a.hkv;
   const int kv = wg / a.chunks;
   const int chunk = wg % a.chunks;
   const int h0 = kv * G;
   const int lane = lane_id();
-  const int lane16 = lane & 15;
+  const int l16 = lane & 15;
+  const int c = score_lane(l16);              // logical lane
   const int sub = lane >> 4;                  // block within a 4-block step
   const int wave_base = (chunk * kScoreWaves + wave_id()) * (4 * STEPS);
-  const Q* qrow = reinterpret_cast<const Q*>(a.q) + (size_t)h0 * a.d;
-  // every load of the wave is issued before any arithmetic, with no branch
-  // around a load: out-of-range blocks, dims and heads read a valid address
-  // and are zeroed
+  // every lo/hi load of the wave is issued before any arithmetic, with no
+  // branch around a load: blocks past n read row 0 and are not stored
   float4 lv[STEPS][P], hv[STEPS][P];
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
-    int nb = wave_base + 4 * s + sub;
-    bool valid = nb < a.n;
+    const int nb = wave_base + 4 * s + sub;
+    const bool valid = nb < a.n;
     const float* lrow = a.lo + ((size_t)kv * a.n + (valid ? nb : 0)) * a.d;
     const float* hrow = a.hi + ((size_t)kv * a.n + (valid ? nb : 0)) * a.d;
 #pragma unroll
     for (int j = 0; j < P; ++j) {
-      int d0 = 64 * j + 4 * lane16;
-      if constexpr (VEC4) {
-        bool ok = valid && d0 < a.d;
-        float4 l4 = *reinterpret_cast<const float4*>(lrow + (ok ? d0 : 0));
-        float4 h4 = *reinterpret_cast<const float4*>(hrow + (ok ? d0 : 0));
-        lv[s][j] = ok ? l4 : make_float4(0.f, 0.f, 0.f, 0.f);
-        hv[s][j] = ok ? h4 : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int d0 = 64 * j + 4 * c;
+      if constexpr (FULL) {
+        const int dd = 64 * j < a.d ? d0 : 0;   // passes past D: unused
+        lv[s][j] = *reinterpret_cast<const float4*>(lrow + dd);
+        hv[s][j] = *reinterpret_cast<const float4*>(hrow + dd);
       } else {
         float l4[4], h4[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          bool ok = valid && d0 + t < a.d;
+          const bool ok = d0 + t < a.d;
           l4[t] = ld_or(lrow, (int64_t)(d0 + t), ok, 0.f);
           h4[t] = ld_or(hrow, (int64_t)(d0 + t), ok, 0.f);
         }
@@ -83,64 +149,58 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg) {
       }
     }
   }
+  const Q* qbase = reinterpret_cast<const Q*>(a.q) + (size_t)h0 * a.d;
   for (int gb = 0; gb < G; gb += GT) {
-    // query values of heads gb .. gb+GT-1 at this lane's dims, as doubles
-    double qd[GT][P][4];
+    if (gb) __syncthreads();   // previous stage fully read
+    for (int x = threadIdx.x; x < QN; x += blockDim.x) {
+      const int gi = x / (64 * P), dim = x % (64 * P);
+      const bool ok = gb + gi < G && dim < a.d;
+      const float qv = ok ? cvt(qbase[(size_t)(gb + gi) * a.d + dim]) : 0.f;
+      s_q[x] = (double)qv;
+      s_m[x] = qv >= 0.f ? 0u : ~0u;   // lo where q < 0 or q is NaN
+    }
+    __syncthreads();
+    double acc[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) acc[i] = 0.0;
 #pragma unroll
     for (int gi = 0; gi < GT; ++gi) {
-      const bool hv_ok = gb + gi < G;
-      const Q* qg = qrow + (size_t)(hv_ok ? gb + gi : 0) * a.d;
 #pragma unroll
       for (int j = 0; j < P; ++j) {
-        int d0 = 64 * j + 4 * lane16;
-        if constexpr (VEC4) {
-          // four consecutive elements in one 8- or 16-byte access
-          bool ok = hv_ok && d0 < a.d;
-          Raw<Q, 4> r;
-          r.load(qg + (ok ? d0 : 0));
+        if (FULL && 64 * j >= a.d) continue;
+        const int x = gi * 64 * P + 64 * j + 4 * c;
+        const double2 q01 = *reinterpret_cast<const double2*>(s_q + x);
+        const double2 q23 = *reinterpret_cast<const double2*>(s_q + x + 2);
+        const uint4 mk = *reinterpret_cast<const uint4*>(s_m + x);
+        const double qd[4] = {q01.x, q01.y, q23.x, q23.y};
+        const uint32_t mm[4] = {mk.x, mk.y, mk.z, mk.w};
 #pragma unroll
-          for (int t = 0; t < 4; ++t) qd[gi][j][t] = ok ? (double)r.get(t) : 0.0;
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            bool ok = hv_ok && d0 + t < a.d;
-            float qv = cvt(qg[ok ? d0 + t : 0]);
-            qd[gi][j][t] = ok ? (double)qv : 0.0;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const int nb = wave_base + 4 * s + sub;
-#pragma unroll
-      for (int gi = 0; gi < GT; ++gi) {
-        double acc = 0.0;
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
+        for (int s = 0; s < STEPS; ++s) {
           const float lvv[4] = {lv[s][j].x, lv[s][j].y, lv[s][j].z, lv[s][j].w};
           const float hvv[4] = {hv[s][j].x, hv[s][j].y, hv[s][j].z, hv[s][j].w};
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            // a zero q (out of range) adds +0.0, which leaves the sum unchanged
-            double b = qd[gi][j][t] >= 0.0 ? (double)hvv[t] : (double)lvv[t];
-            acc = fma(qd[gi][j][t], b, acc);   // exact product, one rounding
+            const uint32_t bits = (__float_as_uint(lvv[t]) & mm[t]) |
+                                  (__float_as_uint(hvv[t]) & ~mm[t]);
+            // exact product, one rounding; a zero q (dims past D) with a zero
+            // bound adds +0.0, which leaves the sum unchanged
+            acc[gi * STEPS + s] = fma(qd[t], (double)__uint_as_float(bits), acc[gi * STEPS + s]);
           }
-        }
-        acc = acc + __shfl_xor(acc, 8);
-        acc = acc + __shfl_xor(acc, 4);
-        acc = acc + __shfl_xor(acc, 2);
-        acc = acc + __shfl_xor(acc, 1);
-        if (lane16 == 0 && nb < a.n && gb + gi < G) {
-          if (acc == 0.0) acc = 0.0;
-          size_t o = (size_t)(h0 + gb + gi) * a.n + nb;
-          if (a.scores) a.scores[o] = (float)acc;
-          if (a.keys) a.keys[o] = score_key(acc);
         }
       }
     }
+    double r = score_rowsum<C>(acc, l16);
+    constexpr int LOGC = C == 8 ? 3 : (C == 4 ? 2 : (C == 2 ? 1 : 0));
+    const int combo = l16 >> (4 - LOGC);
+    const int gi = combo / STEPS, s = combo % STEPS;
+    const int nb = wave_base + 4 * s + sub;
+    if ((l16 & ((16 >> LOGC) - 1)) == 0 && nb < a.n && gb + gi < G) {
+      if (r == 0.0) r = 0.0;
+      const size_t o = (size_t)(h0 + gb + gi) * a.n + nb;
+      if (a.scores) a.scores[o] = (float)r;
+      if (a.keys) a.keys[o] = score_key(r);
+    }
   }
 }
-
 
 }  // namespace stk

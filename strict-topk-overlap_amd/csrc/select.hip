@@ -18,7 +18,7 @@
 //               heads of that head (lo/hi read once per KV head); every lane
 //               issues all its 16-byte loads before any arithmetic.  Writes
 //               an order-preserving 64-bit key per (query head, block).
-//   k_topk   -- one 1024-thread workgroup per query head: MSB-first radix
+//   k_topk   -- one 256-thread workgroup per query head: MSB-first radix
 //               select over the row's keys held in registers (8-bit digits
 //               from the highest bit where the row's keys differ, stopping
 //               as soon as the threshold digit's bin is taken whole), then a
@@ -30,9 +30,9 @@
 namespace stk {
 
 constexpr int kTopkThreads = 256;
-template <typename Q, int P, int STEPS, bool VEC4, int GT>
+template <typename Q, int P, int STEPS, bool FULL, int GT>
 __global__ __launch_bounds__(256) void k_score(ScoreArgs a) {
-  score_wg<Q, P, STEPS, VEC4, GT>(a, blockIdx.x);
+  score_wg<Q, P, STEPS, FULL, GT>(a, blockIdx.x);
 }
 
 struct TopkArgs {
@@ -164,13 +164,12 @@ static StkCheck check_select(int q_dtype, int hq, int hkv, int n, int d) {
 template <typename Q>
 static void launch_score_q(ScoreArgs& a, hipStream_t st) {
   const int passes = (a.d + 63) / 64;
-  const bool vec4 = a.d % 4 == 0 && (reinterpret_cast<uintptr_t>(a.lo) & 15) == 0 &&
-                    (reinterpret_cast<uintptr_t>(a.hi) & 15) == 0 &&
-                    (reinterpret_cast<uintptr_t>(a.q) & (4 * sizeof(Q) - 1)) == 0;
+  const bool full = a.d % 64 == 0 && (reinterpret_cast<uintptr_t>(a.lo) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.hi) & 15) == 0;
 #define STK_SCORE(PP, SS, GG)                                                                  \
   do {                                                                                         \
     a.chunks = (a.n + kScoreWaves * 4 * SS - 1) / (kScoreWaves * 4 * SS);                       \
-    if (vec4)                                                                                  \
+    if (full)                                                                                  \
       hipLaunchKernelGGL((k_score<Q, PP, SS, true, GG>), dim3(a.hkv * a.chunks), dim3(256), 0, st, a); \
     else                                                                                       \
       hipLaunchKernelGGL((k_score<Q, PP, SS, false, GG>), dim3(a.hkv * a.chunks), dim3(256), 0, st, a); \

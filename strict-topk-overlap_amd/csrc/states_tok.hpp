@@ -8,6 +8,10 @@
 
 #include "tile2.hpp"
 
+#ifndef STK_TOK_HT
+#define STK_TOK_HT 1
+#endif
+
 namespace stk {
 
 // Map a launch-order workgroup index to a logical index so that every XCD
@@ -34,7 +38,8 @@ struct StatesArgs {
   int remap;
 };
 
-constexpr int kGrpHT = 4;   // heads sharing one loaded tile
+constexpr int kGrpHT = 4;   // heads sharing one loaded tile (generic-tile kernels)
+constexpr int kTokHT = STK_TOK_HT;   // heads per pass over a resident token tile
 
 // Token-tile states (shapes the token tile supports): one wave per
 // (query head, slot).  GROUP: the wave owning block b (no lower head of its
@@ -42,10 +47,16 @@ constexpr int kGrpHT = 4;   // heads sharing one loaded tile
 // holds b, reading the K/V tile once; non-owners return.  Otherwise each wave
 // computes its own slot, honouring the optional active mask (inactive slots
 // get (-inf, 0, 0), kernels.py:42-71).
-template <typename T, int NCH, int UP, typename I, bool GROUP>
+//
+// ONE (B == CH): the block is loaded once and stays in registers while the
+// heads are processed HT at a time; otherwise the block is streamed chunk by
+// chunk for each batch of HT heads.  HT trades registers
+// for passes: with HT = 1 the wave stays within 128 VGPRs, so four waves
+// share a SIMD.
+template <typename T, int NCH, int UP, typename I, bool GROUP, bool ONE,
+          int HT = (GROUP ? kTokHT : 1)>
 __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
   using TT = TokTile<T, NCH, UP>;
-  constexpr int HT = GROUP ? kGrpHT : 1;
   const int waves = blockDim.x / STK_WAVE;
   int64_t item = (int64_t)wg * waves + wave_id();
   if (item >= (int64_t)a.hq * a.s) return;
@@ -57,9 +68,6 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
   const int g0 = h - hl;
   int64_t bid;
   uint64_t found = 1ull << hl;
-  uint64_t pmask[HT];
-#pragma unroll
-  for (int i = 0; i < HT; ++i) pmask[i] = 0ull;
   if constexpr (GROUP) {
     // rows of the group that list b; G*S <= 256 IDs, 4 per lane, one pass
     const int total = G * a.s;
@@ -100,6 +108,8 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
   const size_t off = (((size_t)kv * a.n + (enabled ? (size_t)bid : 0)) * a.b) * a.d;
   const T* kb = reinterpret_cast<const T*>(a.k) + off;
   const T* vb = reinterpret_cast<const T*>(a.v) + off;
+  uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
+  if constexpr (ONE) t.load(kb, vb, 0, kw, vw);   // the whole block, once
   while (found) {
     int heads[HT];
     int nh = 0;
@@ -114,6 +124,7 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
       }
     }
     uint32_t qw[HT][TT::QW];
+    uint64_t pmask[HT];
     float m[HT], l[HT], acc[HT][TT::DPL];
 #pragma unroll
     for (int i = 0; i < HT; ++i) {
@@ -122,6 +133,7 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
 #pragma unroll
       for (int e = 0; e < TT::DPL; ++e) acc[i][e] = 0.f;
       t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)(g0 + heads[i]) * a.d, qw[i]);
+      pmask[i] = 0ull;
       if constexpr (GROUP) {
         // rows of at most 64 IDs: positions of b, read with the query
         bool in = lane_id() < a.s;
@@ -130,13 +142,19 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
       }
     }
     if (enabled) {
-      for (int t0 = 0; t0 < a.b; t0 += TT::CH) {
-        uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
-        t.load(kb, vb, t0, a.b, kw, vw);
+      if constexpr (ONE) {
 #pragma unroll
         for (int i = 0; i < HT; ++i)
           if (i < nh)
-            t.template update<false, false>(qw[i], kw, vw, t0, a.b, scale, m[i], l[i], acc[i]);
+            t.template update<false, false>(qw[i], kw, vw, 0, a.b, scale, m[i], l[i], acc[i]);
+      } else {
+        for (int t0 = 0; t0 < a.b; t0 += TT::CH) {
+          t.load(kb, vb, t0, kw, vw);
+#pragma unroll
+          for (int i = 0; i < HT; ++i)
+            if (i < nh)
+              t.template update<false, false>(qw[i], kw, vw, t0, a.b, scale, m[i], l[i], acc[i]);
+        }
       }
     }
 #pragma unroll

@@ -8,8 +8,8 @@
 //                  (bound score of a chunk of blocks -> 64-bit keys) or
 //                  speculation workgroups (per-block softmax states of the
 //                  predicted blocks, one K/V read per KV group), the two
-//                  roles interleaved evenly over the launch order so both
-//                  streams of HBM traffic run side by side;
+//                  roles interleaved evenly inside every XCD so both
+//                  streams of HBM traffic run side by side on all of them;
 //   k_topk_repair  one workgroup per query head: exact top-K of the head's
 //                  keys (written out as the selected IDs, ascending) feeding
 //                  the single-workgroup saved / union repair directly from LDS.
@@ -29,16 +29,20 @@ struct FrontArgs {
   int score_wgs, total_wgs;
 };
 
-template <typename T, int NCH, int UP, int P, int STEPS, int GT, bool GROUP>
-__global__ __launch_bounds__(256) void k_front(FrontArgs a) {
-  const int i = blockIdx.x;
-  // score workgroups among launch indices [0, i) and [0, i]
+template <typename T, int NCH, int UP, bool ONE, int P, int STEPS, int GT, bool GROUP>
+__global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_front(FrontArgs a) {
+  // Workgroups are dealt round-robin over the 8 XCDs; roles are interleaved
+  // on an XCD-contiguous logical index, so every XCD gets an even mix of
+  // scoring and speculation work (and, with G query heads per KV head, the
+  // scoring and the states of one KV head land on the same XCD's L2).
+  const int i = xcd_remap(blockIdx.x, gridDim.x);
+  // score workgroups among logical indices [0, i) and [0, i]
   const int before = (int)(((int64_t)i * a.score_wgs) / a.total_wgs);
   const int upto = (int)(((int64_t)(i + 1) * a.score_wgs) / a.total_wgs);
   if (upto > before)
     score_wg<T, P, STEPS, true, GT>(a.sc, before);
   else
-    states_tok_wg<T, NCH, UP, int32_t, GROUP>(a.st, i - upto);
+    states_tok_wg<T, NCH, UP, int32_t, GROUP, ONE>(a.st, i - upto);
 }
 
 struct TailArgs {
@@ -73,7 +77,7 @@ namespace {
 
 struct StepShape {
   int nch, passes, steps, gt, kpt, up;
-  bool group;
+  bool group, one;
 };
 
 // Shape plan of the fused step, or a message saying why it is not supported.
@@ -81,8 +85,9 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
                       int pred_dtype, uintptr_t align, StepShape* s) {
   if (dtype != DT_BF16 && dtype != DT_F16) return "the fused step takes bf16 or fp16 Q/K/V";
   if (pred_dtype != IT_I32) return "the fused step takes int32 predicted IDs";
-  s->nch = tok_nch(dtype, d, align);
-  if (!s->nch) return "the fused step needs D in {64, 128, 256} and 16-byte aligned Q/K/V";
+  s->nch = tok_nch(dtype, d, b, align);
+  if (!s->nch)
+    return "the fused step needs D in {64, 128, 256}, B a multiple of 16 and 16-byte aligned Q/K/V";
   if (n > 8192) return "the fused step supports at most 8192 blocks";
   if (topk < 1 || topk > n || topk > kMaxIds || sp < 1 || sp > kMaxIds)
     return "bad topk or predicted width";
@@ -95,20 +100,21 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
   s->gt = G == 1 ? 1 : (G == 2 ? 2 : (s->passes <= 2 ? 4 : 2));
   if (s->passes > 2 && s->gt > 2) s->gt = 2;
   s->kpt = n <= kRepairThreads * 4 ? 4 : 16;
-  s->up = b <= 16 ? 1 : 2;
+  s->up = tok_up(b);
+  s->one = b == 16 * s->up;
   if (gqa_repair_lds(n, topk, sp, d) > 64 * 1024) return "repair scratch exceeds 64 KiB of LDS";
   return nullptr;
 }
 
-template <typename T, int NCH, int UP, int P, int STEPS>
+template <typename T, int NCH, int UP, bool ONE, int P, int STEPS>
 int launch_front_gt(const FrontArgs& f, const StepShape& s, hipStream_t st) {
   const dim3 grid(f.total_wgs), block(256);
   if (!s.group)
-    hipLaunchKernelGGL((k_front<T, NCH, UP, P, STEPS, 1, false>), grid, block, 0, st, f);
+    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 1, false>), grid, block, 0, st, f);
   else if (s.gt == 2)
-    hipLaunchKernelGGL((k_front<T, NCH, UP, P, STEPS, 2, true>), grid, block, 0, st, f);
+    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 2, true>), grid, block, 0, st, f);
   else
-    hipLaunchKernelGGL((k_front<T, NCH, UP, P, STEPS, 4, true>), grid, block, 0, st, f);
+    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 4, true>), grid, block, 0, st, f);
   return stk_check_launch("k_front");
 }
 
@@ -129,8 +135,11 @@ int launch_step(const FrontArgs& f, const TailArgs& t, const StepShape& s, size_
   constexpr int P = NCH * 16 / (int)sizeof(T) * 4 / 64;   // D / 64
   constexpr int STEPS = P <= 2 ? 2 : 1;
   if (front) {
-    int rc = s.up == 1 ? launch_front_gt<T, NCH, 1, P, STEPS>(f, s, st)
-                       : launch_front_gt<T, NCH, 2, P, STEPS>(f, s, st);
+    // ONE: the whole block is one token chunk (B == 16 * UP)
+    int rc = s.up == 1 ? (s.one ? launch_front_gt<T, NCH, 1, true, P, STEPS>(f, s, st)
+                                : launch_front_gt<T, NCH, 1, false, P, STEPS>(f, s, st))
+                       : (s.one ? launch_front_gt<T, NCH, 2, true, P, STEPS>(f, s, st)
+                                : launch_front_gt<T, NCH, 2, false, P, STEPS>(f, s, st));
     if (rc) return rc;
   }
   if (!tail) return STK_OK;

@@ -15,8 +15,9 @@
 // FP32 FMAs, so no cross-lane reduction of the value vector is needed.  The
 // running state (m, l, acc) is wave-uniform in m and l.
 //
-// Supported shapes: D = 4 * NCH * EPC with D a multiple of 64 (DPL >= 1);
-// every other shape uses the generic Tile.
+// Supported shapes: D = 4 * NCH * EPC with D a multiple of 64 (DPL >= 1)
+// and B a multiple of 16 (whole chunks); every other shape uses the
+// generic Tile.
 #pragma once
 
 #include "attn.hpp"
@@ -77,24 +78,25 @@ struct TokTile {
   }
 
   // K rows of one chunk (tokens t0 + slot + TPP*u) and V rows (tokens t0 .. t0+CH-1)
-  // of the block at kb/vb.  Rows at or past B read row 0 of the block.
-  __device__ __forceinline__ void load(const T* kb, const T* vb, int t0, int B,
+  // of the block at kb/vb.  The chunk lies inside the block (the token tile
+  // is only used when CH divides B), so every row address is a constant
+  // offset from one base per lane and no address needs a clamp.
+  __device__ __forceinline__ void load(const T* kb, const T* vb, int t0,
                                        uint32_t (&kw)[UP][QW], uint32_t (&vw)[CH][VW]) const {
+    const T* krow = kb + (size_t)(t0 + slot) * D;
 #pragma unroll
     for (int u = 0; u < UP; ++u) {
-      int t = t0 + slot + TPP * u;
-      const T* row = kb + (size_t)(t < B ? t : 0) * D;
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        uint4 x = *reinterpret_cast<const uint4*>(row + kdim(c));
+        uint4 x = *reinterpret_cast<const uint4*>(krow + (size_t)TPP * u * D + kdim(c));
         kw[u][4 * c + 0] = x.x; kw[u][4 * c + 1] = x.y; kw[u][4 * c + 2] = x.z;
         kw[u][4 * c + 3] = x.w;
       }
     }
+    const T* vrow = vb + (size_t)t0 * D + lane_id() * DPL;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
-      int t = t0 + i;
-      const T* row = vb + (size_t)(t < B ? t : 0) * D + lane_id() * DPL;
+      const T* row = vrow + (size_t)i * D;
       if constexpr (DPL * sizeof(T) == 2) {
         vw[i][0] = *reinterpret_cast<const uint16_t*>(row);
       } else if constexpr (DPL * sizeof(T) == 4) {
@@ -129,8 +131,7 @@ struct TokTile {
       float acc = 0.f;
 #pragma unroll
       for (int w = 0; w < QW; ++w) acc = Elem<T>::dot(kw[u][w], qw[w], acc);
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
+      acc = quad_sum(acc);
       int t = t0 + slot + TPP * u;
       s[u] = t < B ? acc * scale : -INFINITY;
     }
@@ -150,7 +151,7 @@ struct TokTile {
       float cm = s[0];
 #pragma unroll
       for (int u = 1; u < UP; ++u) cm = fmaxf(cm, s[u]);
-      for (int off = LPT; off < STK_WAVE; off <<= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+      cm = wave_max_u(cm);
       float nm = fmaxf(m, cm);
       if (nm > m) {
         float alpha = m == -INFINITY ? 0.f : expf(m - nm);
@@ -186,9 +187,13 @@ struct TokTile {
   }
 };
 
-// Token-tile shape for (dtype, D): NCH chunks per lane; 0 when unsupported.
-inline int tok_nch(int dtype, int d, uintptr_t align_bits) {
-  if ((align_bits & 15) != 0) return 0;
+// Token passes per chunk for block size B: the largest UP in {2, 1} with
+// 16 * UP dividing B; 0 when B is not a multiple of 16.
+inline int tok_up(int b) { return b % 32 == 0 ? 2 : (b % 16 == 0 ? 1 : 0); }
+
+// Token-tile shape for (dtype, D, B): NCH chunks per lane; 0 when unsupported.
+inline int tok_nch(int dtype, int d, int b, uintptr_t align_bits) {
+  if ((align_bits & 15) != 0 || tok_up(b) == 0) return 0;
   int esize = dtype == DT_F32 ? 4 : 2;
   int epc = 16 / esize;
   if (d % 64 != 0 || d % (4 * epc) != 0) return 0;

@@ -324,6 +324,8 @@ def test_gqa_paths(hq):
     (4, 1, 9000, 8, 256, 100, 120, 100, torch.float16),   # all hits, wide rows, big N
     (6, 3, 12000, 5, 70, 37, 29, 11, torch.float32),      # odd D and B, brute-force membership
     (16, 4, 2048, 32, 128, 64, 64, 48, torch.bfloat16),   # c3-like, 16 misses per head
+    (8, 4, 500, 48, 64, 30, 30, 20, torch.float16),       # three 16-token chunks per block
+    (8, 8, 400, 16, 128, 24, 24, 12, torch.bfloat16),     # G = 1, one 16-token chunk
 ])
 def test_gqa_states_and_repair_shapes(hq, hkv, n, b, d, sa, sp, hits, dtype):
     """Deduplicated GQA states (one tile read per KV group) and the
@@ -472,7 +474,9 @@ def test_touch_kv_checksums():
     (4, 4, 64, 32, 64, 8, 0.75, torch.float16, False),        # c1 shape (G = 1)
     (8, 4, 300, 16, 256, 40, 0.5, torch.bfloat16, False),     # D = 256, one-pass tiles
     (6, 3, 5000, 32, 128, 80, 1.0, torch.float16, False),     # long rows, all hits
-    (12, 1, 700, 8, 64, 20, 0.0, torch.bfloat16, False),      # G = 12, no hits
+    (12, 1, 700, 16, 64, 20, 0.0, torch.bfloat16, False),     # G = 12, no hits, B = 16
+    (8, 2, 400, 64, 128, 32, 0.9, torch.bfloat16, False),     # B = 64: two streamed chunks
+    (4, 2, 300, 48, 64, 16, 0.75, torch.float16, False),      # B = 48: three 16-token chunks
 ])
 def test_speculative_step(hq, hkv, n, b, d, topk, overlap, dtype, union):
     """speculative_step: selected IDs bit-exact, prediction states and the
@@ -499,14 +503,17 @@ def test_speculative_step(hq, hkv, n, b, d, topk, overlap, dtype, union):
     check(res.output, expected, ("step", hq, n, union))
 
 
-def test_speculative_step_composed_fallback():
-    """fp32 inputs and int64 predictions run through the individual kernels."""
+@pytest.mark.parametrize("dtype,b", [(torch.float32, 8), (torch.bfloat16, 8)])
+def test_speculative_step_composed_fallback(dtype, b):
+    """fp32 inputs with int64 predictions, and blocks whose token count is not
+    a multiple of 16, run through the individual kernels."""
     from strict_topk import step
     gen = torch.Generator().manual_seed(9)
-    q = torch.randn((4, 48), generator=gen)
-    k = torch.randn((2, 30, 8, 48), generator=gen)
-    v = torch.randn(k.shape, generator=gen)
-    lo, hi = k.amin(2), k.amax(2)
+    d = 48 if dtype == torch.float32 else 64
+    q = torch.randn((4, d), generator=gen).to(dtype)
+    k = torch.randn((2, 30, b, d), generator=gen).to(dtype)
+    v = torch.randn(k.shape, generator=gen).to(dtype)
+    lo, hi = k.amin(2).float(), k.amax(2).float()
     p = torch.stack([torch.randperm(30, generator=gen)[:6] for _ in range(4)])
     qn, kn, vn = np_(q, k, v)
     ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), 6)
