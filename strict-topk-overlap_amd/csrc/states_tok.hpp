@@ -8,9 +8,6 @@
 
 #include "tile2.hpp"
 
-#ifndef STK_TOK_HT
-#define STK_TOK_HT 1
-#endif
 
 namespace stk {
 
@@ -39,7 +36,15 @@ struct StatesArgs {
 };
 
 constexpr int kGrpHT = 4;   // heads sharing one loaded tile (generic-tile kernels)
-constexpr int kTokHT = STK_TOK_HT;   // heads per pass over a resident token tile
+
+// Up to 64 bits [o, o + len) of a 256-bit mask held as four wave-uniform words.
+__device__ __forceinline__ uint64_t mask_bits(const uint64_t (&m)[4], int o, int len) {
+  const int w = o >> 6, sh = o & 63;
+  const uint64_t a = w == 0 ? m[0] : (w == 1 ? m[1] : (w == 2 ? m[2] : m[3]));
+  const uint64_t b = w == 0 ? m[1] : (w == 1 ? m[2] : (w == 2 ? m[3] : 0ull));
+  const uint64_t r = sh ? (a >> sh) | (b << (64 - sh)) : a;
+  return len >= 64 ? r : (r & ((1ull << len) - 1ull));
+}
 
 // Token-tile states (shapes the token tile supports): one wave per
 // (query head, slot).  GROUP: the wave owning block b (no lower head of its
@@ -48,13 +53,15 @@ constexpr int kTokHT = STK_TOK_HT;   // heads per pass over a resident token til
 // computes its own slot, honouring the optional active mask (inactive slots
 // get (-inf, 0, 0), kernels.py:42-71).
 //
-// ONE (B == CH): the block is loaded once and stays in registers while the
-// heads are processed HT at a time; otherwise the block is streamed chunk by
-// chunk for each batch of HT heads.  HT trades registers
-// for passes: with HT = 1 the wave stays within 128 VGPRs, so four waves
-// share a SIMD.
-template <typename T, int NCH, int UP, typename I, bool GROUP, bool ONE,
-          int HT = (GROUP ? kTokHT : 1)>
+// Dependent memory round trips are what a wave waits for when HBM queues
+// are full, so there are two: (1) the group's IDs and the wave's own query
+// row, (2) the K/V tile.  The rows that list b come from ballots over the
+// IDs of round trip 1, so writing the states needs no further ID loads; a
+// further head's query row is loaded while the previous head finishes.  ONE (B == CH): the block is loaded once
+// and stays in registers while the heads are processed in turn (one head at
+// a time keeps the wave within 128 VGPRs: four waves per SIMD); otherwise
+// each head streams the block chunk by chunk.
+template <typename T, int NCH, int UP, typename I, bool GROUP, bool ONE>
 __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
   using TT = TokTile<T, NCH, UP>;
   const int waves = blockDim.x / STK_WAVE;
@@ -66,10 +73,16 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
   const int G = a.hq / a.hkv;
   const int hl = h % G;
   const int g0 = h - hl;
+  TT t;
+  t.init();
+  const T* qg = reinterpret_cast<const T*>(a.q) + (size_t)g0 * a.d;
+  uint32_t qw[TT::QW];
+  t.load_q(qg + (size_t)hl * a.d, qw);   // own query row, with the IDs
   int64_t bid;
-  uint64_t found = 1ull << hl;
+  uint64_t found = 1ull << hl;           // heads of the group listing b
+  uint64_t rows[4] = {0ull, 0ull, 0ull, 0ull};   // ID == b over the group's G*S IDs
   if constexpr (GROUP) {
-    // rows of the group that list b; G*S <= 256 IDs, 4 per lane, one pass
+    // the group's G*S <= 256 IDs, 4 per lane, in one pass
     const int total = G * a.s;
     const I* grp = ids + (int64_t)g0 * a.s;
     int64_t v[4];
@@ -84,15 +97,14 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
 #pragma unroll
     for (int i = 1; i < 4; ++i) pick = ib == i ? v[i] : pick;
     bid = __shfl(pick, lb);
-    found = 0ull;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int x = i * STK_WAVE + lane_id();
-      if (x < total && v[i] == bid) found |= 1ull << (x / a.s);
-    }
-    for (int off = 1; off < STK_WAVE; off <<= 1) found |= __shfl_xor(found, off);
+    for (int i = 0; i < 4; ++i) rows[i] = __ballot(i * STK_WAVE + lane_id() < total && v[i] == bid);
+    found = 0ull;
+    for (int r = 0; r < G; ++r)
+      if (mask_bits(rows, r * a.s, a.s < 64 ? a.s : 64) != 0ull ||
+          (a.s > 64 && mask_bits(rows, r * a.s + 64, a.s - 64) != 0ull))
+        found |= 1ull << r;
     if (found & ((1ull << hl) - 1ull)) return;   // a lower head owns this block
-    found &= ~((1ull << hl) - 1ull);
   } else {
     bid = ids[item];
   }
@@ -102,93 +114,68 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
     else if (a.active_kind == 2) enabled = enabled && a.active[item] != 0;
   }
   const int kv = h / G;
-  TT t;
-  t.init();
   const float scale = 1.0f / sqrtf((float)a.d);
   const size_t off = (((size_t)kv * a.n + (enabled ? (size_t)bid : 0)) * a.b) * a.d;
   const T* kb = reinterpret_cast<const T*>(a.k) + off;
   const T* vb = reinterpret_cast<const T*>(a.v) + off;
   uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
   if constexpr (ONE) t.load(kb, vb, 0, kw, vw);   // the whole block, once
-  while (found) {
-    int heads[HT];
-    int nh = 0;
+  // heads after the owner, lowest first
+  uint64_t rest = found & ~(1ull << hl);
+  int cur = hl;
+  while (true) {
+    float m = -INFINITY, l = 0.f, acc[TT::DPL];
 #pragma unroll
-    for (int i = 0; i < HT; ++i) {
-      heads[i] = hl;
-      if (found) {
-        int gg = __ffsll((long long)found) - 1;
-        found &= found - 1;
-        heads[i] = gg;
-        nh = i + 1;
-      }
-    }
-    uint32_t qw[HT][TT::QW];
-    uint64_t pmask[HT];
-    float m[HT], l[HT], acc[HT][TT::DPL];
+    for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
+    const int nxt = rest ? __ffsll((long long)rest) - 1 : cur;
+    if constexpr (ONE) {
+      // opaque tile words: the value conversions stay inside the head loop
+      // (hoisted out of it they would hold every token's FP32 values)
 #pragma unroll
-    for (int i = 0; i < HT; ++i) {
-      m[i] = -INFINITY;
-      l[i] = 0.f;
+      for (int i = 0; i < TT::CH; ++i)
 #pragma unroll
-      for (int e = 0; e < TT::DPL; ++e) acc[i][e] = 0.f;
-      t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)(g0 + heads[i]) * a.d, qw[i]);
-      pmask[i] = 0ull;
-      if constexpr (GROUP) {
-        // rows of at most 64 IDs: positions of b, read with the query
-        bool in = lane_id() < a.s;
-        int64_t x = ld_or(ids, (int64_t)(g0 + heads[i]) * a.s + lane_id(), in, (I)-1);
-        pmask[i] = __ballot(in && x == bid);
-      }
-    }
-    if (enabled) {
-      if constexpr (ONE) {
-#pragma unroll
-        for (int i = 0; i < HT; ++i)
-          if (i < nh)
-            t.template update<false, false>(qw[i], kw, vw, 0, a.b, scale, m[i], l[i], acc[i]);
-      } else {
+        for (int w = 0; w < TT::VW; ++w) asm volatile("" : "+v"(vw[i][w]));
+      float s[UP];
+      t.scores(qw, kw, 0, a.b, scale, s);
+      // the next head's query loads into the registers just freed, hidden
+      // behind this head's softmax and P.V
+      if (rest) t.load_q(qg + (size_t)nxt * a.d, qw);
+      if (enabled) t.template accumulate<false, false>(s, vw, m, l, acc);
+    } else {
+      if (enabled) {
         for (int t0 = 0; t0 < a.b; t0 += TT::CH) {
           t.load(kb, vb, t0, kw, vw);
-#pragma unroll
-          for (int i = 0; i < HT; ++i)
-            if (i < nh)
-              t.template update<false, false>(qw[i], kw, vw, t0, a.b, scale, m[i], l[i], acc[i]);
+          t.template update<false, false>(qw, kw, vw, t0, a.b, scale, m, l, acc);
         }
       }
+      if (rest) t.load_q(qg + (size_t)nxt * a.d, qw);
     }
-#pragma unroll
-    for (int i = 0; i < HT; ++i) {
-      if (i >= nh) continue;
-      const int gg = heads[i];
-      if (gg == hl) {
-        if (lane_id() == 0) {
-          a.m[item] = m[i];
-          a.l[item] = l[i];
-        }
-        t.store(a.u + item * a.d, acc[i]);
-        continue;
+    if (cur == hl) {
+      if (lane_id() == 0) {
+        a.m[item] = m;
+        a.l[item] = l;
       }
-      const int64_t rbase = (int64_t)(g0 + gg) * a.s;
+      t.store(a.u + item * a.d, acc);
+    } else {
+      const int64_t rbase = (int64_t)(g0 + cur) * a.s;
       for (int p0 = 0; p0 < a.s; p0 += STK_WAVE) {
-        int p = p0 + lane_id();
-        uint64_t hits = pmask[i];
-        if (p0 > 0) {
-          int64_t x = ld_or(ids, rbase + p, p < a.s, (I)-1);
-          hits = __ballot(p < a.s && x == bid);
-        }
+        const int len = a.s - p0 < 64 ? a.s - p0 : 64;
+        uint64_t hits = mask_bits(rows, cur * a.s + p0, len);
         while (hits) {
-          int bit = __ffsll((long long)hits) - 1;
+          const int bit = __ffsll((long long)hits) - 1;
           hits &= hits - 1;
-          int64_t row = rbase + p0 + bit;
+          const int64_t row = rbase + p0 + bit;
           if (lane_id() == 0) {
-            a.m[row] = m[i];
-            a.l[row] = l[i];
+            a.m[row] = m;
+            a.l[row] = l;
           }
-          t.store(a.u + row * a.d, acc[i]);
+          t.store(a.u + row * a.d, acc);
         }
       }
     }
+    if (!rest) break;
+    rest &= rest - 1;
+    cur = nxt;
   }
 }
 

@@ -137,16 +137,14 @@ struct TokTile {
     }
   }
 
-  // Online-softmax update of (m, l, acc) with one chunk.  FIXED keeps m as
-  // the exponent frame (no rescaling; the caller guarantees it).  ABS also
-  // accumulates sum |w * v| (low-group envelope).
+  // Online-softmax update of (m, l, acc) with one chunk whose scaled logits
+  // s (this lane's slot, scores()) are known.  FIXED keeps m as the exponent
+  // frame (no rescaling; the caller guarantees it).  ABS also accumulates
+  // sum |w * v| (low-group envelope).
   template <bool FIXED, bool ABS>
-  __device__ __forceinline__ void update(const uint32_t* qw, const uint32_t (&kw)[UP][QW],
-                                         const uint32_t (&vw)[CH][VW], int t0, int B,
-                                         float scale, float& m, float& l, float* acc,
-                                         float* aacc = nullptr) const {
-    float s[UP];
-    scores(qw, kw, t0, B, scale, s);
+  __device__ __forceinline__ void accumulate(const float (&s)[UP], const uint32_t (&vw)[CH][VW],
+                                             float& m, float& l, float* acc,
+                                             float* aacc = nullptr) const {
     if constexpr (!FIXED) {
       float cm = s[0];
 #pragma unroll
@@ -178,6 +176,17 @@ struct TokTile {
         if constexpr (ABS) aacc[e] += fabsf(x);
       }
     }
+  }
+
+  // scores() then accumulate() for one chunk
+  template <bool FIXED, bool ABS>
+  __device__ __forceinline__ void update(const uint32_t* qw, const uint32_t (&kw)[UP][QW],
+                                         const uint32_t (&vw)[CH][VW], int t0, int B,
+                                         float scale, float& m, float& l, float* acc,
+                                         float* aacc = nullptr) const {
+    float s[UP];
+    scores(qw, kw, t0, B, scale, s);
+    accumulate<FIXED, ABS>(s, vw, m, l, acc, aacc);
   }
 
   // this lane's DPL dims of a D-vector
