@@ -218,8 +218,11 @@ __device__ __forceinline__ int block_count(int v, int* red) {
 
 // exp(a - b) where an empty state (a == -inf) contributes exactly 0, also
 // when b is -inf.
+// exp(a - b), 0 for a = -inf.  The hardware exponential (2^x after one
+// multiply by log2 e) is accurate to a few ulp, far inside the FP32
+// softmax's own rounding.
 __device__ __forceinline__ float wexp(float a, float b) {
-  return a == -INFINITY ? 0.f : expf(a - b);
+  return a == -INFINITY ? 0.f : __expf(a - b);
 }
 
 // --------------------------------------------------------------- scans
@@ -248,6 +251,61 @@ __device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total) {
     all += x;
   }
   __syncthreads();
+  *total = all;
+  return before + inc - v;
+}
+
+// Inclusive prefix sum over the wave through DPP: row shifts by 1, 2, 4, 8
+// inside each 16-lane row (lanes without a source add 0), then the row
+// broadcasts of lanes 15 and 31 carry the row totals into the later rows.
+// Needs every lane of the wave active.
+__device__ __forceinline__ int wave_incl_scan_dpp(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+  return v;
+}
+
+// Wave-uniform OR / AND of a 32-bit value (DPP reduction pattern of
+// wave_max_u, lane 63 ends with the total).  Needs every lane active.
+template <bool AND>
+__device__ __forceinline__ uint32_t wave_bits_u(uint32_t v) {
+  const int id = AND ? -1 : 0;
+  auto step = [&](int x, int y) { return AND ? (x & y) : (x | y); };
+  int x = (int)v;
+  x = step(x, __builtin_amdgcn_update_dpp(id, x, 0xB1, 0xf, 0xf, false));
+  x = step(x, __builtin_amdgcn_update_dpp(id, x, 0x4E, 0xf, 0xf, false));
+  x = step(x, __builtin_amdgcn_update_dpp(id, x, 0x141, 0xf, 0xf, false));
+  x = step(x, __builtin_amdgcn_update_dpp(id, x, 0x140, 0xf, 0xf, false));
+  x = step(x, __builtin_amdgcn_update_dpp(id, x, 0x142, 0xa, 0xf, false));
+  x = step(x, __builtin_amdgcn_update_dpp(id, x, 0x143, 0xc, 0xf, false));
+  return (uint32_t)__builtin_amdgcn_readlane(x, 63);
+}
+template <bool AND>
+__device__ __forceinline__ uint64_t wave_bits64_u(uint64_t v) {
+  return ((uint64_t)wave_bits_u<AND>((uint32_t)(v >> 32)) << 32) | wave_bits_u<AND>((uint32_t)v);
+}
+
+// Lanes below this one.
+__device__ __forceinline__ uint64_t lanemask_lt() { return (1ull << lane_id()) - 1ull; }
+
+// Exclusive prefix sum over the workgroup in thread order with one barrier;
+// `tmp` holds one int per wave and must not be rewritten until every thread
+// has returned (use a fresh buffer or a barrier).  Needs full waves.
+__device__ __forceinline__ int block_excl_scan1(int v, int* tmp, int* total) {
+  const int inc = wave_incl_scan_dpp(v);
+  const int nw = blockDim.x / STK_WAVE;
+  if (lane_id() == STK_WAVE - 1) tmp[wave_id()] = inc;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < nw; ++w) {
+    const int x = tmp[w];
+    before += w < wave_id() ? x : 0;
+    all += x;
+  }
   *total = all;
   return before + inc - v;
 }

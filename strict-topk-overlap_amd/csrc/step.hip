@@ -10,15 +10,17 @@
 //                  predicted blocks, one K/V read per KV group), the two
 //                  roles interleaved evenly inside every XCD so both
 //                  streams of HBM traffic run side by side on all of them;
-//   k_topk_repair  one workgroup per query head: exact top-K of the head's
-//                  keys (written out as the selected IDs, ascending) feeding
-//                  the single-workgroup saved / union repair directly from LDS.
+//   k_tail         one workgroup per query head: exact top-K of the head's
+//                  keys (written out as the selected IDs, ascending), then the
+//                  saved / union repair, laid out around two dependent memory
+//                  round trips (everything known up front, then the missed
+//                  blocks' tiles).
 // The arithmetic is that of stk_select_blocks, stk_block_partials and
 // stk_gqa_repair; results are identical up to FP32 reduction order.
 #include "score.hpp"
 #include "topk.hpp"
 #include "states_tok.hpp"
-#include "gqa_repair.hpp"
+#include "tail.hpp"
 #include "api.hpp"
 
 namespace stk {
@@ -45,28 +47,9 @@ __global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_front(FrontArgs a) {
     states_tok_wg<T, NCH, UP, int32_t, GROUP, ONE>(a.st, i - upto);
 }
 
-struct TailArgs {
-  GqaRepairArgs r;
-  const uint64_t* keys;
-  int n, k;
-  int32_t* ids;
-};
-
-template <class Stream, int CHUNKS, int KPT>
-__global__ __launch_bounds__(kRepairThreads) void k_topk_repair(TailArgs a) {
-  extern __shared__ int lds_i[];
-  __shared__ TopkLds tl;
-  __shared__ int tmp[kRepairWaves];
-  __shared__ float wm[kRepairWaves], wl[kRepairWaves];
-  const int h = blockIdx.x;
-  const bool use_map = a.r.kv.n <= kRepairMapN;
-  int* ids = lds_i + (use_map ? a.r.kv.n : a.r.sp);
-  int32_t* out = a.ids + (size_t)h * a.k;
-  topk_select<KPT>(a.keys + (size_t)h * a.n, a.n, a.k, tl, [&](int pos, int idx) {
-    ids[pos] = idx;
-    out[pos] = idx;
-  });
-  gqa_repair_head<Stream, CHUNKS, true>(a.r, h, lds_i, tmp, wm, wl, true);
+template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
+__global__ __launch_bounds__(kTailThreads) void k_tail(TailArgs a) {
+  tail_head<T, NCH, UP, ONE, KPT, RPT>(a);
 }
 
 }  // namespace stk
@@ -76,7 +59,7 @@ using namespace stk;
 namespace {
 
 struct StepShape {
-  int nch, passes, steps, gt, kpt, up;
+  int nch, passes, steps, gt, kpt, up, rpt;
   bool group, one;
 };
 
@@ -89,8 +72,7 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
   if (!s->nch)
     return "the fused step needs D in {64, 128, 256}, B a multiple of 16 and 16-byte aligned Q/K/V";
   if (n > 8192) return "the fused step supports at most 8192 blocks";
-  if (topk < 1 || topk > n || topk > kMaxIds || sp < 1 || sp > kMaxIds)
-    return "bad topk or predicted width";
+  if (topk < 1 || topk > n || sp < 1) return "bad topk or predicted width";
   const int G = hq / hkv;
   if (G > 64 || (G > 1 && G * sp > 4 * STK_WAVE))
     return "the fused step needs (Hq/Hkv) * SP <= 256";
@@ -99,10 +81,14 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
   s->group = G > 1;
   s->gt = G == 1 ? 1 : (G == 2 ? 2 : (s->passes <= 2 ? 4 : 2));
   if (s->passes > 2 && s->gt > 2) s->gt = 2;
-  s->kpt = n <= kRepairThreads * 4 ? 4 : 16;
+  s->kpt = n <= kTailThreads * 4 ? 4 : 16;
   s->up = tok_up(b);
   s->one = b == 16 * s->up;
-  if (gqa_repair_lds(n, topk, sp, d) > 64 * 1024) return "repair scratch exceeds 64 KiB of LDS";
+  if (topk > kTailMaxK || sp > kTailMaxK) return "the fused step takes at most 256 selected and predicted IDs";
+  // predicted states held by the tail: sp rows over 512 / D row groups
+  const int rows = (sp + kTailThreads / d - 1) / (kTailThreads / d);
+  if (rows > 32) return "the fused step needs SP * D <= 16384";
+  s->rpt = rows <= 16 ? 16 : 32;
   return nullptr;
 }
 
@@ -118,20 +104,23 @@ int launch_front_gt(const FrontArgs& f, const StepShape& s, hipStream_t st) {
   return stk_check_launch("k_front");
 }
 
-template <typename T, int NCH, int UP>
-int launch_tail(const TailArgs& t, const StepShape& s, size_t lds, hipStream_t st) {
-  const dim3 grid(t.r.kv.hq), block(kRepairThreads);
-  constexpr int CH = NCH * 16 / (int)sizeof(T) * 4 <= 128 ? 1 : 2;   // D <= 128 ?
-  if (s.kpt == 4)
-    hipLaunchKernelGGL((k_topk_repair<TokStream<T, NCH, UP>, CH, 4>), grid, block, lds, st, t);
+template <typename T, int NCH, int UP, bool ONE>
+int launch_tail(const TailArgs& t, const StepShape& s, hipStream_t st) {
+  const dim3 grid(t.kv.hq), block(kTailThreads);
+  if (s.kpt == 4 && s.rpt == 16)
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 4, 16>), grid, block, 0, st, t);
+  else if (s.kpt == 4)
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 4, 32>), grid, block, 0, st, t);
+  else if (s.rpt == 16)
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 16, 16>), grid, block, 0, st, t);
   else
-    hipLaunchKernelGGL((k_topk_repair<TokStream<T, NCH, UP>, CH, 16>), grid, block, lds, st, t);
-  return stk_check_launch("k_topk_repair");
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 16, 32>), grid, block, 0, st, t);
+  return stk_check_launch("k_tail");
 }
 
 template <typename T, int NCH>
-int launch_step(const FrontArgs& f, const TailArgs& t, const StepShape& s, size_t lds,
-                hipStream_t st, bool front, bool tail) {
+int launch_step(const FrontArgs& f, const TailArgs& t, const StepShape& s, hipStream_t st,
+                bool front, bool tail) {
   constexpr int P = NCH * 16 / (int)sizeof(T) * 4 / 64;   // D / 64
   constexpr int STEPS = P <= 2 ? 2 : 1;
   if (front) {
@@ -143,7 +132,10 @@ int launch_step(const FrontArgs& f, const TailArgs& t, const StepShape& s, size_
     if (rc) return rc;
   }
   if (!tail) return STK_OK;
-  return s.up == 1 ? launch_tail<T, NCH, 1>(t, s, lds, st) : launch_tail<T, NCH, 2>(t, s, lds, st);
+  return s.up == 1 ? (s.one ? launch_tail<T, NCH, 1, true>(t, s, st)
+                            : launch_tail<T, NCH, 1, false>(t, s, st))
+                   : (s.one ? launch_tail<T, NCH, 2, true>(t, s, st)
+                            : launch_tail<T, NCH, 2, false>(t, s, st));
 }
 
 }  // namespace
@@ -194,21 +186,19 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
   f.score_wgs = hkv * f.sc.chunks;
   f.total_wgs = f.score_wgs + (int)(((int64_t)hq * sp + 3) / 4);
   TailArgs t{};
-  t.r.kv = KV{q, k, v, hq, hkv, n, b, d};
-  t.r.a = selected; t.r.atype = IT_I32; t.r.sa = topk;
-  t.r.p = predicted; t.r.ptype = IT_I32; t.r.sp = sp;
-  t.r.pm = m; t.r.pl = l; t.r.pu = u; t.r.uni = union_mode ? 1 : 0; t.r.out = out;
-  t.keys = keys; t.n = n; t.k = topk; t.ids = selected;
-  const size_t lds = gqa_repair_lds(n, topk, sp, d);
+  t.kv = KV{q, k, v, hq, hkv, n, b, d};
+  t.keys = keys; t.k = topk; t.ids = selected;
+  t.p = static_cast<const int32_t*>(predicted); t.sp = sp;
+  t.pm = m; t.pl = l; t.pu = u; t.uni = union_mode ? 1 : 0; t.out = out;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DT_BF16) {
-    if (s.nch == 2) return launch_step<bf16s, 2>(f, t, s, lds, st, front, tail);
-    if (s.nch == 4) return launch_step<bf16s, 4>(f, t, s, lds, st, front, tail);
-    return launch_step<bf16s, 8>(f, t, s, lds, st, front, tail);
+    if (s.nch == 2) return launch_step<bf16s, 2>(f, t, s, st, front, tail);
+    if (s.nch == 4) return launch_step<bf16s, 4>(f, t, s, st, front, tail);
+    return launch_step<bf16s, 8>(f, t, s, st, front, tail);
   }
-  if (s.nch == 2) return launch_step<f16s, 2>(f, t, s, lds, st, front, tail);
-  if (s.nch == 4) return launch_step<f16s, 4>(f, t, s, lds, st, front, tail);
-  return launch_step<f16s, 8>(f, t, s, lds, st, front, tail);
+  if (s.nch == 2) return launch_step<f16s, 2>(f, t, s, st, front, tail);
+  if (s.nch == 4) return launch_step<f16s, 4>(f, t, s, st, front, tail);
+  return launch_step<f16s, 8>(f, t, s, st, front, tail);
 }
 
 STK_API int stk_speculative_step(const void* q, const void* k, const void* v, int dtype, int hq,

@@ -1,0 +1,203 @@
+// Tail of the fused decode step: exact top-K of one query head's keys and
+// the strict repair of its speculative attention, in one workgroup per head.
+//
+// Reference: strict_topk/gqa.py:145-161 (select_blocks), :164-193
+// (repair_saved / repair_union) and gqa_light.py:10-92; the arithmetic of
+// the saved repair is that of stk_gqa_repair.
+//
+// The tail runs on 32-64 workgroups, so its time is a chain of latencies;
+// it is laid out around two dependent memory round trips:
+//   1. the head's keys, its predicted row, its query row and every predicted
+//      state (m, l, u) are requested together at entry;
+//   2. the missed blocks' K/V tiles, once the top-K is known.
+// In between: top-K (two barriers per radix pass), membership through an
+// LDS map over block IDs (max predicted slot + 1, plus a selected flag) and
+// a bit mask of the predicted slots to merge, and the hits' LSE partial sums
+// from registers.
+#pragma once
+
+#include "topk.hpp"
+#include "tile2.hpp"
+
+namespace stk {
+
+constexpr int kTailThreads = 512;
+constexpr int kTailWaves = kTailThreads / STK_WAVE;
+constexpr int kTailMapN = 8192;      // block IDs covered by the LDS map
+constexpr int kTailMaxK = 256;       // selected / predicted IDs per row
+constexpr int kSelFlag = 1 << 30;    // map bit: block is selected
+
+struct TailArgs {
+  KV kv;                                  // q, k, v, hq, hkv, n, b, d
+  const uint64_t* keys;                   // [hq, n]
+  int k;                                  // selected per head
+  int32_t* ids;                           // [hq, k] out, ascending
+  const int32_t* p; int sp;               // predicted [hq, sp]
+  const float* pm; const float* pl; const float* pu;   // predicted states
+  int uni;                                // repair_union instead of saved
+  float* out;                             // [hq, d]
+};
+
+// KPT keys per thread (n <= 512 * KPT); RPT predicted rows per thread
+// (sp <= RPT * 512 / D); ONE: a block is one token chunk.
+template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
+__device__ __forceinline__ void tail_head(const TailArgs& a) {
+  using TT = TokTile<T, NCH, UP>;
+  constexpr int D = TT::D;
+  constexpr int RG = kTailThreads / D;    // row groups of the state prefetch
+  __shared__ int map[kTailMapN];
+  __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
+  __shared__ TopkLds tl;
+  __shared__ int s_nm;
+  __shared__ uint64_t s_used[kTailMaxK / 64];   // predicted slots whose state is merged
+  __shared__ float s_hmax[kTailWaves], s_hl[RG], s_hu[RG][D];
+  __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_wu[kTailWaves][D];
+  const int h = blockIdx.x;
+  const int n = a.kv.n, sp = a.sp;
+  const int tid = threadIdx.x, w = wave_id();
+  const int G = a.kv.hq / a.kv.hkv;
+  // ---- round trip 1: every load that does not depend on the top-K
+  uint64_t key[KPT];
+  topk_load<KPT>(a.keys + (size_t)h * n, n, key);
+  const int pid = (int)ld_or(a.p, (int64_t)h * sp + tid, tid < sp, (int32_t)-1);
+  TT t;
+  t.init();
+  uint32_t qw[TT::QW];
+  t.load_q(reinterpret_cast<const T*>(a.kv.q) + (size_t)h * D, qw);
+  const int dcol = tid % D, rg = tid / D;
+  float um[RPT], ul[RPT], uu[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int r = rg + RG * j;
+    const bool on = r < sp;
+    const int64_t row = (int64_t)h * sp + (on ? r : 0);
+    um[j] = ld_or(a.pm, row, on, -INFINITY);
+    ul[j] = ld_or(a.pl, row, on, 0.f);
+    uu[j] = ld_or(a.pu, row * D + dcol, on, 0.f);
+  }
+  // ---- membership map: max predicted slot + 1 per block ID
+  for (int i = tid; i < n; i += kTailThreads) map[i] = 0;
+  if (tid < sp) pids[tid] = pid;
+  __syncthreads();
+  if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
+  // ---- exact top-K (its first barrier orders the map writes above)
+  int32_t* out_ids = a.ids + (size_t)h * a.k;
+  topk_select_keys<KPT>(key, n, a.k, tl, [&](int pos, int idx) {
+    sel[pos] = idx;
+    out_ids[pos] = idx;
+    atomicOr(&map[idx], kSelFlag);
+  });
+  __syncthreads();
+  // ---- misses (selected, not predicted) in ascending block order, and the
+  // predicted slots whose states are merged: saved mode takes slot p when
+  // P[p] is selected and p is the highest slot holding that block; union
+  // mode takes every slot
+  if (w == 0) {
+    int cnt = 0;
+    for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
+      const int p = p0 + lane_id();
+      const bool in = p < a.k;
+      const int id = in ? sel[p] : 0;
+      const bool ms = in && (map[id] & ~kSelFlag) == 0;
+      const uint64_t bal = __ballot(ms);
+      if (ms) miss[cnt + (int)__popcll(bal & lanemask_lt())] = id;
+      cnt += (int)__popcll(bal);
+    }
+    if (lane_id() == 0) s_nm = cnt;
+    for (int p0 = 0; p0 < kTailMaxK; p0 += STK_WAVE) {
+      const int p = p0 + lane_id();
+      const int pv = p < sp ? pids[p] : -1;
+      const int mv = pv >= 0 && pv < n ? map[pv] : 0;
+      const bool use = p < sp && (a.uni || ((mv & kSelFlag) && (mv & ~kSelFlag) == p + 1));
+      const uint64_t bal = __ballot(use);
+      if (lane_id() == 0) s_used[p0 / STK_WAVE] = bal;
+    }
+  }
+  __syncthreads();
+  const int nm = s_nm;
+  // ---- round trip 2: wave w streams misses w, w + 8, ...; the first
+  // tile's loads are issued before the hits' arithmetic
+  const int kvh = h / G;
+  const float scale = 1.0f / sqrtf((float)D);
+  const T* K = reinterpret_cast<const T*>(a.kv.k);
+  const T* V = reinterpret_cast<const T*>(a.kv.v);
+  auto tile = [&](int x) {
+    return (((size_t)kvh * n + miss[x]) * a.kv.b) * D;
+  };
+  uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
+  if (ONE && w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
+  // ---- the hits' (or, for union, every predicted row's) partial LSE sums
+  uint64_t um4[kTailMaxK / 64];
+#pragma unroll
+  for (int x = 0; x < kTailMaxK / 64; ++x) um4[x] = s_used[x];
+  bool used[RPT];
+  float hm = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int r = rg + RG * j;   // < 32 * RG <= 256
+    const uint64_t word = um4[0] * (r < 64) | um4[1] * (r >= 64 && r < 128) |
+                          um4[2] * (r >= 128 && r < 192) | um4[3] * (r >= 192);
+    used[j] = (word >> (r & 63)) & 1ull;
+    hm = used[j] ? fmaxf(hm, um[j]) : hm;
+  }
+  hm = wave_max_u(hm);
+  if (lane_id() == 0) s_hmax[w] = hm;
+  __syncthreads();
+  float mh = -INFINITY;
+#pragma unroll
+  for (int x = 0; x < kTailWaves; ++x) mh = fmaxf(mh, s_hmax[x]);
+  float hl = 0.f, hu = 0.f;
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const float wt = used[j] ? wexp(um[j], mh) : 0.f;
+    hl += wt * ul[j];
+    hu += wt * uu[j];
+  }
+  s_hu[rg][dcol] = hu;
+  if (dcol == 0) s_hl[rg] = hl;
+  // ---- the misses' states with the online softmax
+  float m = -INFINITY, l = 0.f, acc[TT::DPL];
+#pragma unroll
+  for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
+  for (int x = w; x < nm; x += kTailWaves) {
+    if constexpr (ONE) {
+      if (x != w) t.load(K + tile(x), V + tile(x), 0, kw, vw);
+      t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+    } else {
+      for (int t0 = 0; t0 < a.kv.b; t0 += TT::CH) {
+        t.load(K + tile(x), V + tile(x), t0, kw, vw);
+        t.template update<false, false>(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
+      }
+    }
+  }
+  if (lane_id() == 0) {
+    s_wm[w] = m;
+    s_wl[w] = l;
+  }
+  t.store(s_wu[w], acc);
+  __syncthreads();
+  // ---- one LSE merge of the hits' partials and the waves' miss states
+  if (tid < D) {
+    float M = mh;
+#pragma unroll
+    for (int x = 0; x < kTailWaves; ++x) M = fmaxf(M, s_wm[x]);
+    const float fh = wexp(mh, M);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      num += s_hu[g][tid];
+      den += s_hl[g];
+    }
+    num *= fh;
+    den *= fh;
+#pragma unroll
+    for (int x = 0; x < kTailWaves; ++x) {
+      const float f = wexp(s_wm[x], M);
+      num += f * s_wu[x][tid];
+      den += f * s_wl[x];
+    }
+    a.out[(size_t)h * D + tid] = num / den;
+  }
+}
+
+}  // namespace stk

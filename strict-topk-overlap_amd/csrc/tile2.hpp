@@ -152,7 +152,7 @@ struct TokTile {
       cm = wave_max_u(cm);
       float nm = fmaxf(m, cm);
       if (nm > m) {
-        float alpha = m == -INFINITY ? 0.f : expf(m - nm);
+        float alpha = wexp(m, nm);
         l *= alpha;
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
@@ -161,7 +161,7 @@ struct TokTile {
     }
     float w[UP];
 #pragma unroll
-    for (int u = 0; u < UP; ++u) w[u] = s[u] == -INFINITY ? 0.f : expf(s[u] - m);
+    for (int u = 0; u < UP; ++u) w[u] = wexp(s[u], m);
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int u = i / TPP, src = (i % TPP) * LPT;
