@@ -77,12 +77,13 @@ def divisor_at_most(k, m):
 
 
 def traffic_record(workload):
-    """HBM bytes per k_front launch from the committed rocprof counter runs."""
+    """HBM bytes per k_front launch from the committed rocprof counter runs
+    (FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a plain copy of
+    known size), or None when no run covers this workload."""
     path = ROOT / "profiles" / "k_front_traffic.json"
     if not path.exists():
         return None
-    rec = json.loads(path.read_text())
-    return rec.get(workload)
+    return json.loads(path.read_text()).get(workload)
 
 
 def main():
@@ -193,9 +194,12 @@ def main():
     fb = step.front_bytes()
     achieved = fb / (front_us * 1e-6) / 1e9
     workload = f"{cfg.name}@{args.overlap}"
+    tr = traffic_record(workload)
     roofline = {"kernel": "k_front (select || speculate)", "bound": "hbm",
                 "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(achieved / 8000.0, 4), "traffic": traffic_record(workload),
+                "frac": round(achieved / 8000.0, 4),
+                "traffic": tr["traffic"] if tr else None,
+                "traffic_over_algorithmic": tr["traffic_over_algorithmic"] if tr else None,
                 "bytes_per_launch": fb, "us_per_launch": round(front_us, 3)}
 
     by = step.bytes()
