@@ -88,10 +88,10 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
     atomicOr(&map[idx], kSelFlag);
   });
   __syncthreads();
-  // ---- misses (selected, not predicted) in ascending block order, and the
-  // predicted slots whose states are merged: saved mode takes slot p when
-  // P[p] is selected and p is the highest slot holding that block; union
-  // mode takes every slot
+  // ---- misses (selected, not predicted) in ascending block order (wave 0),
+  // and the predicted slots whose states are merged (wave 1): saved mode
+  // takes slot p when P[p] is selected and p is the highest slot holding
+  // that block; union mode takes every slot
   if (w == 0) {
     int cnt = 0;
     for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
@@ -104,12 +104,15 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
       cnt += (int)__popcll(bal);
     }
     if (lane_id() == 0) s_nm = cnt;
+  } else if (w == 1) {
     for (int p0 = 0; p0 < kTailMaxK; p0 += STK_WAVE) {
-      const int p = p0 + lane_id();
-      const int pv = p < sp ? pids[p] : -1;
-      const int mv = pv >= 0 && pv < n ? map[pv] : 0;
-      const bool use = p < sp && (a.uni || ((mv & kSelFlag) && (mv & ~kSelFlag) == p + 1));
-      const uint64_t bal = __ballot(use);
+      uint64_t bal = 0ull;
+      if (p0 < sp) {
+        const int p = p0 + lane_id();
+        const int pv = p < sp ? pids[p] : -1;
+        const int mv = pv >= 0 && pv < n ? map[pv] : 0;
+        bal = __ballot(p < sp && (a.uni || ((mv & kSelFlag) && (mv & ~kSelFlag) == p + 1)));
+      }
       if (lane_id() == 0) s_used[p0 / STK_WAVE] = bal;
     }
   }
@@ -124,8 +127,16 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   auto tile = [&](int x) {
     return (((size_t)kvh * n + miss[x]) * a.kv.b) * D;
   };
+  // Every wave loads a tile here, without a branch: a wave with no miss
+  // reads one that is requested anyway (or block 0).  A branch around the
+  // loads would leave the compiler unable to tell the state prefetch's loads
+  // from these at the join, and the hits' arithmetic below would wait for
+  // the tiles.
   uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
-  if (ONE && w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
+  if constexpr (ONE) {
+    const size_t first = nm > 0 ? tile(w < nm ? w : w % nm) : (size_t)kvh * n * a.kv.b * D;
+    t.load(K + first, V + first, 0, kw, vw);
+  }
   // ---- the hits' (or, for union, every predicted row's) partial LSE sums
   uint64_t um4[kTailMaxK / 64];
 #pragma unroll
