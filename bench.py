@@ -7,9 +7,9 @@ strict repair -- the full path of the reference's ``overlap_run``
 (``benchmarks/run_benchmark.py:99-118``).  It runs as ``strict_topk.step``:
 one launch whose workgroups either score blocks or compute the predicted
 blocks' states, then one launch doing the top-K and the repair per query
-head.  The workload is config c3 (Qwen3-4B-like shape, 64K context, K=64,
-90 % prediction overlap, bf16), the configuration the north-star target is
-stated on.
+head.  The headline workload is config c3 (Qwen3-4B-like shape, 64K context,
+K=64, 90 % prediction overlap, bf16), the configuration the north-star
+target is stated on.
 
 Timing.  M consecutive decode steps are captured into one HIP graph, step i
 reading the i % M-th of M device copies of the inputs (identical values,
@@ -20,17 +20,25 @@ exactly --steps steps (--steps / M replays) bracketed by
 torch.cuda.synchronize().  The same construction times the same-work serial
 path (select, then attention over the selected blocks) and the drop-in
 two-stream composition; "hot" variants replay all M steps on one input copy
-(the reference's own method, caches warm).
+(the reference's own method, caches warm).  Configs c1, c2, c4 and c5 are
+timed the same way (stk_harness/suite.py) and reported under "configs".
+
+CPU leg (skipped with --no-cpu): the repository's torch-CPU port of the
+reference's serial path is timed on a bounded sample on all host cores, and
+the FP64 oracle checks every output the GPU legs produced (block IDs
+bit-exact, outputs within |err| <= 3e-4 + 3e-4 |ref|).
 
 Printed JSON line (one GPU):
-  value / ms_per_step   microseconds per full decode step (lower is better);
+  value / ms_per_step   microseconds per full c3 decode step (lower is better);
   serial_us             the serial path, paired ABBA replay timing;
   roofline              dominant kernel (k_front: select || speculate),
                         algorithmic bytes / average launch time measured here
-                        with HIP events on its stream;
+                        with HIP events on its stream; traffic from the
+                        committed rocprof counter runs;
   path_roofline         the whole step's algorithmic bytes against 8 TB/s;
-  cpu_baseline          this repository's torch-CPU port of the reference's
-                        serial path, timed on a bounded sample.
+  configs               c1, c2, c4, c5: speculative path vs serial;
+  parity                oracle check of every measured output (CPU leg);
+  cpu_baseline          the torch-CPU port of the serial path.
 """
 from __future__ import annotations
 
@@ -49,6 +57,8 @@ for _p in (ROOT / "strict-topk-overlap_amd", ROOT):
 import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
+TOL = "|err| <= 3e-4 + 3e-4 |ref| vs FP64"
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
@@ -65,7 +75,11 @@ def parse():
     ap.add_argument("--graph-steps", type=int, default=12,
                     help="decode steps per captured graph (and input copies)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU leg (CPU baseline and oracle parity)")
+    ap.add_argument("--no-suite", action="store_true", help="time c3 only")
+    ap.add_argument("--suite", default="c1,c2,c4,c5",
+                    help="comma-separated configs timed beside c3")
     return ap.parse_args()
 
 
@@ -86,6 +100,70 @@ def traffic_record(workload):
     return json.loads(path.read_text()).get(workload)
 
 
+def cpu_leg(args, step, c3_outs, cases):
+    """The CPU side: the FP64 oracle as the checker of every GPU output, and
+    the torch-CPU port of the serial path timed as the baseline."""
+    from oracle import cpu_path
+    from oracle import stk_oracle as O
+
+    def f64(t):
+        return t.double().numpy() if isinstance(t, torch.Tensor) else np.asarray(t, np.float64)
+
+    def err(out, expected):
+        o = out.double().numpy()
+        d = np.abs(o - expected)
+        return {"max_abs_err": float(d.max()),
+                "passed": bool((d <= 3e-4 + 3e-4 * np.abs(expected)).all() and
+                               np.isfinite(o).all())}
+
+    log("bench: oracle check of the c3 outputs")
+    cfg = step.cfg
+    q, k, v, lo, hi = step.host
+    qn, kn, vn = f64(q), f64(k), f64(v)
+    ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), cfg.topk)
+    ids_exact = bool(np.array_equal(step.selected.cpu().numpy(), ref_ids))
+    expected = O.attention(qn, kn, vn, ref_ids)
+    c3 = {key: err(out, expected) for key, out in c3_outs.items()}
+    parity = {"c3": {"ids_bit_exact": ids_exact,
+                     "max_abs_err": {k_: v_["max_abs_err"] for k_, v_ in c3.items()},
+                     "passed": ids_exact and all(v_["passed"] for v_ in c3.values())}}
+    for case in cases:
+        log(f"bench: oracle check of {case.name}")
+        res = {}
+        for label, kind, data in case.check:
+            if kind == "select":
+                cq, clo, chi, topk, ids = data
+                res[label] = {"passed": bool(np.array_equal(
+                    ids.numpy(), O.select_blocks(f64(cq), clo.numpy(), chi.numpy(), topk)))}
+            elif kind == "attention":
+                cq, ck, cv, ids, out = data
+                res[label] = err(out, O.attention(f64(cq), f64(ck), f64(cv), ids.numpy()))
+            elif kind == "signed_fused":
+                cq, ck, cv, sel, p, eps, out = data
+                cq, ck, cv = f64(cq), f64(ck), f64(cv)
+                st = O.speculate(cq, ck, cv, p.numpy(), mode="hybrid", mass_threshold=0.2,
+                                 keep_mass=True)
+                ref = O.repair_signed_fused(cq, ck, cv, sel.numpy(), p.numpy(), st,
+                                            max_extra_mass=eps)
+                res[label] = err(out, ref.output)
+        parity[case.name] = {
+            "passed": all(r["passed"] for r in res.values()),
+            "checks": len(res),
+            "max_abs_err": max((r.get("max_abs_err", 0.0) for r in res.values()), default=0.0),
+            "failed": sorted(l_ for l_, r in res.items() if not r["passed"]),
+        }
+        if not parity[case.name]["passed"]:
+            log(f"bench: {case.name} parity FAILED: {parity[case.name]['failed']}")
+    parity["tolerance"] = TOL
+
+    log(f"bench: CPU baseline (~{args.cpu_seconds:.0f} s)")
+    us, steps, threads = cpu_path.time_serial(q, k, v, lo, hi, cfg.topk, budget_s=args.cpu_seconds)
+    cpu = {"value": round(us, 1), "unit": "us/step", "cores": threads, "kind": "port",
+           "sample": f"{steps} serial decode steps of {cfg.name} (torch fp32 CPU: "
+                     "where/sum bound score, topk, gather-softmax attention)"}
+    return parity, cpu
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -96,7 +174,6 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("bench.py: no HIP device visible")
 
-    from oracle import stk_oracle as O
     from stk_harness import decode, timing
     from strict_topk import _lib
 
@@ -108,20 +185,6 @@ def main():
         f"overlap {args.overlap})")
     step = decode.gqa_step(args.config, args.overlap, args.seed, dev, sets=M)
     cfg = step.cfg
-    q, k, v, lo, hi = step.host
-
-    # ---- parity of every measured path against the FP64 oracle
-    log("bench: oracle selection and attention")
-    qn, kn, vn = (t.double().numpy() for t in (q, k, v))
-    ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), cfg.topk)
-    ids_exact = bool(np.array_equal(step.selected.cpu().numpy(), ref_ids))
-    expected = O.attention(qn, kn, vn, ref_ids)
-
-    def err(out):
-        o = out.double().cpu().numpy()
-        d = np.abs(o - expected)
-        return (float(d.max()), float((d / np.maximum(np.abs(expected), 1e-30)).max()),
-                bool((d <= 3e-4 + 3e-4 * np.abs(expected)).all() and np.isfinite(o).all()))
 
     def seq(fn, hot):
         return lambda: [fn(0 if hot else i) for i in range(M)]
@@ -132,13 +195,6 @@ def main():
         for hot in (False, True):
             key = name + ("_hot" if hot else "")
             graphs[key], outs[key] = timing.capture(seq(fn, hot))
-    parity = {}
-    for key, out in outs.items():
-        worst = max((err(o) for o in out), key=lambda e: e[0])
-        parity[key] = worst
-        if not (ids_exact and worst[2]):
-            sys.exit(f"bench: parity failed for {key} (ids exact {ids_exact}, "
-                     f"max abs err {worst[0]:.3g})")
 
     # ---- the timed region: exactly --steps fused decode steps (cold)
     g = graphs["fused"]
@@ -157,8 +213,8 @@ def main():
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     ms_per_step = e0.elapsed_time(e1) / (reps * M)
-    if not all(err(o)[2] for o in outs["fused"]):
-        sys.exit("bench: fused-path output changed during timing")
+    # outputs of the last step of every captured sequence, for the CPU leg
+    c3_outs = {key: out[-1].cpu() for key, out in outs.items()}
 
     log("bench: paired ABBA intervals")
     med, _ = timing.paired(graphs, replays=max(1, 120 // M), rounds=5, seed=args.seed)
@@ -209,23 +265,34 @@ def main():
             "kv_frac": round(by.kv_full / (full_us * 1e-6) / decode.HBM_PEAK, 4),
             "serial_bytes": by.serial,
             "serial_frac": round(by.serial / (per_step["serial"] * 1e-6) / decode.HBM_PEAK, 4)}
+    del graphs, g, g_front
 
-    cpu = None
+    # ---- the other configurations
+    cases, configs = [], {}
+    if not args.no_suite:
+        from stk_harness import suite
+        for name in [x for x in args.suite.split(",") if x]:
+            make = suite.CASES[name]
+            log(f"bench: config {name}")
+            case = make(dev, args.seed)
+            configs[name] = case.measure(seed=args.seed)
+            case.graphs = {}
+            cases.append(case)
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+
+    parity, cpu = None, None
     if not args.no_cpu:
-        from oracle import cpu_path
-        log(f"bench: CPU baseline (~{args.cpu_seconds:.0f} s)")
-        us, steps, threads = cpu_path.time_serial(q, k, v, lo, hi, cfg.topk,
-                                                  budget_s=args.cpu_seconds)
-        cpu = {"value": round(us, 1), "unit": "us/step", "cores": threads, "kind": "port",
-               "sample": f"{steps} serial decode steps of {cfg.name} (torch fp32 CPU: "
-                         "where/sum bound score, topk, gather-softmax attention)"}
+        parity, cpu = cpu_leg(args, step, c3_outs, cases)
+        if not parity["c3"]["passed"]:
+            sys.exit(f"bench: c3 parity failed: {json.dumps(parity['c3'])}")
 
     line = {
         "metric": "us/decode step full path (select+spec+repair) vs serial; HBM GB/s % of peak",
         "value": round(full_us, 3), "unit": "us/step", "n_gpus": 1, "steps": reps * M,
         "warmup": warm * M, "ms_per_step": round(ms_per_step, 6), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded CPU generator, hot blocks +1.5 along the group-mean query)",
+        "data": "synthetic (seeded generators, hot blocks +1.5 along the group-mean query)",
         "config": {"workload": f"{cfg.name}: Hq={cfg.hq} Hkv={cfg.hkv} D={cfg.dim} "
                                f"B={cfg.block} N={cfg.blocks} K={cfg.topk} "
                                f"overlap={args.overlap}, fused select||speculate + "
@@ -238,9 +305,8 @@ def main():
         "paired_us_per_step": per_step,
         "roofline": roofline,
         "path_roofline": path,
-        "parity": {"ids_bit_exact": ids_exact,
-                   "max_abs_err": {k_: v_[0] for k_, v_ in parity.items()},
-                   "tolerance": "|err| <= 3e-4 + 3e-4 |ref| vs FP64"},
+        "configs": configs,
+        "parity": parity,
         "wall_ms_timed_region": round(wall_ms, 2),
         "cpu_baseline": cpu,
     }

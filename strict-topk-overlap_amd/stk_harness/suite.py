@@ -1,0 +1,265 @@
+"""Timed decode steps for configs c1, c2, c4 and c5 (c3 is bench.py's headline).
+
+Each case builds its seeded inputs on the device, captures its speculative
+path and the same-work serial path into HIP graphs, and times them with
+randomized ABBA pairs (``timing.paired``).  The reference strategy each
+config exercises (SURVEY's scope table; BASELINE.json ``configs``):
+
+  c1  selector.select_blocks || kernels.speculate('saved') -> kernels.repair,
+      the same with fused.repair_fused (two streams, the drop-in
+      composition), and strict_topk.step.speculative_step (fused);
+      serial = exact_attention(select).
+  c2  gqa.select_blocks || gqa.partials -> gqa.repair_saved (two streams, the
+      drop-in composition) and strict_topk.step.speculative_step (fused);
+      serial = gqa.exact(select).
+  c4  gqa_hierarchical.partials(P) -> repair_saved_shared, selection given:
+      the reference's shared selector is the QSA indexer, outside this path,
+      so the selected set (top-2048 of the bound score summed over all heads,
+      ties to the lower index, one row shared by every head as
+      repair_saved_shared requires) is built once outside timing and both the
+      speculative and the serial path (gqa_hierarchical.exact) start from it.
+  c5  16 requests with 8K-128K contexts and overlap U[0.5, 1]: per request
+      gqa.select_blocks || kernels.speculate('hybrid', 0.2, keep_mass=True)
+      -> signed_fused.repair_signed_fused with max_extra_mass 0.01 and 0
+      (strict); serial = gqa.exact(select) per request.
+
+No checking happens here: every case keeps host copies of its inputs and the
+device outputs of its captured graphs, which bench.py's CPU leg compares with
+the FP64 oracle.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from strict_topk import fused, gqa, gqa_hierarchical, kernels, selector, signed_fused
+from strict_topk import step as step_mod
+
+from . import timing
+from .configs import C5, CONFIGS, make_qkv, perturb
+from .decode import HBM_PEAK, GqaStep, unique_pairs
+
+
+@dataclass
+class Case:
+    name: str
+    strategy: str
+    graphs: dict                     # name -> captured graph (M steps each)
+    steps_per_graph: int
+    bytes_full: int
+    bytes_kv: int
+    bytes_serial: int
+    primary: str = ""                # the path reported as the speculative step
+    check: list = field(default_factory=list)   # (label, kind, data) for the CPU leg
+    notes: str = ""
+
+    def measure(self, replays=20, rounds=3, seed=20261103):
+        med, _ = timing.paired(self.graphs, replays=replays, rounds=rounds, seed=seed,
+                               warm_ms=50.0)
+        per = {k: v / self.steps_per_graph for k, v in med.items()}
+        full = per[self.primary]
+        return {
+            "strategy": self.strategy, "primary": self.primary,
+            "us_per_step": {k: round(v, 3) for k, v in per.items()},
+            "speedup_vs_serial": round(per["serial"] / full, 4),
+            "algorithmic_bytes": self.bytes_full, "kv_bytes": self.bytes_kv,
+            "serial_bytes": self.bytes_serial,
+            "frac": round(self.bytes_full / (full * 1e-6) / HBM_PEAK, 4),
+            "kv_frac": round(self.bytes_kv / (full * 1e-6) / HBM_PEAK, 4),
+            "notes": self.notes,
+        }
+
+
+def _host(*ts):
+    return tuple(t.detach().cpu() for t in ts)
+
+
+def _seq(fn, m):
+    return lambda: [fn(i) for i in range(m)]
+
+
+# ------------------------------------------------------------------ c1
+def case_c1(dev, seed=20261103):
+    c = CONFIGS["c1"]
+    q, k, v, lo, hi = (t.to(dev) for t in make_qkv(c.hq, c.hkv, c.dim, c.block, c.blocks,
+                                                    c.dtype, c.hot, seed))
+    sel = selector.select_blocks(q, lo, hi, c.topk)
+    p = perturb(sel.cpu(), c.blocks, c.sp, c.overlaps[0], seed).to(dev)
+    ss, ps = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def full(repair):
+        return lambda i: timing.overlap_run(
+            lambda: selector.select_blocks(q, lo, hi, c.topk),
+            lambda: kernels.speculate(q, k, v, p, "saved"),
+            lambda a, st: repair(q, k, v, a, p, st).output, ss, ps)
+
+    m = 4
+    graphs, outs = {}, {}
+    for name, fn in (("split", full(kernels.repair)), ("fused", full(fused.repair_fused)),
+                     ("step", lambda i: step_mod.speculative_step(q, k, v, lo, hi, p,
+                                                                  c.topk).output),
+                     ("serial", lambda i: kernels.exact_attention(
+                         q, k, v, selector.select_blocks(q, lo, hi, c.topk)))):
+        graphs[name], outs[name] = timing.capture(_seq(fn, m))
+    tile = 2 * c.block * c.dim * 2
+    pa, sa = p.cpu().numpy(), sel.cpu().numpy()
+    kv = (unique_pairs(pa, 1) + sum(len(np.setdiff1d(a, b)) for a, b in zip(sa, pa))) * tile
+    meta = 2 * c.hkv * c.blocks * c.dim * 4
+    states = c.hq * c.sp * (c.dim + 2) * 4 * 2
+    small = c.hq * c.dim * (2 + 4) + 4 * (sa.size + pa.size)
+    case = Case("c1", "select || speculate('saved') -> repair (split / repair_fused, two "
+                "streams; and the fused step)", graphs, m,
+                kv + meta + states + small, kv, meta + unique_pairs(sa, 1) * tile + small,
+                primary="step")
+    hq_, hk_, hv_ = _host(q, k, v)
+    case.check = [("ids", "select", (hq_, *_host(lo, hi), c.topk, sel.cpu()))]
+    for name in graphs:
+        case.check.append((name, "attention", (hq_, hk_, hv_, sel.cpu(), outs[name][-1].cpu())))
+    return case
+
+
+# ------------------------------------------------------------------ c2
+def case_c2(dev, seed=20261103):
+    m = 12
+    st = GqaStep(CONFIGS["c2"], 0.9, seed, dev, repair="saved", sets=m)
+    graphs, outs = {}, {}
+    for name, fn in (("composed", st.full), ("fused", st.fused), ("serial", st.serial)):
+        graphs[name], outs[name] = timing.capture(_seq(fn, m))
+    by = st.bytes()
+    case = Case("c2", "gqa.select_blocks || gqa.partials -> gqa.repair_saved (composed, two "
+                "streams; and the fused step)", graphs, m, by.full, by.kv_full, by.serial,
+                primary="fused", notes=f"inputs rotated over {m} device copies")
+    q, k, v, lo, hi = st.host
+    case.check = [("ids", "select", (q, lo, hi, st.cfg.topk, st.selected.cpu()))]
+    for name in graphs:
+        case.check.append((name, "attention", (q, k, v, st.selected.cpu(), outs[name][-1].cpu())))
+    return case
+
+
+# ------------------------------------------------------------------ c4
+def _shared_selection(q, lo, hi, g, topk):
+    """Top-k blocks of the bound score summed over every query head (FP32
+    torch, ties to the lower index), one row repeated for all heads:
+    repair_saved_shared's contract is identical rows for every head
+    (reference strict_topk/gqa_hierarchical.py:137-143), as a per-layer
+    indexer produces."""
+    qg = q.float().view(lo.shape[0], g, -1)
+    s = (torch.einsum("kgd,knd->kgn", qg.clamp(min=0), hi) +
+         torch.einsum("kgd,knd->kgn", qg.clamp(max=0), lo)).sum((0, 1))
+    order = torch.sort(-s, stable=True).indices[:topk]
+    ids = torch.sort(order).values.to(torch.int32)
+    return ids.expand(q.shape[0], -1).contiguous()
+
+
+def case_c4(dev, seed=20261103):
+    c = CONFIGS["c4"]
+    g = c.group
+    q, k, v, lo, hi = make_qkv(c.hq, c.hkv, c.dim, c.block, c.blocks, c.dtype, c.hot, seed,
+                               device=dev)
+    sel = _shared_selection(q, lo, hi, g, c.topk)
+    prow = perturb(sel[:1].cpu(), c.blocks, c.sp, c.overlaps[0], seed)
+    p = prow.expand(c.hq, -1).contiguous().to(dev)
+    m = 2
+
+    def full(i):
+        st = gqa_hierarchical.partials(q, k, v, p)
+        return gqa_hierarchical.repair_saved_shared(q, k, v, sel, p, st)
+
+    graphs, outs = {}, {}
+    for name, fn in (("speculative", full),
+                     ("serial", lambda i: gqa_hierarchical.exact(q, k, v, sel))):
+        graphs[name], outs[name] = timing.capture(_seq(fn, m))
+    tile = 2 * c.block * c.dim * 2
+    sa, pa = sel.cpu().numpy(), p.cpu().numpy()
+    u_p = unique_pairs(pa, g)
+    u_miss = sum(len(np.setdiff1d(sa[x * g], pa[x * g])) for x in range(c.hkv))
+    states = c.hq * c.sp * (c.dim + 2) * 4
+    hits = sum(len(np.intersect1d(a, b)) for a, b in zip(sa, pa))
+    small = c.hq * c.dim * (2 + 4) + 4 * (sa.size + pa.size)
+    kv = (u_p + u_miss) * tile
+    case = Case("c4", "gqa_hierarchical.partials(P) -> repair_saved_shared (selection given)",
+                graphs, m, kv + states + hits * (c.dim + 2) * 4 + small, kv,
+                unique_pairs(sa, g) * tile + small, primary="speculative",
+                notes="selection shared by all heads, built outside timing (head-summed "
+                      "bound score); lo/hi not read")
+    hq_, hk_, hv_ = _host(q, k, v)
+    for name in graphs:
+        case.check.append((name, "attention", (hq_, hk_, hv_, sel.cpu(), outs[name][-1].cpu())))
+    return case
+
+
+# ------------------------------------------------------------------ c5
+def case_c5(dev, seed=20261103):
+    cf = C5
+    rng = np.random.default_rng(seed)
+    blocks = rng.integers(cf["min_blocks"], cf["max_blocks"] + 1, size=cf["requests"])
+    overlaps = rng.uniform(cf["min_overlap"], cf["max_overlap"], size=cf["requests"])
+    reqs = []
+    for r in range(cf["requests"]):
+        q, k, v, lo, hi = make_qkv(cf["hq"], cf["hkv"], cf["dim"], cf["block"], int(blocks[r]),
+                                   cf["dtype"], True, seed + 101 * r, device=dev)
+        sel = gqa.select_blocks(q, lo, hi, cf["topk"])
+        p = perturb(sel.cpu(), int(blocks[r]), cf["topk"], float(overlaps[r]), seed + r).to(dev)
+        reqs.append((q, k, v, lo, hi, sel, p))
+    ss, ps = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def full(eps):
+        def run(i):
+            outs = []
+            for q, k, v, lo, hi, _, p in reqs:
+                outs.append(timing.overlap_run(
+                    lambda: gqa.select_blocks(q, lo, hi, cf["topk"]),
+                    lambda: kernels.speculate(q, k, v, p, "hybrid", 0.2, keep_mass=True),
+                    lambda a, st: signed_fused.repair_signed_fused(
+                        q, k, v, a, p, st, max_extra_mass=eps).output, ss, ps))
+            return outs
+        return run
+
+    def serial(i):
+        return [gqa.exact(q, k, v, gqa.select_blocks(q, lo, hi, cf["topk"]))
+                for q, k, v, lo, hi, _, _ in reqs]
+
+    graphs, outs = {}, {}
+    for name, fn in (("signed_eps0.01", full(0.01)), ("signed_strict", full(0.0)),
+                     ("serial", serial)):
+        graphs[name], outs[name] = timing.capture(lambda fn=fn: fn(0))
+    g = cf["hq"] // cf["hkv"]
+    tile = 2 * cf["block"] * cf["dim"] * 2
+    full_b = kv_b = ser_b = 0
+    for (q, k, v, lo, hi, sel, p), n in zip(reqs, blocks):
+        sa, pa = sel.cpu().numpy(), p.cpu().numpy()
+        u_p, u_a = unique_pairs(pa, g), unique_pairs(sa, g)
+        u_union = unique_pairs(np.concatenate([sa, pa], axis=1), g)
+        meta = 2 * cf["hkv"] * int(n) * cf["dim"] * 4
+        small = cf["hq"] * cf["dim"] * (2 + 4) + 4 * (sa.size + pa.size)
+        # misses are added and wrong blocks subtracted: every tile of P u A is read
+        kv = u_union * tile
+        kv_b += kv
+        full_b += kv + meta + cf["hq"] * cf["topk"] * (cf["dim"] + 2) * 4 * 2 + small
+        ser_b += meta + u_a * tile + small
+    case = Case("c5", "per request: gqa.select_blocks || kernels.speculate('hybrid', 0.2, "
+                "keep_mass) -> signed_fused.repair_signed_fused (eps 0.01 and strict)",
+                graphs, 1, full_b, kv_b, ser_b, primary="signed_eps0.01",
+                notes=f"16 requests, contexts {int(blocks.min()) * 32}-{int(blocks.max()) * 32} "
+                      "tokens; one graph replay = one batched decode step")
+    for r, (q, k, v, lo, hi, sel, p) in enumerate(reqs):
+        hq_, hlo, hhi = _host(q, lo, hi)
+        case.check.append((f"ids[{r}]", "select", (hq_, hlo, hhi, cf["topk"], sel.cpu())))
+        need = torch.unique(torch.cat([sel.flatten(), p.flatten()]).long())
+        ks, vs = _host(k[:, need], v[:, need])
+        remap = torch.full((int(blocks[r]),), -1, dtype=torch.int64)
+        remap[need.cpu()] = torch.arange(len(need))
+        sel_r = remap[sel.cpu().long()].to(torch.int32)
+        p_r = remap[p.cpu().long()].to(torch.int32)
+        case.check.append((f"strict[{r}]", "attention",
+                           (hq_, ks, vs, sel_r, outs["signed_strict"][r].cpu())))
+        case.check.append((f"serial[{r}]", "attention",
+                           (hq_, ks, vs, sel_r, outs["serial"][r].cpu())))
+        case.check.append((f"eps0.01[{r}]", "signed_fused",
+                           (hq_, ks, vs, sel_r, p_r, 0.01, outs["signed_eps0.01"][r].cpu())))
+    return case
+
+
+CASES = {"c1": case_c1, "c2": case_c2, "c4": case_c4, "c5": case_c5}
