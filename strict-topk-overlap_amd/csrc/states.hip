@@ -8,7 +8,7 @@
 //   strict_topk/kernels.py:94-117  _group        -> k_hybrid_group
 //   strict_topk/kernels.py:263-356 _mass_only / _compact_group / _compact_values
 //   strict_topk/kernels.py:250-260 _touch        -> k_touch
-#include "states_tok.hpp"
+#include "states_pack.hpp"
 #include "api.hpp"
 
 namespace stk {
@@ -68,6 +68,12 @@ __global__ __launch_bounds__(256) void k_states(StatesArgs a) {
 template <typename T, int NCH, int UP, typename I, bool GROUP, bool ONE>
 __global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_states_tok(StatesArgs a) {
   states_tok_wg<T, NCH, UP, I, GROUP, ONE>(a, a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x);
+}
+
+// Small blocks (B = 4 or 8): one wave per (query head, 32-token pack).
+template <typename T, int NCH, int BB, typename I>
+__global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_states_pack(StatesArgs a) {
+  states_pack_wg<T, NCH, BB, I>(a, a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x);
 }
 
 // LSE merge arguments (kernels.py:74-91, merge_partials :437-442).
@@ -567,6 +573,24 @@ static int launch_states(StatesArgs& a, int dtype, bool with_v, bool slot, hipSt
   const int G = a.hq / a.hkv;
   const uintptr_t align = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
                           reinterpret_cast<uintptr_t>(a.v);
+  const int pnch = with_v && !slot ? pack_nch(dtype, a.d, a.b, align) : 0;
+  if (pnch) {
+    const int64_t packs = (int64_t)a.hq * ((a.s + 32 / a.b - 1) / (32 / a.b));
+    const int pgrid = (int)((packs + 3) / 4);
+    a.remap = pgrid >= 8 ? 1 : 0;
+    const bool i64 = a.itype == IT_I64;
+#define STK_PACK(BBV)                                                                              \
+    STK_DISPATCH_TOK(dtype, pnch, {                                                                \
+      if (i64)                                                                                     \
+        hipLaunchKernelGGL((k_states_pack<T, NCH, BBV, int64_t>), dim3(pgrid), dim3(256), 0, st, a); \
+      else                                                                                         \
+        hipLaunchKernelGGL((k_states_pack<T, NCH, BBV, int32_t>), dim3(pgrid), dim3(256), 0, st, a); \
+    })
+    if (a.b == 4) STK_PACK(4);
+    else STK_PACK(8);
+#undef STK_PACK
+    return stk_check_launch("k_states_pack");
+  }
   const int nch = with_v && !slot && !a.slot_in ? tok_nch(dtype, a.d, a.b, align) : 0;
   if (nch) {
     // grouped: one tile read per KV group when the group's rows fit one pass

@@ -119,7 +119,12 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
   const T* kb = reinterpret_cast<const T*>(a.k) + off;
   const T* vb = reinterpret_cast<const T*>(a.v) + off;
   uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
-  if constexpr (ONE) t.load(kb, vb, 0, kw, vw);   // the whole block, once
+  if constexpr (ONE) {
+    t.load(kb, vb, 0, kw, vw);   // the whole block, once
+    // all of the tile's loads are issued before any arithmetic (the
+    // scheduler would otherwise sink the V loads below the Q.K products)
+    __builtin_amdgcn_sched_barrier(0);
+  }
   // heads after the owner, lowest first
   uint64_t rest = found & ~(1ull << hl);
   int cur = hl;

@@ -376,6 +376,63 @@ def test_gqa_validation_messages():
         gqa.partials(q, k[:2], k[:2], ids.float())
 
 
+# ------------------------------------------------- packed small-block states
+@pytest.mark.parametrize("b,d,dtype,itype", [
+    (4, 128, torch.bfloat16, torch.int32),
+    (8, 64, torch.float16, torch.int64),
+    (4, 256, torch.bfloat16, torch.int64),
+    (8, 128, torch.bfloat16, torch.int32),
+])
+def test_packed_small_block_states(b, d, dtype, itype):
+    """Blocks of 4 or 8 tokens run 32-token packs per wave: per-block states
+    against the oracle, with a ragged row, invalid IDs, both active-mask
+    kinds, and the hierarchical exact / saved repair (skip mode) on top."""
+    from strict_topk import gqa_hierarchical as hier
+    from strict_topk.kernels import block_partials
+    gen = torch.Generator().manual_seed(11 + b + d)
+    hq, hkv, n, s = 6, 2, 300, 37   # 37 positions: the last pack is partial
+    q = torch.randn((hq, d), generator=gen).to(dtype)
+    k = torch.randn((hkv, n, b, d), generator=gen).to(dtype)
+    v = torch.randn(k.shape, generator=gen).to(dtype)
+    valid = torch.stack([torch.randperm(n, generator=gen)[:s] for _ in range(hq)]).to(itype)
+    ids = valid.clone()
+    ids[1, 5] = -1
+    ids[2, 36] = -1
+    qn, kn, vn = np_(q, k, v)
+    ref = O.block_states(qn, kn, vn, C.ids_np(ids))
+    qd, kd, vd, idd = dev(q, k, v, ids)
+
+    def same(st, r, what):
+        m, l, u = (x.cpu().double().numpy() for x in (st.m, st.l, st.u))
+        off = np.isinf(r.m)
+        assert np.isinf(m[off]).all() and (m[off] < 0).all(), what
+        assert (l[off] == 0).all() and (u[off] == 0).all(), what
+        np.testing.assert_allclose(m[~off], r.m[~off], rtol=1e-5, atol=1e-5, err_msg=what)
+        np.testing.assert_allclose(l, r.l, rtol=1e-4, atol=1e-6, err_msg=what)
+        np.testing.assert_allclose(u, r.u, rtol=1e-4, atol=1e-4, err_msg=what)
+
+    same(block_partials(qd, kd, vd, idd), ref, "states")
+    big = idd.clone()
+    big[0, 3] = n + 7   # out of range: empty state, no memory read
+    st = block_partials(qd, kd, vd, big)
+    assert torch.isinf(st.m[0, 3]) and st.l[0, 3] == 0 and (st.u[0, 3] == 0).all()
+    mask = torch.zeros((hq, s), dtype=torch.bool)
+    mask[:, ::3] = True
+    same(block_partials(qd, kd, vd, idd, mask.to(DEV)),
+         O.block_states(qn, kn, vn, C.ids_np(ids), mask.numpy()), "slot mask")
+    head = torch.tensor([True, False, True, True, False, True])
+    same(block_partials(qd, kd, vd, idd, head.to(DEV)),
+         O.block_states(qn, kn, vn, C.ids_np(ids), head.numpy()), "head mask")
+    an = C.ids_np(valid)
+    expected = O.attention(qn, kn, vn, an)
+    a = valid.to(DEV)
+    check(hier.exact(qd, kd, vd, a), expected, "packed exact")
+    for hits in (0, s // 2, s):
+        p = C.prediction_rows(valid, n, s, hits).to(itype).to(DEV)
+        check(hier.repair_saved(qd, kd, vd, a, p, hier.partials(qd, kd, vd, p)), expected,
+              ("packed saved", hits))
+
+
 # ------------------------------------------------------------ hierarchical
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_hierarchical_paths(dtype):
