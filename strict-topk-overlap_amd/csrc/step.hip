@@ -85,10 +85,11 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
   s->up = tok_up(b);
   s->one = b == 16 * s->up;
   if (topk > kTailMaxK || sp > kTailMaxK) return "the fused step takes at most 256 selected and predicted IDs";
-  // predicted states held by the tail: sp rows over 512 / D row groups
-  const int rows = (sp + kTailThreads / d - 1) / (kTailThreads / d);
-  if (rows > 32) return "the fused step needs SP * D <= 16384";
-  s->rpt = rows <= 16 ? 16 : 32;
+  // predicted states held by the tail: sp rows over 2048 / D rows per pass
+  const int per_pass = kTailThreads * 4 / d;
+  const int rows = (sp + per_pass - 1) / per_pass;
+  if (rows > 16) return "the fused step needs SP * D <= 32768";
+  s->rpt = rows <= 4 ? 4 : 16;
   return nullptr;
 }
 
@@ -107,14 +108,14 @@ int launch_front_gt(const FrontArgs& f, const StepShape& s, hipStream_t st) {
 template <typename T, int NCH, int UP, bool ONE>
 int launch_tail(const TailArgs& t, const StepShape& s, hipStream_t st) {
   const dim3 grid(t.kv.hq), block(kTailThreads);
-  if (s.kpt == 4 && s.rpt == 16)
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 4, 16>), grid, block, 0, st, t);
+  if (s.kpt == 4 && s.rpt == 4)
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 4, 4>), grid, block, 0, st, t);
   else if (s.kpt == 4)
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 4, 32>), grid, block, 0, st, t);
-  else if (s.rpt == 16)
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 16, 16>), grid, block, 0, st, t);
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 4, 16>), grid, block, 0, st, t);
+  else if (s.rpt == 4)
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 16, 4>), grid, block, 0, st, t);
   else
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 16, 32>), grid, block, 0, st, t);
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 16, 16>), grid, block, 0, st, t);
   return stk_check_launch("k_tail");
 }
 

@@ -38,19 +38,22 @@ struct TailArgs {
   float* out;                             // [hq, d]
 };
 
-// KPT keys per thread (n <= 512 * KPT); RPT predicted rows per thread
-// (sp <= RPT * 512 / D); ONE: a block is one token chunk.
+// KPT keys per thread (n <= 512 * KPT); RPT predicted-state rows per thread,
+// four columns each (sp <= RPT * 2048 / D); ONE: a block is one token chunk.
 template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
 __device__ __forceinline__ void tail_head(const TailArgs& a) {
   using TT = TokTile<T, NCH, UP>;
   constexpr int D = TT::D;
-  constexpr int RG = kTailThreads / D;    // row groups of the state prefetch
+  constexpr int TPR = D / 4;              // threads per state row (16-byte loads)
+  constexpr int RG = kTailThreads / TPR;  // rows per pass of the state prefetch
   __shared__ int map[kTailMapN];
   __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
+  __shared__ float s_pm[kTailMaxK], s_pl[kTailMaxK];
   __shared__ TopkLds tl;
   __shared__ int s_nm;
   __shared__ uint64_t s_used[kTailMaxK / 64];   // predicted slots whose state is merged
-  __shared__ float s_hmax[kTailWaves], s_hl[RG], s_hu[RG][D];
+  __shared__ float s_hmax[kTailWaves], s_hl[RG];
+  __shared__ __align__(16) float s_hu[RG][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_wu[kTailWaves][D];
   const int h = blockIdx.x;
   const int n = a.kv.n, sp = a.sp;
@@ -64,20 +67,25 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   t.init();
   uint32_t qw[TT::QW];
   t.load_q(reinterpret_cast<const T*>(a.kv.q) + (size_t)h * D, qw);
-  const int dcol = tid % D, rg = tid / D;
-  float um[RPT], ul[RPT], uu[RPT];
+  // predicted (m, l) once per slot (to LDS below); u rows as 16-byte loads,
+  // thread (rg, c4) holding columns 4*c4 .. 4*c4+3 of rows rg + RG*j
+  const float pmv = ld_or(a.pm, (int64_t)h * sp + tid, tid < sp, -INFINITY);
+  const float plv = ld_or(a.pl, (int64_t)h * sp + tid, tid < sp, 0.f);
+  const int c4 = tid % TPR, rg = tid / TPR;
+  float4 uu[RPT];
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int r = rg + RG * j;
-    const bool on = r < sp;
-    const int64_t row = (int64_t)h * sp + (on ? r : 0);
-    um[j] = ld_or(a.pm, row, on, -INFINITY);
-    ul[j] = ld_or(a.pl, row, on, 0.f);
-    uu[j] = ld_or(a.pu, row * D + dcol, on, 0.f);
+    const int64_t row = (int64_t)h * sp + (r < sp ? r : 0);
+    uu[j] = *reinterpret_cast<const float4*>(a.pu + row * D + 4 * c4);
   }
   // ---- membership map: max predicted slot + 1 per block ID
   for (int i = tid; i < n; i += kTailThreads) map[i] = 0;
-  if (tid < sp) pids[tid] = pid;
+  if (tid < sp) {
+    pids[tid] = pid;
+    s_pm[tid] = pmv;
+    s_pl[tid] = plv;
+  }
   __syncthreads();
   if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
   // ---- exact top-K (its first barrier orders the map writes above)
@@ -127,28 +135,23 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   auto tile = [&](int x) {
     return (((size_t)kvh * n + miss[x]) * a.kv.b) * D;
   };
-  // Every wave loads a tile here, without a branch: a wave with no miss
-  // reads one that is requested anyway (or block 0).  A branch around the
-  // loads would leave the compiler unable to tell the state prefetch's loads
-  // from these at the join, and the hits' arithmetic below would wait for
-  // the tiles.
   uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
-  if constexpr (ONE) {
-    const size_t first = nm > 0 ? tile(w < nm ? w : w % nm) : (size_t)kvh * n * a.kv.b * D;
-    t.load(K + first, V + first, 0, kw, vw);
-  }
+  if (ONE && w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
   // ---- the hits' (or, for union, every predicted row's) partial LSE sums
   uint64_t um4[kTailMaxK / 64];
 #pragma unroll
   for (int x = 0; x < kTailMaxK / 64; ++x) um4[x] = s_used[x];
   bool used[RPT];
+  float um[RPT];
   float hm = -INFINITY;
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
-    const int r = rg + RG * j;   // < 32 * RG <= 256
-    const uint64_t word = um4[0] * (r < 64) | um4[1] * (r >= 64 && r < 128) |
-                          um4[2] * (r >= 128 && r < 192) | um4[3] * (r >= 192);
-    used[j] = (word >> (r & 63)) & 1ull;
+    const int r = rg + RG * j;   // < 16 * RG <= 512
+    const int rr = r < kTailMaxK ? r : 0;
+    const uint64_t word = um4[0] * (rr < 64) | um4[1] * (rr >= 64 && rr < 128) |
+                          um4[2] * (rr >= 128 && rr < 192) | um4[3] * (rr >= 192);
+    used[j] = r < sp && ((word >> (rr & 63)) & 1ull);
+    um[j] = s_pm[rr];
     hm = used[j] ? fmaxf(hm, um[j]) : hm;
   }
   hm = wave_max_u(hm);
@@ -157,15 +160,17 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   float mh = -INFINITY;
 #pragma unroll
   for (int x = 0; x < kTailWaves; ++x) mh = fmaxf(mh, s_hmax[x]);
-  float hl = 0.f, hu = 0.f;
+  float hl = 0.f;
+  float4 hu = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
+    const int r = rg + RG * j;
     const float wt = used[j] ? wexp(um[j], mh) : 0.f;
-    hl += wt * ul[j];
-    hu += wt * uu[j];
+    hl += wt * s_pl[r < kTailMaxK ? r : 0];
+    hu.x += wt * uu[j].x; hu.y += wt * uu[j].y; hu.z += wt * uu[j].z; hu.w += wt * uu[j].w;
   }
-  s_hu[rg][dcol] = hu;
-  if (dcol == 0) s_hl[rg] = hl;
+  *reinterpret_cast<float4*>(&s_hu[rg][4 * c4]) = hu;
+  if (c4 == 0) s_hl[rg] = hl;
   // ---- the misses' states with the online softmax
   float m = -INFINITY, l = 0.f, acc[TT::DPL];
 #pragma unroll
