@@ -65,9 +65,9 @@ __global__ __launch_bounds__(256) void k_states(StatesArgs a) {
   if (WITH_V) t.store(a.u + row * a.d, acc);
 }
 
-template <typename T, int NCH, int UP, typename I, bool GROUP, bool ONE>
+template <typename T, int NCH, int UP, typename I, bool ONE>
 __global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_states_tok(StatesArgs a) {
-  states_tok_wg<T, NCH, UP, I, GROUP, ONE>(a, a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x);
+  states_tok_wg<T, NCH, UP, I, ONE>(a, a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x);
 }
 
 // Small blocks (B = 4 or 8): one wave per (query head, 32-token pack).
@@ -593,20 +593,14 @@ static int launch_states(StatesArgs& a, int dtype, bool with_v, bool slot, hipSt
   }
   const int nch = with_v && !slot && !a.slot_in ? tok_nch(dtype, a.d, a.b, align) : 0;
   if (nch) {
-    // grouped: one tile read per KV group when the group's rows fit one pass
-    const bool group = !a.active && G > 1 && G <= 64 && (int64_t)G * a.s <= 4 * STK_WAVE;
     const bool i64 = a.itype == IT_I64;
     const bool one = tok_up(a.b) == 1;
 #define STK_TOK(UPV, ONE)                                                                       \
     STK_DISPATCH_TOK(dtype, nch, {                                                              \
-      if (group && i64)                                                                         \
-        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int64_t, true, ONE>), dim3(grid), dim3(256), 0, st, a); \
-      else if (group)                                                                           \
-        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int32_t, true, ONE>), dim3(grid), dim3(256), 0, st, a); \
-      else if (i64)                                                                             \
-        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int64_t, false, ONE>), dim3(grid), dim3(256), 0, st, a); \
+      if (i64)                                                                                  \
+        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int64_t, ONE>), dim3(grid), dim3(256), 0, st, a); \
       else                                                                                      \
-        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int32_t, false, ONE>), dim3(grid), dim3(256), 0, st, a); \
+        hipLaunchKernelGGL((k_states_tok<T, NCH, UPV, int32_t, ONE>), dim3(grid), dim3(256), 0, st, a); \
     })
     if (a.b == 16) STK_TOK(1, true);     // whole block in one chunk
     else if (one) STK_TOK(1, false);

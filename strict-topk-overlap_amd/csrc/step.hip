@@ -7,7 +7,7 @@
 //   k_front        one grid whose workgroups are either scoring workgroups
 //                  (bound score of a chunk of blocks -> 64-bit keys) or
 //                  speculation workgroups (per-block softmax states of the
-//                  predicted blocks, one K/V read per KV group), the two
+//                  predicted blocks, one wave per (query head, slot)), the two
 //                  roles interleaved evenly inside every XCD so both
 //                  streams of HBM traffic run side by side on all of them;
 //   k_tail         one workgroup per query head: exact top-K of the head's
@@ -31,7 +31,7 @@ struct FrontArgs {
   int score_wgs, total_wgs;
 };
 
-template <typename T, int NCH, int UP, bool ONE, int P, int STEPS, int GT, bool GROUP>
+template <typename T, int NCH, int UP, bool ONE, int P, int STEPS, int GT>
 __global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_front(FrontArgs a) {
   // Workgroups are dealt round-robin over the 8 XCDs; roles are interleaved
   // on an XCD-contiguous logical index, so every XCD gets an even mix of
@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_front(FrontArgs a) {
   if (upto > before)
     score_wg<T, P, STEPS, true, GT>(a.sc, before);
   else
-    states_tok_wg<T, NCH, UP, int32_t, GROUP, ONE>(a.st, i - upto);
+    states_tok_wg<T, NCH, UP, int32_t, ONE>(a.st, i - upto);
 }
 
 template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
@@ -60,7 +60,7 @@ namespace {
 
 struct StepShape {
   int nch, passes, steps, gt, kpt, up, rpt;
-  bool group, one;
+  bool one;
 };
 
 // Shape plan of the fused step, or a message saying why it is not supported.
@@ -74,11 +74,8 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
   if (n > 8192) return "the fused step supports at most 8192 blocks";
   if (topk < 1 || topk > n || sp < 1) return "bad topk or predicted width";
   const int G = hq / hkv;
-  if (G > 64 || (G > 1 && G * sp > 4 * STK_WAVE))
-    return "the fused step needs (Hq/Hkv) * SP <= 256";
   s->passes = d / 64;
   s->steps = s->passes <= 2 ? 2 : 1;
-  s->group = G > 1;
   s->gt = G == 1 ? 1 : (G == 2 ? 2 : (s->passes <= 2 ? 4 : 2));
   if (s->passes > 2 && s->gt > 2) s->gt = 2;
   s->kpt = n <= kTailThreads * 4 ? 4 : 16;
@@ -96,12 +93,12 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
 template <typename T, int NCH, int UP, bool ONE, int P, int STEPS>
 int launch_front_gt(const FrontArgs& f, const StepShape& s, hipStream_t st) {
   const dim3 grid(f.total_wgs), block(256);
-  if (!s.group)
-    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 1, false>), grid, block, 0, st, f);
+  if (s.gt == 1)
+    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 1>), grid, block, 0, st, f);
   else if (s.gt == 2)
-    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 2, true>), grid, block, 0, st, f);
+    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 2>), grid, block, 0, st, f);
   else
-    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 4, true>), grid, block, 0, st, f);
+    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 4>), grid, block, 0, st, f);
   return stk_check_launch("k_front");
 }
 

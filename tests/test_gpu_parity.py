@@ -534,6 +534,7 @@ def test_touch_kv_checksums():
     (12, 1, 700, 16, 64, 20, 0.0, torch.bfloat16, False),     # G = 12, no hits, B = 16
     (8, 2, 400, 64, 128, 32, 0.9, torch.bfloat16, False),     # B = 64: two streamed chunks
     (4, 2, 300, 48, 64, 16, 0.75, torch.float16, False),      # B = 48: three 16-token chunks
+    (32, 2, 1000, 32, 128, 64, 0.9, torch.bfloat16, True),    # G = 16: G * SP = 1024
 ])
 def test_speculative_step(hq, hkv, n, b, d, topk, overlap, dtype, union):
     """speculative_step: selected IDs bit-exact, prediction states and the
