@@ -9,6 +9,12 @@ No timing is done here; run it under ``rocprofv3 --pmc FETCH_SIZE`` and
 ``rocprofv3 --pmc WRITE_SIZE`` (one counter block per run).
 
     python3 -m stk_harness.profile_front --launches 48
+
+``--summarize FETCH_CSV WRITE_CSV --alg-bytes N`` (no GPU needed) turns the
+two runs' counter_collection.csv files into the traffic record that
+bench.py reports: each counter's mean k_front reading (KiB per dispatch)
+scaled by bytes copied / reading of the calibration copies; N is the
+algorithmic byte count the counter runs printed.
 """
 from __future__ import annotations
 
@@ -24,6 +30,55 @@ for _p in (ROOT / "strict-topk-overlap_amd", ROOT):
 import torch  # noqa: E402
 
 
+def _readings(path, launches):
+    """Mean k_front reading and mean calibration-copy reading (KiB) of one
+    rocprofv3 counter_collection.csv.  The calibration copies are the
+    copyBuffer dispatches after the last k_front launch with the largest
+    grid (smaller copies, such as reading results back, are skipped)."""
+    import csv
+    with open(path, newline="") as f:
+        rows = [(int(r["Dispatch_Id"]), r["Kernel_Name"], int(r["Grid_Size"]),
+                 float(r["Counter_Value"])) for r in csv.DictReader(f)]
+    front = [(d, k, v) for d, k, g, v in rows if "k_front" in k]
+    if not front:
+        raise SystemExit(f"profile_front: {path} holds no k_front dispatch")
+    last = max(d for d, _, _ in front)
+    after = [(g, v) for d, k, g, v in rows if d > last and "copyBuffer" in k]
+    big = max((g for g, _ in after), default=0)
+    copies = [v for g, v in after if g == big]
+    if len(copies) != launches:
+        raise SystemExit(f"profile_front: {path}: {len(copies)} calibration copies, "
+                         f"expected {launches}")
+    vals = [v for _, _, v in front]
+    return front[-1][1], len(vals), sum(vals) / len(vals), sum(copies) / len(copies)
+
+
+def summarize(fetch_csv, write_csv, args):
+    import json
+    if not args.alg_bytes:
+        raise SystemExit("profile_front: --summarize needs --alg-bytes")
+    copy_bytes = args.copy_mib * (1 << 20)
+    name, disp, f_raw, f_cal = _readings(fetch_csv, args.launches)
+    _, _, w_raw, w_cal = _readings(write_csv, args.launches)
+    ff, wf = copy_bytes / (f_cal * 1024), copy_bytes / (w_cal * 1024)
+    fetch, write = f_raw * 1024 * ff, w_raw * 1024 * wf
+    alg = args.alg_bytes
+    key = f"{args.config}@{args.overlap:g}"
+    rec = {"kernel": name, "traffic": int(fetch + write), "fetch_bytes": int(fetch),
+           "write_bytes": int(write), "fetch_kib_raw": round(f_raw, 1),
+           "write_kib_raw": round(w_raw, 1), "dispatches": disp,
+           "fetch_factor": round(ff, 5), "write_factor": round(wf, 5),
+           "calibration": f"torch copy_ of {args.copy_mib} MiB (__amd_rocclr_copyBuffer): "
+                          f"FETCH_SIZE {f_cal:.1f} KiB, WRITE_SIZE {w_cal:.1f} KiB per dispatch",
+           "algorithmic_bytes": alg, "traffic_over_algorithmic": round((fetch + write) / alg, 4)}
+    out = ROOT / "profiles" / "k_front_traffic.json"
+    data = json.loads(out.read_text()) if out.exists() else {}
+    rec["commands"] = data.get(key, {}).get("commands", [])
+    data[key] = rec
+    out.write_text(json.dumps(data, indent=1) + "\n")
+    print(json.dumps(rec, indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--config", default="c3")
@@ -32,7 +87,11 @@ def main():
     ap.add_argument("--launches", type=int, default=48)
     ap.add_argument("--sets", type=int, default=12)
     ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--summarize", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--alg-bytes", type=int, default=0)
     args = ap.parse_args()
+    if args.summarize:
+        return summarize(*args.summarize, args)
     if not torch.cuda.is_available():
         sys.exit("profile_front: no HIP device visible")
     from stk_harness import decode
