@@ -234,6 +234,29 @@ int stk_step_tail(const void* q, const void* k, const void* v, int dtype, int hq
                   int32_t* selected, float* out, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* The signed speculative decode step: gqa.select_blocks (strict_topk/gqa.py:145-161)
+ * || kernels.speculate(mode, mass_threshold, keep_mass=True)
+ * (strict_topk/kernels.py:450-477, _group :94-117), then
+ * signed_fused.repair_signed_fused (strict_topk/signed_fused.py:148-193:
+ * _schedule signed_repair.py:18-82, _corrections :30-67, _finalize :70-145),
+ * in two launches on one stream (the front of stk_speculative_step, then one
+ * workgroup per query head doing the top-K, the grouping, the signed
+ * corrections, the guarded merge and the strict fallback).  hybrid 1: hybrid
+ * prediction, 0: saved.  Outputs: selected[Hq,topk] int32 ascending, the
+ * prediction state m,l[Hq,sp], u[Hq,sp,D], out[Hq,D], fallback[Hq] and
+ * approx[Hq] as bytes 0/1, remaining[Hq], extra[Hq], positive and total job
+ * counts [Hq] int32; approx and extra may be null when max_extra_mass == 0.
+ * Supported shapes are those of stk_step_supported; the workspace is
+ * stk_step_workspace_bytes. */
+int stk_signed_step(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
+                    int n, int b, int d, const float* lo, const float* hi, int topk,
+                    const void* predicted, int pred_dtype, int sp, int hybrid,
+                    float mass_threshold, float min_remaining, float cancellation_tol,
+                    float max_extra_mass, int32_t* selected, float* m, float* l, float* u,
+                    float* out, uint8_t* fallback, float* remaining, uint8_t* approx,
+                    float* extra, int32_t* positive, int32_t* total, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,19 +17,11 @@
 //                  blocks' tiles).
 // The arithmetic is that of stk_select_blocks, stk_block_partials and
 // stk_gqa_repair; results are identical up to FP32 reduction order.
-#include "score.hpp"
+#include "step.hpp"
 #include "topk.hpp"
-#include "states_tok.hpp"
 #include "tail.hpp"
-#include "api.hpp"
 
 namespace stk {
-
-struct FrontArgs {
-  ScoreArgs sc;
-  StatesArgs st;
-  int score_wgs, total_wgs;
-};
 
 template <typename T, int NCH, int UP, bool ONE, int P, int STEPS, int GT>
 __global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_front(FrontArgs a) {
@@ -54,16 +46,8 @@ __global__ __launch_bounds__(kTailThreads) void k_tail(TailArgs a) {
 
 }  // namespace stk
 
-using namespace stk;
+namespace stk {
 
-namespace {
-
-struct StepShape {
-  int nch, passes, steps, gt, kpt, up, rpt;
-  bool one;
-};
-
-// Shape plan of the fused step, or a message saying why it is not supported.
 const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
                       int pred_dtype, uintptr_t align, StepShape* s) {
   if (dtype != DT_BF16 && dtype != DT_F16) return "the fused step takes bf16 or fp16 Q/K/V";
@@ -89,6 +73,29 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
   s->rpt = rows <= 4 ? 4 : 16;
   return nullptr;
 }
+
+FrontArgs make_front_args(const void* q, const void* k, const void* v, int dtype, int hq,
+                          int hkv, int n, int b, int d, const float* lo, const float* hi,
+                          const void* predicted, int sp, float* m, float* l, float* u,
+                          uint64_t* keys, const StepShape& s) {
+  FrontArgs f{};
+  f.sc.q = q; f.sc.qtype = dtype; f.sc.lo = lo; f.sc.hi = hi;
+  f.sc.hq = hq; f.sc.hkv = hkv; f.sc.n = n; f.sc.d = d;
+  f.sc.scores = nullptr; f.sc.keys = keys;
+  f.sc.chunks = (n + kScoreWaves * 4 * s.steps - 1) / (kScoreWaves * 4 * s.steps);
+  f.st.q = q; f.st.k = k; f.st.v = v; f.st.ids = predicted; f.st.itype = IT_I32;
+  f.st.hq = hq; f.st.hkv = hkv; f.st.n = n; f.st.b = b; f.st.d = d; f.st.s = sp;
+  f.st.m = m; f.st.l = l; f.st.u = u;
+  f.score_wgs = hkv * f.sc.chunks;
+  f.total_wgs = f.score_wgs + (int)(((int64_t)hq * sp + 3) / 4);
+  return f;
+}
+
+}  // namespace stk
+
+using namespace stk;
+
+namespace {
 
 template <typename T, int NCH, int UP, bool ONE, int P, int STEPS>
 int launch_front_gt(const FrontArgs& f, const StepShape& s, hipStream_t st) {
@@ -117,19 +124,18 @@ int launch_tail(const TailArgs& t, const StepShape& s, hipStream_t st) {
 }
 
 template <typename T, int NCH>
-int launch_step(const FrontArgs& f, const TailArgs& t, const StepShape& s, hipStream_t st,
-                bool front, bool tail) {
+int launch_front_t(const FrontArgs& f, const StepShape& s, hipStream_t st) {
   constexpr int P = NCH * 16 / (int)sizeof(T) * 4 / 64;   // D / 64
   constexpr int STEPS = P <= 2 ? 2 : 1;
-  if (front) {
-    // ONE: the whole block is one token chunk (B == 16 * UP)
-    int rc = s.up == 1 ? (s.one ? launch_front_gt<T, NCH, 1, true, P, STEPS>(f, s, st)
-                                : launch_front_gt<T, NCH, 1, false, P, STEPS>(f, s, st))
-                       : (s.one ? launch_front_gt<T, NCH, 2, true, P, STEPS>(f, s, st)
-                                : launch_front_gt<T, NCH, 2, false, P, STEPS>(f, s, st));
-    if (rc) return rc;
-  }
-  if (!tail) return STK_OK;
+  // ONE: the whole block is one token chunk (B == 16 * UP)
+  return s.up == 1 ? (s.one ? launch_front_gt<T, NCH, 1, true, P, STEPS>(f, s, st)
+                            : launch_front_gt<T, NCH, 1, false, P, STEPS>(f, s, st))
+                   : (s.one ? launch_front_gt<T, NCH, 2, true, P, STEPS>(f, s, st)
+                            : launch_front_gt<T, NCH, 2, false, P, STEPS>(f, s, st));
+}
+
+template <typename T, int NCH>
+int launch_tail_t(const TailArgs& t, const StepShape& s, hipStream_t st) {
   return s.up == 1 ? (s.one ? launch_tail<T, NCH, 1, true>(t, s, st)
                             : launch_tail<T, NCH, 1, false>(t, s, st))
                    : (s.one ? launch_tail<T, NCH, 2, true>(t, s, st)
@@ -137,6 +143,11 @@ int launch_step(const FrontArgs& f, const TailArgs& t, const StepShape& s, hipSt
 }
 
 }  // namespace
+
+int stk::launch_front(int dtype, const FrontArgs& f, const StepShape& s, hipStream_t st) {
+  STK_DISPATCH_STEP(dtype, s.nch, { return launch_front_t<T, NCH>(f, s, st); });
+  return STK_EINVAL;
+}
 
 extern "C" {
 
@@ -173,30 +184,21 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
   const char* why = plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, align, &s);
   STK_REQUIRE(why == nullptr, why ? why : "");
   uint64_t* keys = static_cast<uint64_t*>(workspace);
-  FrontArgs f{};
-  f.sc.q = q; f.sc.qtype = dtype; f.sc.lo = lo; f.sc.hi = hi;
-  f.sc.hq = hq; f.sc.hkv = hkv; f.sc.n = n; f.sc.d = d;
-  f.sc.scores = nullptr; f.sc.keys = keys;
-  f.sc.chunks = (n + kScoreWaves * 4 * s.steps - 1) / (kScoreWaves * 4 * s.steps);
-  f.st.q = q; f.st.k = k; f.st.v = v; f.st.ids = predicted; f.st.itype = IT_I32;
-  f.st.hq = hq; f.st.hkv = hkv; f.st.n = n; f.st.b = b; f.st.d = d; f.st.s = sp;
-  f.st.m = m; f.st.l = l; f.st.u = u;
-  f.score_wgs = hkv * f.sc.chunks;
-  f.total_wgs = f.score_wgs + (int)(((int64_t)hq * sp + 3) / 4);
+  const FrontArgs f = make_front_args(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, predicted, sp, m,
+                                      l, u, keys, s);
   TailArgs t{};
   t.kv = KV{q, k, v, hq, hkv, n, b, d};
   t.keys = keys; t.k = topk; t.ids = selected;
   t.p = static_cast<const int32_t*>(predicted); t.sp = sp;
   t.pm = m; t.pl = l; t.pu = u; t.uni = union_mode ? 1 : 0; t.out = out;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == DT_BF16) {
-    if (s.nch == 2) return launch_step<bf16s, 2>(f, t, s, st, front, tail);
-    if (s.nch == 4) return launch_step<bf16s, 4>(f, t, s, st, front, tail);
-    return launch_step<bf16s, 8>(f, t, s, st, front, tail);
+  if (front) {
+    const int rc = launch_front(dtype, f, s, st);
+    if (rc) return rc;
   }
-  if (s.nch == 2) return launch_step<f16s, 2>(f, t, s, st, front, tail);
-  if (s.nch == 4) return launch_step<f16s, 4>(f, t, s, st, front, tail);
-  return launch_step<f16s, 8>(f, t, s, st, front, tail);
+  if (!tail) return STK_OK;
+  STK_DISPATCH_STEP(dtype, s.nch, { return launch_tail_t<T, NCH>(t, s, st); });
+  return STK_EINVAL;
 }
 
 STK_API int stk_speculative_step(const void* q, const void* k, const void* v, int dtype, int hq,

@@ -1,0 +1,415 @@
+// Tail of the fused signed decode step: exact top-K of one query head's keys,
+// then the hybrid grouping of its predicted states, the signed add/erase
+// corrections and the guarded merge with the strict fallback, in one
+// workgroup per head.
+//
+// Reference:
+//   strict_topk/gqa.py:145-161           select_blocks (the keys' top-K)
+//   strict_topk/kernels.py:94-117        _group (hybrid: high = mass >= tau *
+//                                        total, low aggregate (m, l, u) and the
+//                                        absolute envelope)
+//   strict_topk/signed_repair.py:18-82   _schedule (misses, wrong low blocks,
+//                                        kept states, the max_extra_mass skip)
+//   strict_topk/signed_fused.py:30-67    _corrections (signed block states;
+//                                        hybrid negatives in the low frame)
+//   strict_topk/signed_fused.py:70-145   _finalize (guards, merge, fallback)
+// The arithmetic is that of stk_speculate (hybrid) + stk_repair_signed with
+// the fused rule; results agree up to FP32 reduction order.
+//
+// Layout (512 threads, every memory round trip issued as early as its
+// inputs allow):
+//   1. keys, predicted row, query row and every predicted state (m, l, u);
+//      the u rows stay in registers (RPT rows of four columns per thread);
+//   2. top-K; then wave 0 does the per-slot work (grouping, membership,
+//      keep / low / wrong sets, the extra-mass test) while wave 1 lists the
+//      misses;
+//   3. the corrections' K/V tiles (wave w takes jobs w, w + 8, ...):
+//      misses with an online softmax, wrong low blocks with weights
+//      exp(s - low_m) (every low block's maximum is <= low_m, so these never
+//      exceed 1), overlapped with the kept and low partial sums of the
+//      registered u rows;
+//   4. one merge by D threads, the guard flags OR-ed through LDS, and on a
+//      flagged head the strict online softmax over the selected tiles.
+#pragma once
+
+#include "topk.hpp"
+#include "tile2.hpp"
+#include "tail.hpp"
+
+namespace stk {
+
+struct STailArgs {
+  KV kv;                                  // q, k, v, hq, hkv, n, b, d
+  const uint64_t* keys;                   // [hq, n]
+  int k;                                  // selected per head
+  int32_t* ids;                           // [hq, k] out, ascending
+  const int32_t* p; int sp;               // predicted [hq, sp]
+  const float* pm; const float* pl; const float* pu;   // predicted states
+  int hybrid;                             // 1: hybrid prediction, 0: saved
+  float tau, min_remaining, cancel_tol, eps;
+  float* out;                             // [hq, d]
+  uint8_t* bad; float* remain;            // [hq]
+  uint8_t* approx; float* extra;          // [hq] or null when eps == 0
+  int32_t* pos; int32_t* total;           // [hq] job counts
+};
+
+template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
+__device__ __forceinline__ void stail_head(const STailArgs& a) {
+  using TT = TokTile<T, NCH, UP>;
+  constexpr int D = TT::D;
+  constexpr int TPR = D / 4;              // threads per state row (16-byte loads)
+  constexpr int RG = kTailThreads / TPR;  // rows per pass of the state prefetch
+  constexpr int SW = kTailMaxK / STK_WAVE;   // slot words of wave 0
+  __shared__ int map[kTailMapN];
+  __shared__ int sel[kTailMaxK], miss[kTailMaxK], wrong_id[kTailMaxK], pids[kTailMaxK];
+  __shared__ float s_pm[kTailMaxK], s_pl[kTailMaxK];
+  __shared__ TopkLds tl;
+  __shared__ int s_nm, s_nw, s_lowhit, s_skip, s_bad;
+  __shared__ float s_lowm, s_ll, s_mk, s_extra;
+  __shared__ uint64_t s_keep[SW], s_low[SW];
+  __shared__ float s_hl[RG];
+  __shared__ __align__(16) float s_hu[RG][D];
+  __shared__ __align__(16) float s_lu[RG][D];
+  __shared__ __align__(16) float s_la[RG][D];
+  __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_nl[kTailWaves];
+  __shared__ float s_wu[kTailWaves][D], s_nu[kTailWaves][D];
+  const int h = blockIdx.x;
+  const int n = a.kv.n, sp = a.sp;
+  const int tid = threadIdx.x, w = wave_id();
+  const int G = a.kv.hq / a.kv.hkv;
+  const bool hybrid = a.hybrid != 0;
+  // ---- round trip 1: every load that does not depend on the top-K
+  uint64_t key[KPT];
+  topk_load<KPT>(a.keys + (size_t)h * n, n, key);
+  const int pid = (int)ld_or(a.p, (int64_t)h * sp + tid, tid < sp, (int32_t)-1);
+  TT t;
+  t.init();
+  uint32_t qw[TT::QW];
+  t.load_q(reinterpret_cast<const T*>(a.kv.q) + (size_t)h * D, qw);
+  const float pmv = ld_or(a.pm, (int64_t)h * sp + tid, tid < sp, -INFINITY);
+  const float plv = ld_or(a.pl, (int64_t)h * sp + tid, tid < sp, 0.f);
+  const int c4 = tid % TPR, rg = tid / TPR;
+  float4 uu[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int r = rg + RG * j;
+    const int64_t row = (int64_t)h * sp + (r < sp ? r : 0);
+    uu[j] = *reinterpret_cast<const float4*>(a.pu + row * D + 4 * c4);
+  }
+  // ---- membership map: max predicted slot + 1 per block ID
+  for (int i = tid; i < n; i += kTailThreads) map[i] = 0;
+  if (tid < sp) {
+    pids[tid] = pid;
+    s_pm[tid] = pmv;
+    s_pl[tid] = plv;
+  }
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
+  // ---- exact top-K (its first barrier orders the map writes above)
+  int32_t* out_ids = a.ids + (size_t)h * a.k;
+  topk_select_keys<KPT>(key, n, a.k, tl, [&](int pos, int idx) {
+    sel[pos] = idx;
+    out_ids[pos] = idx;
+    atomicOr(&map[idx], kSelFlag);
+  });
+  __syncthreads();
+  if (w == 0) {
+    // ---- per-slot work, lane l holding slots l, l + 64, ...
+    float pm_[SW], pl_[SW];
+    bool ok[SW], hit[SW], real[SW];
+    float gm = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < SW; ++c) {
+      const int p = c * STK_WAVE + lane_id();
+      ok[c] = p < sp;
+      pm_[c] = ok[c] ? s_pm[p] : -INFINITY;
+      pl_[c] = ok[c] ? s_pl[p] : 0.f;
+      const int id = ok[c] ? pids[p] : -1;
+      real[c] = id >= 0 && id < n;
+      hit[c] = real[c] && (map[id] & kSelFlag) != 0;
+      gm = fmaxf(gm, pm_[c]);
+    }
+    bool high[SW], low[SW], wrong[SW], keep[SW];
+    float lowm = 0.f, ll = 0.f;
+    bool lowhit = false;
+    if (hybrid) {
+      // kernels.py:102-117: mass under the predicted-set softmax
+      gm = wave_max_u(gm);
+      float tot = 0.f;
+#pragma unroll
+      for (int c = 0; c < SW; ++c) tot += wexp(pm_[c], gm) * pl_[c];
+      tot = wave_sum_u(tot);
+      float lm = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < SW; ++c) {
+        high[c] = ok[c] && wexp(pm_[c], gm) * pl_[c] >= a.tau * tot;
+        low[c] = ok[c] && !high[c];
+        lm = low[c] ? fmaxf(lm, pm_[c]) : lm;
+      }
+      lm = wave_max_u(lm);
+      lowm = lm == -INFINITY ? 0.f : lm;
+      float x = 0.f;
+      bool lh = false;
+#pragma unroll
+      for (int c = 0; c < SW; ++c) {
+        x += low[c] ? wexp(pm_[c], lowm) * pl_[c] : 0.f;
+        lh = lh || (hit[c] && low[c]);
+      }
+      ll = wave_sum_u(x);
+      lowhit = __ballot(lh) != 0ull;
+#pragma unroll
+      for (int c = 0; c < SW; ++c) {
+        // an ID outside [0, n) has the empty state (-inf, 0, 0): nothing to
+        // subtract, and no tile to read
+        wrong[c] = lowhit && low[c] && !hit[c] && real[c];
+        keep[c] = hit[c] && high[c];
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < SW; ++c) {
+        high[c] = low[c] = wrong[c] = false;
+        keep[c] = hit[c];
+      }
+    }
+    float mk = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < SW; ++c) mk = keep[c] ? fmaxf(mk, pm_[c]) : mk;
+    mk = wave_max_u(mk);
+    // signed_repair.py:61-72: skip the wrong blocks when their mass is small
+    bool skip = false;
+    float ex = 0.f;
+    bool anyw = false;
+#pragma unroll
+    for (int c = 0; c < SW; ++c) anyw = anyw || wrong[c];
+    if (hybrid && a.eps > 0.f && __ballot(anyw) != 0ull) {
+      const float ref = fmaxf(lowm, mk);
+      float dk = 0.f, dw = 0.f;
+#pragma unroll
+      for (int c = 0; c < SW; ++c) {
+        dk += keep[c] ? wexp(pm_[c], ref) * pl_[c] : 0.f;
+        dw += wrong[c] ? wexp(pm_[c], ref) * pl_[c] : 0.f;
+      }
+      const float denom = wexp(lowm, ref) * ll + wave_sum_u(dk);
+      ex = wave_sum_u(dw) / denom;
+      skip = ex <= a.eps;
+    }
+    int nw = 0;
+#pragma unroll
+    for (int c = 0; c < SW; ++c) {
+      const bool wr = wrong[c] && !skip;
+      const uint64_t bal = __ballot(wr);
+      if (wr) wrong_id[nw + (int)__popcll(bal & lanemask_lt())] = pids[c * STK_WAVE + lane_id()];
+      nw += (int)__popcll(bal);
+      const uint64_t kb = __ballot(keep[c]), lb = __ballot(low[c]);
+      if (lane_id() == 0) {
+        s_keep[c] = kb;
+        s_low[c] = lb;
+      }
+    }
+    if (lane_id() == 0) {
+      s_nw = nw;
+      s_lowm = lowm;
+      s_ll = ll;
+      s_mk = mk;
+      s_lowhit = lowhit ? 1 : 0;
+      s_skip = skip ? 1 : 0;
+      s_extra = skip ? ex : 0.f;
+    }
+  } else if (w == 1) {
+    // ---- misses (selected, not predicted) in ascending block order
+    int cnt = 0;
+    for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
+      const int p = p0 + lane_id();
+      const bool in = p < a.k;
+      const int id = in ? sel[p] : 0;
+      const bool ms = in && (map[id] & ~kSelFlag) == 0;
+      const uint64_t bal = __ballot(ms);
+      if (ms) miss[cnt + (int)__popcll(bal & lanemask_lt())] = id;
+      cnt += (int)__popcll(bal);
+    }
+    if (lane_id() == 0) s_nm = cnt;
+  }
+  __syncthreads();
+  const int nm = s_nm, nw = s_nw, jobs = nm + nw;
+  const float lowm = s_lowm, mk = s_mk;
+  // ---- round trip 2: wave w streams jobs w, w + 8, ...; the first tile's
+  // loads are issued before the partial sums below
+  const int kvh = h / G;
+  const float scale = 1.0f / sqrtf((float)D);
+  const T* K = reinterpret_cast<const T*>(a.kv.k);
+  const T* V = reinterpret_cast<const T*>(a.kv.v);
+  auto tile = [&](int x) {
+    const int id = x < nm ? miss[x] : wrong_id[x - nm];
+    return (((size_t)kvh * n + id) * a.kv.b) * D;
+  };
+  uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
+  if (ONE && w < jobs) t.load(K + tile(w), V + tile(w), 0, kw, vw);
+  // ---- partial sums of the registered u rows: kept states relative to mk,
+  // the low aggregate and its envelope relative to low_m
+  uint64_t kb4[SW], lb4[SW];
+#pragma unroll
+  for (int x = 0; x < SW; ++x) {
+    kb4[x] = s_keep[x];
+    lb4[x] = s_low[x];
+  }
+  float hl = 0.f;
+  float4 hu = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 lu = hu, la = hu;
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int r = rg + RG * j;   // < 16 * RG <= 512
+    const int rr = r < kTailMaxK ? r : 0;
+    const int wd = rr >> 6, bit = rr & 63;
+    const uint64_t kword = wd == 0 ? kb4[0] : (wd == 1 ? kb4[1] : (wd == 2 ? kb4[2] : kb4[3]));
+    const uint64_t lword = wd == 0 ? lb4[0] : (wd == 1 ? lb4[1] : (wd == 2 ? lb4[2] : lb4[3]));
+    const bool kp = r < sp && ((kword >> bit) & 1ull);
+    const bool lo = r < sp && ((lword >> bit) & 1ull);
+    const float pm = s_pm[rr];
+    const float wk = kp ? wexp(pm, mk) : 0.f;
+    const float wl = lo ? wexp(pm, lowm) : 0.f;
+    hl += wk * s_pl[rr];
+    hu.x += wk * uu[j].x; hu.y += wk * uu[j].y; hu.z += wk * uu[j].z; hu.w += wk * uu[j].w;
+    lu.x += wl * uu[j].x; lu.y += wl * uu[j].y; lu.z += wl * uu[j].z; lu.w += wl * uu[j].w;
+    la.x += wl * fabsf(uu[j].x); la.y += wl * fabsf(uu[j].y);
+    la.z += wl * fabsf(uu[j].z); la.w += wl * fabsf(uu[j].w);
+  }
+  *reinterpret_cast<float4*>(&s_hu[rg][4 * c4]) = hu;
+  *reinterpret_cast<float4*>(&s_lu[rg][4 * c4]) = lu;
+  *reinterpret_cast<float4*>(&s_la[rg][4 * c4]) = la;
+  if (c4 == 0) s_hl[rg] = hl;
+  // ---- the corrections: misses with the online softmax, wrong low blocks
+  // in the low frame (their sign is applied in the merge)
+  float m = -INFINITY, l = 0.f, acc[TT::DPL];
+  float nl = 0.f, nacc[TT::DPL];
+#pragma unroll
+  for (int e = 0; e < TT::DPL; ++e) acc[e] = nacc[e] = 0.f;
+  for (int x = w; x < jobs; x += kTailWaves) {
+    const bool neg = x >= nm;
+    float fm = lowm;
+    if constexpr (ONE) {
+      if (x != w) t.load(K + tile(x), V + tile(x), 0, kw, vw);
+      float s[UP];
+      t.scores(qw, kw, 0, a.kv.b, scale, s);
+      if (neg) t.template accumulate<true, false>(s, vw, fm, nl, nacc);
+      else t.template accumulate<false, false>(s, vw, m, l, acc);
+    } else {
+      for (int t0 = 0; t0 < a.kv.b; t0 += TT::CH) {
+        t.load(K + tile(x), V + tile(x), t0, kw, vw);
+        float s[UP];
+        t.scores(qw, kw, t0, a.kv.b, scale, s);
+        if (neg) t.template accumulate<true, false>(s, vw, fm, nl, nacc);
+        else t.template accumulate<false, false>(s, vw, m, l, acc);
+      }
+    }
+  }
+  if (lane_id() == 0) {
+    s_wm[w] = m;
+    s_wl[w] = l;
+    s_nl[w] = nl;
+  }
+  t.store(s_wu[w], acc);
+  t.store(s_nu[w], nacc);
+  __syncthreads();
+  // ---- guarded merge (signed_fused.py:98-122), one thread per dim
+  float frac = 1.f, o = 0.f;
+  const bool lowhit = hybrid && s_lowhit != 0;
+  if (tid < D) {
+    float lm_eff = -INFINITY, lowl = 0.f, lowu = 0.f;
+    bool bad = false;
+    if (lowhit) {
+      float nls = 0.f, nus = 0.f, lus = 0.f, env = 0.f;
+#pragma unroll
+      for (int x = 0; x < kTailWaves; ++x) {
+        nls += s_nl[x];
+        nus += s_nu[x][tid];
+      }
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        lus += s_lu[g][tid];
+        env += s_la[g][tid];
+      }
+      const float ll = s_ll;
+      const float removed = -nus;
+      lowl = ll - nls;
+      lowu = lus + removed;
+      frac = lowl / ll;
+      const float cs = env + fabsf(removed);
+      bad = (frac < a.min_remaining) || (frac != frac) ||
+            (fabsf(lowu) < a.cancel_tol * cs && cs > 0.f);
+      lm_eff = lowm;
+    }
+    float M = fmaxf(mk, lm_eff);
+#pragma unroll
+    for (int x = 0; x < kTailWaves; ++x) M = fmaxf(M, s_wm[x]);
+    const float fk = wexp(mk, M), fl = wexp(lm_eff, M);
+    float hls = 0.f, hus = 0.f;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      hls += s_hl[g];
+      hus += s_hu[g][tid];
+    }
+    float den = fk * hls + fl * lowl;
+    float num = fk * hus + fl * lowu;
+#pragma unroll
+    for (int x = 0; x < kTailWaves; ++x) {
+      const float f = wexp(s_wm[x], M);
+      den += f * s_wl[x];
+      num += f * s_wu[x][tid];
+    }
+    o = num / den;
+    if (hybrid)
+      bad = bad || !isfinite(o) || den <= 0.f || isinf(den);
+    if (bad) s_bad = 1;
+  }
+  __syncthreads();
+  const bool fallback = s_bad != 0;
+  if (tid == 0) {
+    a.bad[h] = fallback ? 1 : 0;
+    a.remain[h] = frac;
+    a.pos[h] = nm;
+    a.total[h] = jobs;
+    if (a.approx) {
+      a.approx[h] = (!fallback && s_skip) ? 1 : 0;
+      a.extra[h] = fallback ? 0.f : s_extra;
+    }
+  }
+  if (!fallback) {
+    if (tid < D) a.out[(size_t)h * D + tid] = o;
+    return;
+  }
+  // ---- strict fallback (signed_fused.py:123-142): online softmax over the
+  // selected blocks, wave w taking selected w, w + 8, ...
+  m = -INFINITY;
+  l = 0.f;
+#pragma unroll
+  for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
+  for (int x = w; x < a.k; x += kTailWaves) {
+    const size_t off = (((size_t)kvh * n + sel[x]) * a.kv.b) * D;
+    for (int t0 = 0; t0 < a.kv.b; t0 += TT::CH) {
+      t.load(K + off, V + off, t0, kw, vw);
+      t.template update<false, false>(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
+    }
+  }
+  if (lane_id() == 0) {
+    s_wm[w] = m;
+    s_wl[w] = l;
+  }
+  t.store(s_wu[w], acc);
+  __syncthreads();
+  if (tid < D) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int x = 0; x < kTailWaves; ++x) M = fmaxf(M, s_wm[x]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int x = 0; x < kTailWaves; ++x) {
+      const float f = wexp(s_wm[x], M);
+      den += f * s_wl[x];
+      num += f * s_wu[x][tid];
+    }
+    a.out[(size_t)h * D + tid] = num / den;
+  }
+}
+
+}  // namespace stk

@@ -12,6 +12,13 @@ blocks' states side by side, then one workgroup per query head doing the
 exact top-K and the repair.  Shapes the fused kernels do not cover (fp32,
 other head dims, long rows) run the same steps through the individual entry
 points, still on the GPU.
+
+``speculative_signed_step`` does the same for the signed strategy:
+``select_blocks`` || ``kernels.speculate(mode, keep_mass=True)``, then
+``signed_fused.repair_signed_fused`` (strict_topk/signed_fused.py:148-193),
+again in two launches (the same front, then one workgroup per query head for
+the top-K, the hybrid grouping, the signed corrections, the guarded merge
+and the strict fallback).
 """
 from dataclasses import dataclass
 
@@ -73,3 +80,70 @@ def speculative_step(q, k, v, lo, hi, predicted, topk, union=False):
     else:
         out = gqa_light.repair_saved_light(q, k, v, selected, predicted, state)
     return StepResult(selected, state, out)
+
+
+@dataclass
+class SignedStepResult:
+    selected: torch.Tensor     # int32 [Hq, topk], ascending block IDs
+    state: PartialState        # prediction state over the predicted blocks
+    result: "SignedRepairResult"   # output and guard results of repair_signed_fused
+
+
+def speculative_signed_step(q, k, v, lo, hi, predicted, topk, mode="hybrid", mass_threshold=0.1,
+                            min_remaining=1.e-3, cancellation_tol=1.e-5, max_extra_mass=0.):
+    """select(q, lo, hi, topk) || speculate(q, k, v, predicted, mode,
+    mass_threshold, keep_mass=True), then repair_signed_fused.
+
+    ``mode`` is "hybrid" or "saved".  The result's fields are those of
+    ``signed_fused.repair_signed_fused`` on the same selection and
+    prediction.  Shapes the fused kernels do not cover (and the "compact"
+    mode) run the same three steps through the individual entry points.
+    """
+    from . import kernels, signed_fused
+    from .signed_repair import SignedRepairResult
+    if mode not in ("saved", "hybrid", "compact"):
+        raise ValueError(mode)
+    if not 0 <= mass_threshold <= 1:
+        raise ValueError("mass_threshold must be in [0,1]")
+    if not 0 <= max_extra_mass <= 1:
+        raise ValueError("max_extra_mass must be in [0,1]")
+    gqa._shape(q, k, v, predicted)
+    if lo.ndim != 3 or hi.shape != lo.shape or lo.shape[0] != k.shape[0] or \
+            lo.shape[1:] != (k.shape[1], k.shape[3]):
+        raise ValueError("expected LO/HI[Hkv,N,D] matching K")
+    if lo.dtype != torch.float32 or hi.dtype != torch.float32:
+        raise ValueError("lo and hi must be FP32")
+    if any(x.device != q.device or not x.is_contiguous() for x in (lo, hi)):
+        raise ValueError("Q/LO/HI must be contiguous and on the same CUDA device")
+    topk = int(topk)
+    hq, d = q.shape
+    hkv, n, b, _ = k.shape
+    if topk < 1 or topk > n:
+        raise RuntimeError("selected index k out of range")
+    sp = predicted.shape[1]
+    if mode != "compact" and supported(q, k, lo, topk, predicted):
+        dev = q.device
+        selected = torch.empty((hq, topk), device=dev, dtype=torch.int32)
+        state = _allocate_state(hq, sp, d, dev)
+        out = torch.empty((hq, d), device=dev, dtype=torch.float32)
+        fallback = torch.empty((hq,), device=dev, dtype=torch.bool)
+        remaining = torch.empty((hq,), device=dev, dtype=torch.float32)
+        approx = torch.empty_like(fallback) if max_extra_mass > 0 else None
+        extra = torch.empty_like(remaining) if max_extra_mass > 0 else None
+        positive = torch.empty((hq,), device=dev, dtype=torch.int32)
+        total = torch.empty_like(positive)
+        ws = _lib.workspace(_lib.size("stk_step_workspace_bytes", hq, hkv, n, d, topk), dev)
+        _lib.call("stk_signed_step", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi), topk,
+                  _lib.ptr(predicted), _lib.id_code(predicted), sp, 1 if mode == "hybrid" else 0,
+                  float(mass_threshold), float(min_remaining), float(cancellation_tol),
+                  float(max_extra_mass), _lib.ptr(selected), _lib.ptr(state.m),
+                  _lib.ptr(state.l), _lib.ptr(state.u), _lib.ptr(out), _lib.ptr(fallback),
+                  _lib.ptr(remaining), _lib.ptr(approx), _lib.ptr(extra), _lib.ptr(positive),
+                  _lib.ptr(total), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
+        res = SignedRepairResult(out, fallback, remaining, approx, extra, positive, total)
+        return SignedStepResult(selected, state, res)
+    selected = gqa.select_blocks(q, lo, hi, topk)
+    pred = kernels.speculate(q, k, v, predicted, mode, mass_threshold, keep_mass=True)
+    res = signed_fused.repair_signed_fused(q, k, v, selected, predicted, pred, min_remaining,
+                                           cancellation_tol, max_extra_mass)
+    return SignedStepResult(selected, pred.state, res)

@@ -561,6 +561,54 @@ def test_speculative_step(hq, hkv, n, b, d, topk, overlap, dtype, union):
     check(res.output, expected, ("step", hq, n, union))
 
 
+@pytest.mark.parametrize("hq,hkv,n,b,d,topk,overlap,dtype,mode,tau,eps,min_rem,tol", [
+    (32, 8, 1000, 32, 128, 64, 0.75, torch.bfloat16, "hybrid", 0.2, 0.01, 1e-3, 1e-5),  # c5 shape
+    (32, 8, 1000, 32, 128, 64, 0.75, torch.bfloat16, "hybrid", 0.2, 0.0, 1e-3, 1e-5),   # strict
+    (8, 2, 3000, 32, 128, 64, 0.6, torch.bfloat16, "hybrid", 0.2, 0.01, 1e-3, 1e-5),    # n > 2048
+    (8, 2, 400, 16, 64, 20, 0.5, torch.float16, "hybrid", 0.1, 0.0, 1e-3, 1e-5),        # B = 16
+    (16, 8, 512, 32, 128, 64, 0.9, torch.bfloat16, "saved", 0.2, 0.0, 1e-3, 1e-5),      # saved
+    (8, 4, 300, 32, 128, 32, 0.5, torch.bfloat16, "hybrid", 0.05, 1.0, 1e-3, 1e-5),     # skip all
+    (8, 4, 300, 32, 128, 32, 0.5, torch.bfloat16, "hybrid", 0.05, 0.0, 1.0, 1e-5),      # fallback
+    (8, 4, 300, 64, 128, 32, 0.5, torch.bfloat16, "hybrid", 0.05, 0.01, 1e-3, 2.0),     # cancel
+])
+def test_signed_step(hq, hkv, n, b, d, topk, overlap, dtype, mode, tau, eps, min_rem, tol):
+    """speculative_signed_step against the oracle's select || speculate ->
+    repair_signed_fused on the same inputs: IDs and job counts exact, guard
+    flags exact, outputs within tolerance."""
+    from stk_harness.configs import make_qkv, perturb
+    from strict_topk import step
+    q, k, v, lo, hi = make_qkv(hq, hkv, d, b, n, dtype, True, 20261201 + n + hq)
+    qn, kn, vn = np_(q, k, v)
+    ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), topk)
+    p = perturb(torch.from_numpy(ref_ids), n, topk, overlap, 11)
+    pn = p.numpy().astype(np.int64)
+    qd, kd, vd, lod, hid, pd = dev(q, k, v, lo, hi, p)
+    assert step.supported(qd, kd, lod, topk, pd)
+    got = step.speculative_signed_step(qd, kd, vd, lod, hid, pd, topk, mode, tau, min_rem, tol,
+                                       eps)
+    assert got.selected.cpu().numpy().tolist() == ref_ids.tolist()
+    pred = O.speculate(qn, kn, vn, pn, mode, tau, keep_mass=True)
+    np.testing.assert_allclose(got.state.m.cpu().double().numpy(), pred.state.m, rtol=1e-5,
+                               atol=1e-5)
+    np.testing.assert_allclose(got.state.l.cpu().double().numpy(), pred.state.l, rtol=1e-4)
+    ref = O.repair_signed_fused(qn, kn, vn, ref_ids, pn, pred, min_rem, tol, eps)
+    res = got.result
+    assert res.fallback.cpu().numpy().tolist() == ref.fallback.tolist()
+    assert res.positive_jobs.cpu().numpy().tolist() == ref.positive_jobs.tolist()
+    assert res.total_jobs.cpu().numpy().tolist() == ref.total_jobs.tolist()
+    np.testing.assert_allclose(res.remaining.cpu().double().numpy(), ref.remaining, rtol=1e-4,
+                               atol=1e-6)
+    if eps > 0:
+        assert res.approximate_heads.cpu().numpy().tolist() == ref.approximate_heads.tolist()
+        np.testing.assert_allclose(res.extra_mass_bound.cpu().double().numpy(),
+                                   ref.extra_mass_bound, rtol=1e-4, atol=1e-7)
+    else:
+        assert res.approximate_heads is None and res.extra_mass_bound is None
+    check(res.output, ref.output, ("signed step", mode, n, eps))
+    if min_rem == 1.0:
+        assert res.fallback.any()
+
+
 @pytest.mark.parametrize("dtype,b", [(torch.float32, 8), (torch.bfloat16, 8)])
 def test_speculative_step_composed_fallback(dtype, b):
     """fp32 inputs with int64 predictions, and blocks whose token count is not
