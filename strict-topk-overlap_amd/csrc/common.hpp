@@ -292,6 +292,14 @@ __device__ __forceinline__ uint64_t wave_bits64_u(uint64_t v) {
 // Lanes below this one.
 __device__ __forceinline__ uint64_t lanemask_lt() { return (1ull << lane_id()) - 1ull; }
 
+// Wait until every vector memory load of this wave has returned (s_waitcnt
+// vmcnt(0); expcnt and lgkmcnt left free).  Placed where the outstanding
+// loads are known to have returned long ago, it costs nothing and resets
+// the compiler's count: loads issued afterwards under a branch then do not
+// make later uses of the earlier loads wait for them (at a join the
+// compiler assumes the path without those loads and waits for everything).
+__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Exclusive prefix sum over the workgroup in thread order with one barrier;
 // `tmp` holds one int per wave and must not be rewritten until every thread
 // has returned (use a fresh buffer or a barrier).  Needs full waves.

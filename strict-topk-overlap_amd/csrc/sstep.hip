@@ -27,14 +27,15 @@ namespace {
 template <typename T, int NCH, int UP, bool ONE>
 int launch_stail(const STailArgs& t, const StepShape& s, hipStream_t st) {
   const dim3 grid(t.kv.hq), block(kTailThreads);
-  if (s.kpt == 4 && s.rpt == 4)
-    hipLaunchKernelGGL((k_stail<T, NCH, UP, ONE, 4, 4>), grid, block, 0, st, t);
-  else if (s.kpt == 4)
-    hipLaunchKernelGGL((k_stail<T, NCH, UP, ONE, 4, 16>), grid, block, 0, st, t);
-  else if (s.rpt == 4)
-    hipLaunchKernelGGL((k_stail<T, NCH, UP, ONE, 16, 4>), grid, block, 0, st, t);
-  else
-    hipLaunchKernelGGL((k_stail<T, NCH, UP, ONE, 16, 16>), grid, block, 0, st, t);
+#define STK_STAIL(KPT)                                                                  \
+  if (s.rpt == 4)                                                                       \
+    hipLaunchKernelGGL((k_stail<T, NCH, UP, ONE, KPT, 4>), grid, block, 0, st, t);      \
+  else                                                                                  \
+    hipLaunchKernelGGL((k_stail<T, NCH, UP, ONE, KPT, 16>), grid, block, 0, st, t);
+  if (s.kpt == 4) { STK_STAIL(4) }
+  else if (s.kpt == 8) { STK_STAIL(8) }
+  else { STK_STAIL(16) }
+#undef STK_STAIL
   return stk_check_launch("k_stail");
 }
 

@@ -62,7 +62,7 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
   s->steps = s->passes <= 2 ? 2 : 1;
   s->gt = G == 1 ? 1 : (G == 2 ? 2 : (s->passes <= 2 ? 4 : 2));
   if (s->passes > 2 && s->gt > 2) s->gt = 2;
-  s->kpt = n <= kTailThreads * 4 ? 4 : 16;
+  s->kpt = n <= kTailThreads * 4 ? 4 : (n <= kTailThreads * 8 ? 8 : 16);
   s->up = tok_up(b);
   s->one = b == 16 * s->up;
   if (topk > kTailMaxK || sp > kTailMaxK) return "the fused step takes at most 256 selected and predicted IDs";
@@ -112,14 +112,15 @@ int launch_front_gt(const FrontArgs& f, const StepShape& s, hipStream_t st) {
 template <typename T, int NCH, int UP, bool ONE>
 int launch_tail(const TailArgs& t, const StepShape& s, hipStream_t st) {
   const dim3 grid(t.kv.hq), block(kTailThreads);
-  if (s.kpt == 4 && s.rpt == 4)
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 4, 4>), grid, block, 0, st, t);
-  else if (s.kpt == 4)
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 4, 16>), grid, block, 0, st, t);
-  else if (s.rpt == 4)
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 16, 4>), grid, block, 0, st, t);
-  else
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, 16, 16>), grid, block, 0, st, t);
+#define STK_TAIL(KPT)                                                                   \
+  if (s.rpt == 4)                                                                       \
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, KPT, 4>), grid, block, 0, st, t);       \
+  else                                                                                  \
+    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, KPT, 16>), grid, block, 0, st, t);
+  if (s.kpt == 4) { STK_TAIL(4) }
+  else if (s.kpt == 8) { STK_TAIL(8) }
+  else { STK_TAIL(16) }
+#undef STK_TAIL
   return stk_check_launch("k_tail");
 }
 

@@ -136,6 +136,8 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
     return (((size_t)kvh * n + miss[x]) * a.kv.b) * D;
   };
   uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
+  // the entry loads (u rows, query) returned during the top-K
+  vm_drain();
   if (ONE && w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
   // ---- the hits' (or, for union, every predicted row's) partial LSE sums
   uint64_t um4[kTailMaxK / 64];

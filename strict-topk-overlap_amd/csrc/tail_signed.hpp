@@ -23,11 +23,15 @@
 //   2. top-K; then wave 0 does the per-slot work (grouping, membership,
 //      keep / low / wrong sets, the extra-mass test) while wave 1 lists the
 //      misses;
-//   3. the corrections' K/V tiles (wave w takes jobs w, w + 8, ...):
-//      misses with an online softmax, wrong low blocks with weights
-//      exp(s - low_m) (every low block's maximum is <= low_m, so these never
-//      exceed 1), overlapped with the kept and low partial sums of the
-//      registered u rows;
+//   3. the missed blocks' K/V tiles (wave w takes misses w, w + 8, ..., two
+//      tiles in flight), folded with an online softmax, overlapped with the
+//      partial sums of the registered u rows: the kept states, the low
+//      aggregate with its envelope, and the wrong low blocks' corrections.
+//      A wrong block's correction in the reference (_corrections :52-61) is
+//      its block-local state (max m, l, u of the recomputed tile) times
+//      exp(m - low_m); that state is the prediction state this step's front
+//      computed for the same block with the same arithmetic, so it is taken
+//      from the registered rows instead of re-reading the tile;
 //   4. one merge by D threads, the guard flags OR-ed through LDS, and on a
 //      flagged head the strict online softmax over the selected tiles.
 #pragma once
@@ -60,19 +64,22 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   constexpr int TPR = D / 4;              // threads per state row (16-byte loads)
   constexpr int RG = kTailThreads / TPR;  // rows per pass of the state prefetch
   constexpr int SW = kTailMaxK / STK_WAVE;   // slot words of wave 0
+  // two tile buffers in flight when they fit the register budget
+  constexpr bool DB = ONE && RPT == 4 && UP * TT::QW + TT::CH * TT::VW <= 64;
   __shared__ int map[kTailMapN];
-  __shared__ int sel[kTailMaxK], miss[kTailMaxK], wrong_id[kTailMaxK], pids[kTailMaxK];
+  __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
   __shared__ float s_pm[kTailMaxK], s_pl[kTailMaxK];
   __shared__ TopkLds tl;
   __shared__ int s_nm, s_nw, s_lowhit, s_skip, s_bad;
   __shared__ float s_lowm, s_ll, s_mk, s_extra;
-  __shared__ uint64_t s_keep[SW], s_low[SW];
-  __shared__ float s_hl[RG];
+  __shared__ uint64_t s_keep[SW], s_low[SW], s_wrong[SW];
+  __shared__ float s_hl[RG], s_nl[RG];
   __shared__ __align__(16) float s_hu[RG][D];
   __shared__ __align__(16) float s_lu[RG][D];
   __shared__ __align__(16) float s_la[RG][D];
-  __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_nl[kTailWaves];
-  __shared__ float s_wu[kTailWaves][D], s_nu[kTailWaves][D];
+  __shared__ __align__(16) float s_nu[RG][D];
+  __shared__ float s_wm[kTailWaves], s_wl[kTailWaves];
+  __shared__ float s_wu[kTailWaves][D];
   const int h = blockIdx.x;
   const int n = a.kv.n, sp = a.sp;
   const int tid = threadIdx.x, w = wave_id();
@@ -197,14 +204,13 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     int nw = 0;
 #pragma unroll
     for (int c = 0; c < SW; ++c) {
-      const bool wr = wrong[c] && !skip;
-      const uint64_t bal = __ballot(wr);
-      if (wr) wrong_id[nw + (int)__popcll(bal & lanemask_lt())] = pids[c * STK_WAVE + lane_id()];
-      nw += (int)__popcll(bal);
+      const uint64_t wb = __ballot(wrong[c] && !skip);
+      nw += (int)__popcll(wb);
       const uint64_t kb = __ballot(keep[c]), lb = __ballot(low[c]);
       if (lane_id() == 0) {
         s_keep[c] = kb;
         s_low[c] = lb;
+        s_wrong[c] = wb;
       }
     }
     if (lane_id() == 0) {
@@ -231,85 +237,97 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     if (lane_id() == 0) s_nm = cnt;
   }
   __syncthreads();
-  const int nm = s_nm, nw = s_nw, jobs = nm + nw;
+  const int nm = s_nm, nw = s_nw;
   const float lowm = s_lowm, mk = s_mk;
-  // ---- round trip 2: wave w streams jobs w, w + 8, ...; the first tile's
-  // loads are issued before the partial sums below
+  // ---- round trip 2: wave w streams misses w, w + 8, ...; its first two
+  // tiles' loads are issued before the partial sums below
   const int kvh = h / G;
   const float scale = 1.0f / sqrtf((float)D);
   const T* K = reinterpret_cast<const T*>(a.kv.k);
   const T* V = reinterpret_cast<const T*>(a.kv.v);
-  auto tile = [&](int x) {
-    const int id = x < nm ? miss[x] : wrong_id[x - nm];
-    return (((size_t)kvh * n + id) * a.kv.b) * D;
-  };
+  auto tile = [&](int x) { return (((size_t)kvh * n + miss[x]) * a.kv.b) * D; };
   uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
-  if (ONE && w < jobs) t.load(K + tile(w), V + tile(w), 0, kw, vw);
-  // ---- partial sums of the registered u rows: kept states relative to mk,
-  // the low aggregate and its envelope relative to low_m
-  uint64_t kb4[SW], lb4[SW];
-#pragma unroll
-  for (int x = 0; x < SW; ++x) {
-    kb4[x] = s_keep[x];
-    lb4[x] = s_low[x];
-  }
-  float hl = 0.f;
+  uint32_t kw2[UP][TT::QW], vw2[TT::CH][TT::VW];
+  // the entry loads (u rows, query) returned during the top-K
+  vm_drain();
+  if (ONE && w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
+  // ---- partial sums of the registered u rows: kept states relative to mk;
+  // the low aggregate, its envelope and the wrong blocks' corrections
+  // relative to low_m
+  float hl = 0.f, nl = 0.f;
   float4 hu = make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 lu = hu, la = hu;
+  float4 lu = hu, la = hu, nu = hu;
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int r = rg + RG * j;   // < 16 * RG <= 512
     const int rr = r < kTailMaxK ? r : 0;
     const int wd = rr >> 6, bit = rr & 63;
-    const uint64_t kword = wd == 0 ? kb4[0] : (wd == 1 ? kb4[1] : (wd == 2 ? kb4[2] : kb4[3]));
-    const uint64_t lword = wd == 0 ? lb4[0] : (wd == 1 ? lb4[1] : (wd == 2 ? lb4[2] : lb4[3]));
+    // mask words straight from LDS (a private array indexed per thread
+    // would live in scratch memory, whose loads share the vector memory
+    // counter with the tile loads in flight and would wait for them)
+    const uint64_t kword = s_keep[wd], lword = s_low[wd], wword = s_wrong[wd];
     const bool kp = r < sp && ((kword >> bit) & 1ull);
     const bool lo = r < sp && ((lword >> bit) & 1ull);
-    const float pm = s_pm[rr];
+    const bool wr = r < sp && ((wword >> bit) & 1ull);
+    const float pm = s_pm[rr], pl = s_pl[rr];
     const float wk = kp ? wexp(pm, mk) : 0.f;
     const float wl = lo ? wexp(pm, lowm) : 0.f;
-    hl += wk * s_pl[rr];
+    const float wn = wr ? wl : 0.f;
+    hl += wk * pl;
+    nl += wn * pl;
     hu.x += wk * uu[j].x; hu.y += wk * uu[j].y; hu.z += wk * uu[j].z; hu.w += wk * uu[j].w;
     lu.x += wl * uu[j].x; lu.y += wl * uu[j].y; lu.z += wl * uu[j].z; lu.w += wl * uu[j].w;
     la.x += wl * fabsf(uu[j].x); la.y += wl * fabsf(uu[j].y);
     la.z += wl * fabsf(uu[j].z); la.w += wl * fabsf(uu[j].w);
+    nu.x += wn * uu[j].x; nu.y += wn * uu[j].y; nu.z += wn * uu[j].z; nu.w += wn * uu[j].w;
   }
   *reinterpret_cast<float4*>(&s_hu[rg][4 * c4]) = hu;
   *reinterpret_cast<float4*>(&s_lu[rg][4 * c4]) = lu;
   *reinterpret_cast<float4*>(&s_la[rg][4 * c4]) = la;
-  if (c4 == 0) s_hl[rg] = hl;
-  // ---- the corrections: misses with the online softmax, wrong low blocks
-  // in the low frame (their sign is applied in the merge)
+  *reinterpret_cast<float4*>(&s_nu[rg][4 * c4]) = nu;
+  if (c4 == 0) {
+    s_hl[rg] = hl;
+    s_nl[rg] = nl;
+  }
+  // the second tile's loads only now: with both tiles' loads ahead of the
+  // partial sums, more loads would be in flight than the vector memory
+  // counter can tell apart, and the sums would wait for the tiles
+  if (DB && w + kTailWaves < nm)
+    t.load(K + tile(w + kTailWaves), V + tile(w + kTailWaves), 0, kw2, vw2);
+  // ---- the misses' states with the online softmax
   float m = -INFINITY, l = 0.f, acc[TT::DPL];
-  float nl = 0.f, nacc[TT::DPL];
 #pragma unroll
-  for (int e = 0; e < TT::DPL; ++e) acc[e] = nacc[e] = 0.f;
-  for (int x = w; x < jobs; x += kTailWaves) {
-    const bool neg = x >= nm;
-    float fm = lowm;
-    if constexpr (ONE) {
+  for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
+  if constexpr (DB) {
+    // two register buffers: tile x computes while tile x + 8 is in flight
+    for (int x = w; x < nm; x += 2 * kTailWaves) {
+      t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+      if (x + 2 * kTailWaves < nm)
+        t.load(K + tile(x + 2 * kTailWaves), V + tile(x + 2 * kTailWaves), 0, kw, vw);
+      if (x + kTailWaves < nm) {
+        t.template update<false, false>(qw, kw2, vw2, 0, a.kv.b, scale, m, l, acc);
+        if (x + 3 * kTailWaves < nm)
+          t.load(K + tile(x + 3 * kTailWaves), V + tile(x + 3 * kTailWaves), 0, kw2, vw2);
+      }
+    }
+  } else if constexpr (ONE) {
+    for (int x = w; x < nm; x += kTailWaves) {
       if (x != w) t.load(K + tile(x), V + tile(x), 0, kw, vw);
-      float s[UP];
-      t.scores(qw, kw, 0, a.kv.b, scale, s);
-      if (neg) t.template accumulate<true, false>(s, vw, fm, nl, nacc);
-      else t.template accumulate<false, false>(s, vw, m, l, acc);
-    } else {
+      t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+    }
+  } else {
+    for (int x = w; x < nm; x += kTailWaves) {
       for (int t0 = 0; t0 < a.kv.b; t0 += TT::CH) {
         t.load(K + tile(x), V + tile(x), t0, kw, vw);
-        float s[UP];
-        t.scores(qw, kw, t0, a.kv.b, scale, s);
-        if (neg) t.template accumulate<true, false>(s, vw, fm, nl, nacc);
-        else t.template accumulate<false, false>(s, vw, m, l, acc);
+        t.template update<false, false>(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
       }
     }
   }
   if (lane_id() == 0) {
     s_wm[w] = m;
     s_wl[w] = l;
-    s_nl[w] = nl;
   }
   t.store(s_wu[w], acc);
-  t.store(s_nu[w], nacc);
   __syncthreads();
   // ---- guarded merge (signed_fused.py:98-122), one thread per dim
   float frac = 1.f, o = 0.f;
@@ -320,12 +338,9 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     if (lowhit) {
       float nls = 0.f, nus = 0.f, lus = 0.f, env = 0.f;
 #pragma unroll
-      for (int x = 0; x < kTailWaves; ++x) {
-        nls += s_nl[x];
-        nus += s_nu[x][tid];
-      }
-#pragma unroll
       for (int g = 0; g < RG; ++g) {
+        nls += s_nl[g];
+        nus += s_nu[g][tid];
         lus += s_lu[g][tid];
         env += s_la[g][tid];
       }
@@ -368,7 +383,7 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     a.bad[h] = fallback ? 1 : 0;
     a.remain[h] = frac;
     a.pos[h] = nm;
-    a.total[h] = jobs;
+    a.total[h] = nm + nw;
     if (a.approx) {
       a.approx[h] = (!fallback && s_skip) ? 1 : 0;
       a.extra[h] = fallback ? 0.f : s_extra;

@@ -217,12 +217,20 @@ def case_c5(dev, seed=20261103):
             return outs
         return run
 
+    def fused_step(eps):
+        def run(i):
+            return [step_mod.speculative_signed_step(q, k, v, lo, hi, p, cf["topk"], "hybrid",
+                                                     0.2, max_extra_mass=eps).result.output
+                    for q, k, v, lo, hi, _, p in reqs]
+        return run
+
     def serial(i):
         return [gqa.exact(q, k, v, gqa.select_blocks(q, lo, hi, cf["topk"]))
                 for q, k, v, lo, hi, _, _ in reqs]
 
     graphs, outs = {}, {}
-    for name, fn in (("signed_eps0.01", full(0.01)), ("signed_strict", full(0.0)),
+    for name, fn in (("step_eps0.01", fused_step(0.01)), ("step_strict", fused_step(0.0)),
+                     ("signed_eps0.01", full(0.01)), ("signed_strict", full(0.0)),
                      ("serial", serial)):
         graphs[name], outs[name] = timing.capture(lambda fn=fn: fn(0))
     g = cf["hq"] // cf["hkv"]
@@ -240,8 +248,9 @@ def case_c5(dev, seed=20261103):
         full_b += kv + meta + cf["hq"] * cf["topk"] * (cf["dim"] + 2) * 4 * 2 + small
         ser_b += meta + u_a * tile + small
     case = Case("c5", "per request: gqa.select_blocks || kernels.speculate('hybrid', 0.2, "
-                "keep_mass) -> signed_fused.repair_signed_fused (eps 0.01 and strict)",
-                graphs, 1, full_b, kv_b, ser_b, primary="signed_eps0.01",
+                "keep_mass) -> signed_fused.repair_signed_fused (eps 0.01 and strict): the "
+                "fused two-launch step (step_*) and the two-stream composition (signed_*)",
+                graphs, 1, full_b, kv_b, ser_b, primary="step_eps0.01",
                 notes=f"16 requests, contexts {int(blocks.min()) * 32}-{int(blocks.max()) * 32} "
                       "tokens; one graph replay = one batched decode step")
     for r, (q, k, v, lo, hi, sel, p) in enumerate(reqs):
@@ -259,6 +268,10 @@ def case_c5(dev, seed=20261103):
                            (hq_, ks, vs, sel_r, outs["serial"][r].cpu())))
         case.check.append((f"eps0.01[{r}]", "signed_fused",
                            (hq_, ks, vs, sel_r, p_r, 0.01, outs["signed_eps0.01"][r].cpu())))
+        case.check.append((f"step_strict[{r}]", "attention",
+                           (hq_, ks, vs, sel_r, outs["step_strict"][r].cpu())))
+        case.check.append((f"step_eps0.01[{r}]", "signed_fused",
+                           (hq_, ks, vs, sel_r, p_r, 0.01, outs["step_eps0.01"][r].cpu())))
     return case
 
 
