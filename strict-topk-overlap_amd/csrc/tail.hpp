@@ -89,10 +89,8 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   __syncthreads();
   if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
   // ---- exact top-K (its first barrier orders the map writes above)
-  int32_t* out_ids = a.ids + (size_t)h * a.k;
   topk_select_keys<KPT>(key, n, a.k, tl, [&](int pos, int idx) {
     sel[pos] = idx;
-    out_ids[pos] = idx;
     atomicOr(&map[idx], kSelFlag);
   });
   __syncthreads();
@@ -139,6 +137,9 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   // the entry loads (u rows, query) returned during the top-K
   vm_drain();
   if (ONE && w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
+  // the selected IDs go out behind the tile loads (stores count in the same
+  // vector memory counter, so stores issued before the drain would hold it)
+  for (int i = tid; i < a.k; i += kTailThreads) a.ids[(size_t)h * a.k + i] = sel[i];
   // ---- the hits' (or, for union, every predicted row's) partial LSE sums
   uint64_t um4[kTailMaxK / 64];
 #pragma unroll

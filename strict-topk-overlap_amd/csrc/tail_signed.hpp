@@ -20,21 +20,25 @@
 // inputs allow):
 //   1. keys, predicted row, query row and every predicted state (m, l, u);
 //      the u rows stay in registers (RPT rows of four columns per thread);
-//   2. top-K; then wave 0 does the per-slot work (grouping, membership,
-//      keep / low / wrong sets, the extra-mass test) while wave 1 lists the
-//      misses;
-//   3. the missed blocks' K/V tiles (wave w takes misses w, w + 8, ..., two
-//      tiles in flight), folded with an online softmax, overlapped with the
-//      partial sums of the registered u rows: the kept states, the low
+//   2. top-K; then every wave lists its own misses and issues their tile
+//      loads at once (wave w takes misses w, w + 8, ..., two tiles in
+//      flight), and wave 0 does the per-slot work (grouping, membership,
+//      keep / low / wrong sets, the extra-mass test) while they travel;
+//   3. the partial sums of the registered u rows: the kept states, the low
 //      aggregate with its envelope, and the wrong low blocks' corrections.
 //      A wrong block's correction in the reference (_corrections :52-61) is
 //      its block-local state (max m, l, u of the recomputed tile) times
 //      exp(m - low_m); that state is the prediction state this step's front
 //      computed for the same block with the same arithmetic, so it is taken
-//      from the registered rows instead of re-reading the tile;
+//      from the registered rows instead of re-reading the tile; then the
+//      missed tiles, folded with an online softmax;
 //   4. one merge by D threads, the guard flags OR-ed through LDS, and on a
-//      flagged head the strict online softmax over the selected tiles.
+//      flagged head the strict softmax over the selected blocks, merged
+//      from their exact block states (hits from the registered rows, misses
+//      from the waves' online states).
 #pragma once
+
+#include <type_traits>
 
 #include "topk.hpp"
 #include "tile2.hpp"
@@ -70,14 +74,17 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
   __shared__ float s_pm[kTailMaxK], s_pl[kTailMaxK];
   __shared__ TopkLds tl;
-  __shared__ int s_nm, s_nw, s_lowhit, s_skip, s_bad;
-  __shared__ float s_lowm, s_ll, s_mk, s_extra;
-  __shared__ uint64_t s_keep[SW], s_low[SW], s_wrong[SW];
-  __shared__ float s_hl[RG], s_nl[RG];
-  __shared__ __align__(16) float s_hu[RG][D];
-  __shared__ __align__(16) float s_lu[RG][D];
-  __shared__ __align__(16) float s_la[RG][D];
-  __shared__ __align__(16) float s_nu[RG][D];
+  __shared__ int s_nw, s_lowhit, s_skip, s_bad;
+  __shared__ float s_lowm, s_ll, s_mk, s_mu, s_extra;
+  __shared__ uint64_t s_keep[SW], s_low[SW], s_wrong[SW], s_used[SW];
+  // partial sums of the registered rows, one row per wave (row groups that
+  // share a wave are folded in registers first)
+  __shared__ float s_hl[kTailWaves], s_nl[kTailWaves], s_sl[kTailWaves];
+  __shared__ __align__(16) float s_hu[kTailWaves][D];
+  __shared__ __align__(16) float s_lu[kTailWaves][D];
+  __shared__ __align__(16) float s_la[kTailWaves][D];
+  __shared__ __align__(16) float s_nu[kTailWaves][D];
+  __shared__ __align__(16) float s_su[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves];
   __shared__ float s_wu[kTailWaves][D];
   const int h = blockIdx.x;
@@ -114,30 +121,36 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   __syncthreads();
   if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
   // ---- exact top-K (its first barrier orders the map writes above)
-  int32_t* out_ids = a.ids + (size_t)h * a.k;
   topk_select_keys<KPT>(key, n, a.k, tl, [&](int pos, int idx) {
     sel[pos] = idx;
-    out_ids[pos] = idx;
     atomicOr(&map[idx], kSelFlag);
   });
   __syncthreads();
-  if (w == 0) {
-    // ---- per-slot work, lane l holding slots l, l + 64, ...
-    float pm_[SW], pl_[SW];
-    bool ok[SW], hit[SW], real[SW];
-    float gm = -INFINITY;
+  // ---- per-slot work (wave 0), lane l holding slots l, l + 64, ...; SWN
+  // slot words, one when SP <= 64 (a single wave runs this part alone, so
+  // its instruction count is latency)
+  auto slots = [&](auto swn) {
+    constexpr int SWN = decltype(swn)::value;
+    float pm_[SWN], pl_[SWN];
+    bool ok[SWN], hit[SWN], real[SWN], used[SWN];
+    float gm = -INFINITY, mu = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < SW; ++c) {
+    for (int c = 0; c < SWN; ++c) {
       const int p = c * STK_WAVE + lane_id();
       ok[c] = p < sp;
       pm_[c] = ok[c] ? s_pm[p] : -INFINITY;
       pl_[c] = ok[c] ? s_pl[p] : 0.f;
       const int id = ok[c] ? pids[p] : -1;
       real[c] = id >= 0 && id < n;
-      hit[c] = real[c] && (map[id] & kSelFlag) != 0;
+      const int mv = real[c] ? map[id] : 0;
+      hit[c] = (mv & kSelFlag) != 0;
+      // each selected block once (its highest slot), for the strict merge
+      used[c] = hit[c] && (mv & ~kSelFlag) == p + 1;
       gm = fmaxf(gm, pm_[c]);
+      mu = used[c] ? fmaxf(mu, pm_[c]) : mu;
     }
-    bool high[SW], low[SW], wrong[SW], keep[SW];
+    mu = wave_max_u(mu);
+    bool high[SWN], low[SWN], wrong[SWN], keep[SWN];
     float lowm = 0.f, ll = 0.f;
     bool lowhit = false;
     if (hybrid) {
@@ -145,11 +158,11 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
       gm = wave_max_u(gm);
       float tot = 0.f;
 #pragma unroll
-      for (int c = 0; c < SW; ++c) tot += wexp(pm_[c], gm) * pl_[c];
+      for (int c = 0; c < SWN; ++c) tot += wexp(pm_[c], gm) * pl_[c];
       tot = wave_sum_u(tot);
       float lm = -INFINITY;
 #pragma unroll
-      for (int c = 0; c < SW; ++c) {
+      for (int c = 0; c < SWN; ++c) {
         high[c] = ok[c] && wexp(pm_[c], gm) * pl_[c] >= a.tau * tot;
         low[c] = ok[c] && !high[c];
         lm = low[c] ? fmaxf(lm, pm_[c]) : lm;
@@ -159,14 +172,14 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
       float x = 0.f;
       bool lh = false;
 #pragma unroll
-      for (int c = 0; c < SW; ++c) {
+      for (int c = 0; c < SWN; ++c) {
         x += low[c] ? wexp(pm_[c], lowm) * pl_[c] : 0.f;
         lh = lh || (hit[c] && low[c]);
       }
       ll = wave_sum_u(x);
       lowhit = __ballot(lh) != 0ull;
 #pragma unroll
-      for (int c = 0; c < SW; ++c) {
+      for (int c = 0; c < SWN; ++c) {
         // an ID outside [0, n) has the empty state (-inf, 0, 0): nothing to
         // subtract, and no tile to read
         wrong[c] = lowhit && low[c] && !hit[c] && real[c];
@@ -174,26 +187,26 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
       }
     } else {
 #pragma unroll
-      for (int c = 0; c < SW; ++c) {
+      for (int c = 0; c < SWN; ++c) {
         high[c] = low[c] = wrong[c] = false;
         keep[c] = hit[c];
       }
     }
     float mk = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < SW; ++c) mk = keep[c] ? fmaxf(mk, pm_[c]) : mk;
+    for (int c = 0; c < SWN; ++c) mk = keep[c] ? fmaxf(mk, pm_[c]) : mk;
     mk = wave_max_u(mk);
     // signed_repair.py:61-72: skip the wrong blocks when their mass is small
     bool skip = false;
     float ex = 0.f;
     bool anyw = false;
 #pragma unroll
-    for (int c = 0; c < SW; ++c) anyw = anyw || wrong[c];
+    for (int c = 0; c < SWN; ++c) anyw = anyw || wrong[c];
     if (hybrid && a.eps > 0.f && __ballot(anyw) != 0ull) {
       const float ref = fmaxf(lowm, mk);
       float dk = 0.f, dw = 0.f;
 #pragma unroll
-      for (int c = 0; c < SW; ++c) {
+      for (int c = 0; c < SWN; ++c) {
         dk += keep[c] ? wexp(pm_[c], ref) * pl_[c] : 0.f;
         dw += wrong[c] ? wexp(pm_[c], ref) * pl_[c] : 0.f;
       }
@@ -203,14 +216,15 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     }
     int nw = 0;
 #pragma unroll
-    for (int c = 0; c < SW; ++c) {
+    for (int c = 0; c < SWN; ++c) {
       const uint64_t wb = __ballot(wrong[c] && !skip);
       nw += (int)__popcll(wb);
-      const uint64_t kb = __ballot(keep[c]), lb = __ballot(low[c]);
+      const uint64_t kb = __ballot(keep[c]), lb = __ballot(low[c]), ub = __ballot(used[c]);
       if (lane_id() == 0) {
         s_keep[c] = kb;
         s_low[c] = lb;
         s_wrong[c] = wb;
+        s_used[c] = ub;
       }
     }
     if (lane_id() == 0) {
@@ -218,29 +232,32 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
       s_lowm = lowm;
       s_ll = ll;
       s_mk = mk;
+      s_mu = mu;
       s_lowhit = lowhit ? 1 : 0;
       s_skip = skip ? 1 : 0;
       s_extra = skip ? ex : 0.f;
     }
-  } else if (w == 1) {
-    // ---- misses (selected, not predicted) in ascending block order
-    int cnt = 0;
-    for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
-      const int p = p0 + lane_id();
-      const bool in = p < a.k;
-      const int id = in ? sel[p] : 0;
-      const bool ms = in && (map[id] & ~kSelFlag) == 0;
-      const uint64_t bal = __ballot(ms);
-      if (ms) miss[cnt + (int)__popcll(bal & lanemask_lt())] = id;
-      cnt += (int)__popcll(bal);
-    }
-    if (lane_id() == 0) s_nm = cnt;
+#pragma unroll
+    for (int c = SWN; c < SW; ++c)
+      if (lane_id() == 0) s_keep[c] = s_low[c] = s_wrong[c] = s_used[c] = 0ull;
+  };
+  // ---- misses (selected, not predicted) in ascending block order, listed
+  // by every wave for itself: wave w keeps misses w, w + 8, ... (its own
+  // entries of the list, read back only by it) and the count, so its tile
+  // loads go out before the per-slot work and the barrier below
+  int nm = 0;
+  for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
+    const int p = p0 + lane_id();
+    const bool in = p < a.k;
+    const int id = in ? sel[p] : 0;
+    const bool ms = in && (map[id] & ~kSelFlag) == 0;
+    const uint64_t bal = __ballot(ms);
+    const int x = nm + (int)__popcll(bal & lanemask_lt());
+    if (ms && x % kTailWaves == w) miss[x] = id;
+    nm += (int)__popcll(bal);
   }
-  __syncthreads();
-  const int nm = s_nm, nw = s_nw;
-  const float lowm = s_lowm, mk = s_mk;
-  // ---- round trip 2: wave w streams misses w, w + 8, ...; its first two
-  // tiles' loads are issued before the partial sums below
+  // ---- round trip 2: wave w streams misses w, w + 8, ..., two tiles in
+  // flight when they fit
   const int kvh = h / G;
   const float scale = 1.0f / sqrtf((float)D);
   const T* K = reinterpret_cast<const T*>(a.kv.k);
@@ -248,15 +265,27 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   auto tile = [&](int x) { return (((size_t)kvh * n + miss[x]) * a.kv.b) * D; };
   uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
   uint32_t kw2[UP][TT::QW], vw2[TT::CH][TT::VW];
-  // the entry loads (u rows, query) returned during the top-K
+  // the entry loads (u rows, query) returned during the top-K; after this
+  // wait the compiler knows it, and the sums below never wait for the tiles
   vm_drain();
   if (ONE && w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
+  if (DB && w + kTailWaves < nm)
+    t.load(K + tile(w + kTailWaves), V + tile(w + kTailWaves), 0, kw2, vw2);
+  // the selected IDs go out behind the tile loads
+  for (int i = tid; i < a.k; i += kTailThreads) a.ids[(size_t)h * a.k + i] = sel[i];
+  if (w == 0) {
+    if (sp <= STK_WAVE) slots(std::integral_constant<int, 1>{});
+    else slots(std::integral_constant<int, SW>{});
+  }
+  __syncthreads();
+  const int nw = s_nw;
+  const float lowm = s_lowm, mk = s_mk, mu = s_mu;
   // ---- partial sums of the registered u rows: kept states relative to mk;
   // the low aggregate, its envelope and the wrong blocks' corrections
   // relative to low_m
-  float hl = 0.f, nl = 0.f;
+  float hl = 0.f, nl = 0.f, sl = 0.f;
   float4 hu = make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 lu = hu, la = hu, nu = hu;
+  float4 lu = hu, la = hu, nu = hu, su = hu;
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int r = rg + RG * j;   // < 16 * RG <= 512
@@ -266,34 +295,58 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     // would live in scratch memory, whose loads share the vector memory
     // counter with the tile loads in flight and would wait for them)
     const uint64_t kword = s_keep[wd], lword = s_low[wd], wword = s_wrong[wd];
+    const uint64_t uword = s_used[wd];
     const bool kp = r < sp && ((kword >> bit) & 1ull);
     const bool lo = r < sp && ((lword >> bit) & 1ull);
     const bool wr = r < sp && ((wword >> bit) & 1ull);
+    const bool us = r < sp && ((uword >> bit) & 1ull);
     const float pm = s_pm[rr], pl = s_pl[rr];
     const float wk = kp ? wexp(pm, mk) : 0.f;
     const float wl = lo ? wexp(pm, lowm) : 0.f;
     const float wn = wr ? wl : 0.f;
+    const float ws = us ? wexp(pm, mu) : 0.f;
     hl += wk * pl;
     nl += wn * pl;
+    sl += ws * pl;
     hu.x += wk * uu[j].x; hu.y += wk * uu[j].y; hu.z += wk * uu[j].z; hu.w += wk * uu[j].w;
     lu.x += wl * uu[j].x; lu.y += wl * uu[j].y; lu.z += wl * uu[j].z; lu.w += wl * uu[j].w;
     la.x += wl * fabsf(uu[j].x); la.y += wl * fabsf(uu[j].y);
     la.z += wl * fabsf(uu[j].z); la.w += wl * fabsf(uu[j].w);
     nu.x += wn * uu[j].x; nu.y += wn * uu[j].y; nu.z += wn * uu[j].z; nu.w += wn * uu[j].w;
+    su.x += ws * uu[j].x; su.y += ws * uu[j].y; su.z += ws * uu[j].z; su.w += ws * uu[j].w;
   }
-  *reinterpret_cast<float4*>(&s_hu[rg][4 * c4]) = hu;
-  *reinterpret_cast<float4*>(&s_lu[rg][4 * c4]) = lu;
-  *reinterpret_cast<float4*>(&s_la[rg][4 * c4]) = la;
-  *reinterpret_cast<float4*>(&s_nu[rg][4 * c4]) = nu;
-  if (c4 == 0) {
-    s_hl[rg] = hl;
-    s_nl[rg] = nl;
+  // fold the row groups of this wave (lanes with the same columns)
+#pragma unroll
+  for (int off = TPR; off < STK_WAVE; off <<= 1) {
+    hl += __shfl_xor(hl, off);
+    nl += __shfl_xor(nl, off);
+    hu.x += __shfl_xor(hu.x, off); hu.y += __shfl_xor(hu.y, off);
+    hu.z += __shfl_xor(hu.z, off); hu.w += __shfl_xor(hu.w, off);
+    lu.x += __shfl_xor(lu.x, off); lu.y += __shfl_xor(lu.y, off);
+    lu.z += __shfl_xor(lu.z, off); lu.w += __shfl_xor(lu.w, off);
+    la.x += __shfl_xor(la.x, off); la.y += __shfl_xor(la.y, off);
+    la.z += __shfl_xor(la.z, off); la.w += __shfl_xor(la.w, off);
+    nu.x += __shfl_xor(nu.x, off); nu.y += __shfl_xor(nu.y, off);
+    nu.z += __shfl_xor(nu.z, off); nu.w += __shfl_xor(nu.w, off);
+    sl += __shfl_xor(sl, off);
+    su.x += __shfl_xor(su.x, off); su.y += __shfl_xor(su.y, off);
+    su.z += __shfl_xor(su.z, off); su.w += __shfl_xor(su.w, off);
   }
-  // the second tile's loads only now: with both tiles' loads ahead of the
-  // partial sums, more loads would be in flight than the vector memory
-  // counter can tell apart, and the sums would wait for the tiles
-  if (DB && w + kTailWaves < nm)
-    t.load(K + tile(w + kTailWaves), V + tile(w + kTailWaves), 0, kw2, vw2);
+  // a wave holds STK_WAVE / TPR row groups; with TPR > STK_WAVE (D = 512)
+  // a row group spans waves, which the fused step does not support
+  static_assert(TPR <= STK_WAVE, "state rows wider than a wave");
+  if (lane_id() < TPR) {
+    *reinterpret_cast<float4*>(&s_hu[w][4 * c4]) = hu;
+    *reinterpret_cast<float4*>(&s_lu[w][4 * c4]) = lu;
+    *reinterpret_cast<float4*>(&s_la[w][4 * c4]) = la;
+    *reinterpret_cast<float4*>(&s_nu[w][4 * c4]) = nu;
+    *reinterpret_cast<float4*>(&s_su[w][4 * c4]) = su;
+  }
+  if (lane_id() == 0) {
+    s_hl[w] = hl;
+    s_nl[w] = nl;
+    s_sl[w] = sl;
+  }
   // ---- the misses' states with the online softmax
   float m = -INFINITY, l = 0.f, acc[TT::DPL];
 #pragma unroll
@@ -338,7 +391,7 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     if (lowhit) {
       float nls = 0.f, nus = 0.f, lus = 0.f, env = 0.f;
 #pragma unroll
-      for (int g = 0; g < RG; ++g) {
+      for (int g = 0; g < kTailWaves; ++g) {
         nls += s_nl[g];
         nus += s_nu[g][tid];
         lus += s_lu[g][tid];
@@ -360,7 +413,7 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     const float fk = wexp(mk, M), fl = wexp(lm_eff, M);
     float hls = 0.f, hus = 0.f;
 #pragma unroll
-    for (int g = 0; g < RG; ++g) {
+    for (int g = 0; g < kTailWaves; ++g) {
       hls += s_hl[g];
       hus += s_hu[g][tid];
     }
@@ -393,30 +446,25 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     if (tid < D) a.out[(size_t)h * D + tid] = o;
     return;
   }
-  // ---- strict fallback (signed_fused.py:123-142): online softmax over the
-  // selected blocks, wave w taking selected w, w + 8, ...
-  m = -INFINITY;
-  l = 0.f;
-#pragma unroll
-  for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
-  for (int x = w; x < a.k; x += kTailWaves) {
-    const size_t off = (((size_t)kvh * n + sel[x]) * a.kv.b) * D;
-    for (int t0 = 0; t0 < a.kv.b; t0 += TT::CH) {
-      t.load(K + off, V + off, t0, kw, vw);
-      t.template update<false, false>(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
-    }
-  }
-  if (lane_id() == 0) {
-    s_wm[w] = m;
-    s_wl[w] = l;
-  }
-  t.store(s_wu[w], acc);
-  __syncthreads();
+  // ---- strict fallback (signed_fused.py:123-142): the softmax over the
+  // selected blocks alone.  Every selected block's exact block-local state
+  // is at hand (the predicted ones in the registered rows, each block once;
+  // the missed ones in the waves' online states), so the fallback merges
+  // those with positive weights (no signed term, no second pass over the
+  // tiles) instead of streaming the selected tiles again.
   if (tid < D) {
-    float M = -INFINITY;
+    float M = mu;
 #pragma unroll
     for (int x = 0; x < kTailWaves; ++x) M = fmaxf(M, s_wm[x]);
+    const float fs = wexp(mu, M);
     float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int g = 0; g < kTailWaves; ++g) {
+      den += s_sl[g];
+      num += s_su[g][tid];
+    }
+    num *= fs;
+    den *= fs;
 #pragma unroll
     for (int x = 0; x < kTailWaves; ++x) {
       const float f = wexp(s_wm[x], M);
