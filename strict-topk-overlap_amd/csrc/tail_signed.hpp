@@ -63,13 +63,13 @@ struct STailArgs {
 
 template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
 __device__ __forceinline__ void stail_head(const STailArgs& a) {
-  using TT = TokTile<T, NCH, UP>;
+  using TT = TokTileW<T, NCH, UP>;
   constexpr int D = TT::D;
   constexpr int TPR = D / 4;              // threads per state row (16-byte loads)
   constexpr int RG = kTailThreads / TPR;  // rows per pass of the state prefetch
   constexpr int SW = kTailMaxK / STK_WAVE;   // slot words of wave 0
   // two tile buffers in flight when they fit the register budget
-  constexpr bool DB = ONE && RPT == 4 && UP * TT::QW + TT::CH * TT::VW <= 64;
+  constexpr bool DB = ONE && RPT == 4 && UP * TT::QW + 4 * TT::NV <= 64;
   __shared__ int map[kTailMapN];
   __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
   __shared__ float s_pm[kTailMaxK], s_pl[kTailMaxK];
@@ -263,8 +263,10 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   const T* K = reinterpret_cast<const T*>(a.kv.k);
   const T* V = reinterpret_cast<const T*>(a.kv.v);
   auto tile = [&](int x) { return (((size_t)kvh * n + miss[x]) * a.kv.b) * D; };
-  uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
-  uint32_t kw2[UP][TT::QW], vw2[TT::CH][TT::VW];
+  uint32_t kw[UP][TT::QW];
+  uint4 vw[TT::NV];
+  uint32_t kw2[UP][TT::QW];
+  uint4 vw2[TT::NV];
   // the entry loads (u rows, query) returned during the top-K; after this
   // wait the compiler knows it, and the sums below never wait for the tiles
   vm_drain();
@@ -348,17 +350,17 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     s_sl[w] = sl;
   }
   // ---- the misses' states with the online softmax
-  float m = -INFINITY, l = 0.f, acc[TT::DPL];
+  float m = -INFINITY, l = 0.f, acc[TT::ACC];
 #pragma unroll
-  for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
+  for (int e = 0; e < TT::ACC; ++e) acc[e] = 0.f;
   if constexpr (DB) {
     // two register buffers: tile x computes while tile x + 8 is in flight
     for (int x = w; x < nm; x += 2 * kTailWaves) {
-      t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+      t.update(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
       if (x + 2 * kTailWaves < nm)
         t.load(K + tile(x + 2 * kTailWaves), V + tile(x + 2 * kTailWaves), 0, kw, vw);
       if (x + kTailWaves < nm) {
-        t.template update<false, false>(qw, kw2, vw2, 0, a.kv.b, scale, m, l, acc);
+        t.update(qw, kw2, vw2, 0, a.kv.b, scale, m, l, acc);
         if (x + 3 * kTailWaves < nm)
           t.load(K + tile(x + 3 * kTailWaves), V + tile(x + 3 * kTailWaves), 0, kw2, vw2);
       }
@@ -366,13 +368,13 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   } else if constexpr (ONE) {
     for (int x = w; x < nm; x += kTailWaves) {
       if (x != w) t.load(K + tile(x), V + tile(x), 0, kw, vw);
-      t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+      t.update(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
     }
   } else {
     for (int x = w; x < nm; x += kTailWaves) {
       for (int t0 = 0; t0 < a.kv.b; t0 += TT::CH) {
         t.load(K + tile(x), V + tile(x), t0, kw, vw);
-        t.template update<false, false>(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
+        t.update(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
       }
     }
   }

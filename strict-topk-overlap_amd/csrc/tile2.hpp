@@ -198,6 +198,98 @@ struct TokTile {
 
 // Token passes per chunk for block size B: the largest UP in {2, 1} with
 // 16 * UP dividing B; 0 when B is not a multiple of 16.
+// The token tile with wide V loads, for single-workgroup kernels that keep
+// several tiles in flight per wave (the signed step's tail).  Q.K is that of
+// TokTile.  V is loaded 16 bytes per lane: a row of D elements spans
+// LPR = D / 8 lanes and one load instruction covers RPI = 64 / LPR rows, so
+// a 32-token chunk of D = 128 is 8 loads instead of 32 (a wave may have at
+// most 63 vector memory instructions outstanding; with one load per token
+// row, two tiles in flight exceed that and the wave stalls until the first
+// returns).  Lane l accumulates dims 8 (l % LPR) .. + 7 over the rows
+// RPI i + l / LPR; each token's weight comes from its Q.K lane with one
+// ds_bpermute per load, and the RPI lane groups are folded once, in store().
+template <typename T, int NCH, int UP>
+struct TokTileW : TokTile<T, NCH, UP> {
+  using B = TokTile<T, NCH, UP>;
+  static_assert(sizeof(T) == 2, "wide V rows take 16-bit elements");
+  static constexpr int D = B::D, CH = B::CH, QW = B::QW, TPP = B::TPP, LPT = B::LPT;
+  static constexpr int LPR = D / 8;              // lanes per V row
+  static constexpr int RPI = STK_WAVE / LPR;     // V rows per load instruction
+  static constexpr int NV = CH / RPI;            // V loads per chunk
+  static constexpr int ACC = 8;                  // accumulated dims per lane
+  static_assert(LPR <= STK_WAVE && CH % RPI == 0 && TPP % RPI == 0,
+                "V rows must tile the chunk");
+
+  __device__ __forceinline__ void load(const T* kb, const T* vb, int t0,
+                                       uint32_t (&kw)[UP][QW], uint4 (&vw)[NV]) const {
+    const T* krow = kb + (size_t)(t0 + this->slot) * D;
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        uint4 x = *reinterpret_cast<const uint4*>(krow + (size_t)TPP * u * D + this->kdim(c));
+        kw[u][4 * c + 0] = x.x; kw[u][4 * c + 1] = x.y; kw[u][4 * c + 2] = x.z;
+        kw[u][4 * c + 3] = x.w;
+      }
+    }
+    const T* vrow = vb + (size_t)(t0 + lane_id() / LPR) * D + 8 * (lane_id() % LPR);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) vw[i] = *reinterpret_cast<const uint4*>(vrow + (size_t)i * RPI * D);
+  }
+
+  // Online softmax over one chunk (token t0 + j valid when < B).
+  __device__ __forceinline__ void update(const uint32_t* qw, const uint32_t (&kw)[UP][QW],
+                                         const uint4 (&vw)[NV], int t0, int Bn, float scale,
+                                         float& m, float& l, float (&acc)[ACC]) const {
+    float s[UP];
+    this->scores(qw, kw, t0, Bn, scale, s);
+    float cm = s[0];
+#pragma unroll
+    for (int u = 1; u < UP; ++u) cm = fmaxf(cm, s[u]);
+    cm = wave_max_u(cm);
+    const float nm = fmaxf(m, cm);
+    if (nm > m) {
+      const float alpha = wexp(m, nm);
+      l *= alpha;
+#pragma unroll
+      for (int e = 0; e < ACC; ++e) acc[e] *= alpha;
+      m = nm;
+    }
+    float w[UP], ws = 0.f;
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      w[u] = wexp(s[u], m);
+      ws += this->part == 0 ? w[u] : 0.f;
+    }
+    l += wave_sum_u(ws);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int u = (RPI * i) / TPP;                       // same pass for the whole load
+      const int tk = (RPI * i) % TPP + lane_id() / LPR;    // token slot within the pass
+      const float wt = __shfl(w[u], tk * LPT);
+      const uint32_t x[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += wt * Elem<T>::lo(x[e]);
+        acc[2 * e + 1] += wt * Elem<T>::hi(x[e]);
+      }
+    }
+  }
+
+  // Fold the lane groups and write D floats (times `scale`) to dst.
+  __device__ __forceinline__ void store(float* dst, float (&acc)[ACC], float scale = 1.f) const {
+#pragma unroll
+    for (int off = LPR; off < STK_WAVE; off <<= 1)
+#pragma unroll
+      for (int e = 0; e < ACC; ++e) acc[e] += __shfl_xor(acc[e], off);
+    if (lane_id() < LPR) {
+      float4* p = reinterpret_cast<float4*>(dst + 8 * lane_id());
+      p[0] = make_float4(acc[0] * scale, acc[1] * scale, acc[2] * scale, acc[3] * scale);
+      p[1] = make_float4(acc[4] * scale, acc[5] * scale, acc[6] * scale, acc[7] * scale);
+    }
+  }
+};
+
 inline int tok_up(int b) { return b % 32 == 0 ? 2 : (b % 16 == 0 ? 1 : 0); }
 
 // Token-tile shape for (dtype, D, B): NCH chunks per lane; 0 when unsupported.
