@@ -11,9 +11,10 @@
 //      state (m, l, u) are requested together at entry;
 //   2. the missed blocks' K/V tiles, once the top-K is known.
 // In between: top-K (two barriers per radix pass), membership through an
-// LDS map over block IDs (max predicted slot + 1, plus a selected flag) and
-// a bit mask of the predicted slots to merge, and the hits' LSE partial sums
-// from registers.
+// LDS map over block IDs (max predicted slot + 1, plus a selected flag),
+// each wave's own misses (their tile loads go out at once), and the hits'
+// LSE partial sums from registers, per wave, with no further barrier before
+// the merge.
 #pragma once
 
 #include "topk.hpp"
@@ -50,10 +51,9 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
   __shared__ float s_pm[kTailMaxK], s_pl[kTailMaxK];
   __shared__ TopkLds tl;
-  __shared__ int s_nm;
-  __shared__ uint64_t s_used[kTailMaxK / 64];   // predicted slots whose state is merged
-  __shared__ float s_hmax[kTailWaves], s_hl[RG];
-  __shared__ __align__(16) float s_hu[RG][D];
+  // the hits' partial sums, one row per wave (relative to the wave's max)
+  __shared__ float s_hmax[kTailWaves], s_hl[kTailWaves];
+  __shared__ __align__(16) float s_hu[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_wu[kTailWaves][D];
   const int h = blockIdx.x;
   const int n = a.kv.n, sp = a.sp;
@@ -94,36 +94,20 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
     atomicOr(&map[idx], kSelFlag);
   });
   __syncthreads();
-  // ---- misses (selected, not predicted) in ascending block order (wave 0),
-  // and the predicted slots whose states are merged (wave 1): saved mode
-  // takes slot p when P[p] is selected and p is the highest slot holding
-  // that block; union mode takes every slot
-  if (w == 0) {
-    int cnt = 0;
-    for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
-      const int p = p0 + lane_id();
-      const bool in = p < a.k;
-      const int id = in ? sel[p] : 0;
-      const bool ms = in && (map[id] & ~kSelFlag) == 0;
-      const uint64_t bal = __ballot(ms);
-      if (ms) miss[cnt + (int)__popcll(bal & lanemask_lt())] = id;
-      cnt += (int)__popcll(bal);
-    }
-    if (lane_id() == 0) s_nm = cnt;
-  } else if (w == 1) {
-    for (int p0 = 0; p0 < kTailMaxK; p0 += STK_WAVE) {
-      uint64_t bal = 0ull;
-      if (p0 < sp) {
-        const int p = p0 + lane_id();
-        const int pv = p < sp ? pids[p] : -1;
-        const int mv = pv >= 0 && pv < n ? map[pv] : 0;
-        bal = __ballot(p < sp && (a.uni || ((mv & kSelFlag) && (mv & ~kSelFlag) == p + 1)));
-      }
-      if (lane_id() == 0) s_used[p0 / STK_WAVE] = bal;
-    }
+  // ---- misses (selected, not predicted) in ascending block order, listed
+  // by every wave for itself: wave w keeps misses w, w + 8, ... (its own
+  // entries of the list, read back only by it) and the count
+  int nm = 0;
+  for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
+    const int p = p0 + lane_id();
+    const bool in = p < a.k;
+    const int id = in ? sel[p] : 0;
+    const bool ms = in && (map[id] & ~kSelFlag) == 0;
+    const uint64_t bal = __ballot(ms);
+    const int x = nm + (int)__popcll(bal & lanemask_lt());
+    if (ms && x % kTailWaves == w) miss[x] = id;
+    nm += (int)__popcll(bal);
   }
-  __syncthreads();
-  const int nm = s_nm;
   // ---- round trip 2: wave w streams misses w, w + 8, ...; the first
   // tile's loads are issued before the hits' arithmetic
   const int kvh = h / G;
@@ -140,10 +124,10 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   // the selected IDs go out behind the tile loads (stores count in the same
   // vector memory counter, so stores issued before the drain would hold it)
   for (int i = tid; i < a.k; i += kTailThreads) a.ids[(size_t)h * a.k + i] = sel[i];
-  // ---- the hits' (or, for union, every predicted row's) partial LSE sums
-  uint64_t um4[kTailMaxK / 64];
-#pragma unroll
-  for (int x = 0; x < kTailMaxK / 64; ++x) um4[x] = s_used[x];
+  // ---- the hits' (or, for union, every predicted row's) partial LSE sums:
+  // saved mode takes slot p when P[p] is selected and p is the highest slot
+  // holding that block; union mode takes every slot.  Each wave sums its
+  // rows relative to its own maximum (no barrier); the merge rescales.
   bool used[RPT];
   float um[RPT];
   float hm = -INFINITY;
@@ -151,29 +135,35 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   for (int j = 0; j < RPT; ++j) {
     const int r = rg + RG * j;   // < 16 * RG <= 512
     const int rr = r < kTailMaxK ? r : 0;
-    const uint64_t word = um4[0] * (rr < 64) | um4[1] * (rr >= 64 && rr < 128) |
-                          um4[2] * (rr >= 128 && rr < 192) | um4[3] * (rr >= 192);
-    used[j] = r < sp && ((word >> (rr & 63)) & 1ull);
+    const int pv = pids[rr];
+    const int mv = pv >= 0 && pv < n ? map[pv] : 0;
+    used[j] = r < sp && (a.uni || ((mv & kSelFlag) && (mv & ~kSelFlag) == r + 1));
     um[j] = s_pm[rr];
     hm = used[j] ? fmaxf(hm, um[j]) : hm;
   }
   hm = wave_max_u(hm);
-  if (lane_id() == 0) s_hmax[w] = hm;
-  __syncthreads();
-  float mh = -INFINITY;
-#pragma unroll
-  for (int x = 0; x < kTailWaves; ++x) mh = fmaxf(mh, s_hmax[x]);
   float hl = 0.f;
   float4 hu = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int r = rg + RG * j;
-    const float wt = used[j] ? wexp(um[j], mh) : 0.f;
+    const float wt = used[j] ? wexp(um[j], hm) : 0.f;
     hl += wt * s_pl[r < kTailMaxK ? r : 0];
     hu.x += wt * uu[j].x; hu.y += wt * uu[j].y; hu.z += wt * uu[j].z; hu.w += wt * uu[j].w;
   }
-  *reinterpret_cast<float4*>(&s_hu[rg][4 * c4]) = hu;
-  if (c4 == 0) s_hl[rg] = hl;
+  // fold the row groups of this wave (lanes with the same columns)
+  static_assert(TPR <= STK_WAVE, "state rows wider than a wave");
+#pragma unroll
+  for (int off = TPR; off < STK_WAVE; off <<= 1) {
+    hl += __shfl_xor(hl, off);
+    hu.x += __shfl_xor(hu.x, off); hu.y += __shfl_xor(hu.y, off);
+    hu.z += __shfl_xor(hu.z, off); hu.w += __shfl_xor(hu.w, off);
+  }
+  if (lane_id() < TPR) *reinterpret_cast<float4*>(&s_hu[w][4 * c4]) = hu;
+  if (lane_id() == 0) {
+    s_hl[w] = hl;
+    s_hmax[w] = hm;
+  }
   // ---- the misses' states with the online softmax
   float m = -INFINITY, l = 0.f, acc[TT::DPL];
 #pragma unroll
@@ -197,23 +187,15 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   __syncthreads();
   // ---- one LSE merge of the hits' partials and the waves' miss states
   if (tid < D) {
-    float M = mh;
+    float M = -INFINITY;
 #pragma unroll
-    for (int x = 0; x < kTailWaves; ++x) M = fmaxf(M, s_wm[x]);
-    const float fh = wexp(mh, M);
+    for (int x = 0; x < kTailWaves; ++x) M = fmaxf(M, fmaxf(s_hmax[x], s_wm[x]));
     float num = 0.f, den = 0.f;
 #pragma unroll
-    for (int g = 0; g < RG; ++g) {
-      num += s_hu[g][tid];
-      den += s_hl[g];
-    }
-    num *= fh;
-    den *= fh;
-#pragma unroll
     for (int x = 0; x < kTailWaves; ++x) {
-      const float f = wexp(s_wm[x], M);
-      num += f * s_wu[x][tid];
-      den += f * s_wl[x];
+      const float fh = wexp(s_hmax[x], M), f = wexp(s_wm[x], M);
+      num += fh * s_hu[x][tid] + f * s_wu[x][tid];
+      den += fh * s_hl[x] + f * s_wl[x];
     }
     a.out[(size_t)h * D + tid] = num / den;
   }

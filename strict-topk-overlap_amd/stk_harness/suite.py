@@ -54,6 +54,7 @@ class Case:
     primary: str = ""                # the path reported as the speculative step
     check: list = field(default_factory=list)   # (label, kind, data) for the CPU leg
     notes: str = ""
+    pairs: dict = field(default_factory=dict)   # label -> (speculative, serial) also reported
 
     def measure(self, replays=20, rounds=3, seed=20261103):
         med, _ = timing.paired(self.graphs, replays=replays, rounds=rounds, seed=seed,
@@ -64,6 +65,8 @@ class Case:
             "strategy": self.strategy, "primary": self.primary,
             "us_per_step": {k: round(v, 3) for k, v in per.items()},
             "speedup_vs_serial": round(per["serial"] / full, 4),
+            **({"speedups": {k: round(per[b] / per[a], 4) for k, (a, b) in self.pairs.items()}}
+               if self.pairs else {}),
             "algorithmic_bytes": self.bytes_full, "kv_bytes": self.bytes_kv,
             "serial_bytes": self.bytes_serial,
             "frac": round(self.bytes_full / (full * 1e-6) / HBM_PEAK, 4),
@@ -228,10 +231,31 @@ def case_c5(dev, seed=20261103):
         return [gqa.exact(q, k, v, gqa.select_blocks(q, lo, hi, cf["topk"]))
                 for q, k, v, lo, hi, _, _ in reqs]
 
+    # the same independent requests of one batched step spread over four
+    # streams (one fork and one join per step; four hardware queues per
+    # process): one request's latency-bound kernels overlap the next one's
+    # bandwidth-bound ones, for both paths alike
+    rs = [torch.cuda.Stream() for _ in range(4)]
+
+    def fused_step_conc(eps):
+        def run(i):
+            return timing.across_streams(
+                [lambda r=r: step_mod.speculative_signed_step(
+                    r[0], r[1], r[2], r[3], r[4], r[6], cf["topk"], "hybrid", 0.2,
+                    max_extra_mass=eps).result.output for r in reqs], rs)
+        return run
+
+    def serial_conc(i):
+        return timing.across_streams(
+            [lambda r=r: gqa.exact(r[0], r[1], r[2], gqa.select_blocks(r[0], r[3], r[4],
+                                                                       cf["topk"]))
+             for r in reqs], rs)
+
     graphs, outs = {}, {}
     for name, fn in (("step_eps0.01", fused_step(0.01)), ("step_strict", fused_step(0.0)),
                      ("signed_eps0.01", full(0.01)), ("signed_strict", full(0.0)),
-                     ("serial", serial)):
+                     ("serial", serial), ("step_eps0.01_4streams", fused_step_conc(0.01)),
+                     ("serial_4streams", serial_conc)):
         graphs[name], outs[name] = timing.capture(lambda fn=fn: fn(0))
     g = cf["hq"] // cf["hkv"]
     tile = 2 * cf["block"] * cf["dim"] * 2
@@ -252,7 +276,10 @@ def case_c5(dev, seed=20261103):
                 "fused two-launch step (step_*) and the two-stream composition (signed_*)",
                 graphs, 1, full_b, kv_b, ser_b, primary="step_eps0.01",
                 notes=f"16 requests, contexts {int(blocks.min()) * 32}-{int(blocks.max()) * 32} "
-                      "tokens; one graph replay = one batched decode step")
+                      "tokens; one graph replay = one batched decode step; *_4streams: the "
+                      "requests spread over four streams",
+                pairs={"sequential": ("step_eps0.01", "serial"),
+                       "four_streams": ("step_eps0.01_4streams", "serial_4streams")})
     for r, (q, k, v, lo, hi, sel, p) in enumerate(reqs):
         hq_, hlo, hhi = _host(q, lo, hi)
         case.check.append((f"ids[{r}]", "select", (hq_, hlo, hhi, cf["topk"], sel.cpu())))
@@ -272,6 +299,11 @@ def case_c5(dev, seed=20261103):
                            (hq_, ks, vs, sel_r, outs["step_strict"][r].cpu())))
         case.check.append((f"step_eps0.01[{r}]", "signed_fused",
                            (hq_, ks, vs, sel_r, p_r, 0.01, outs["step_eps0.01"][r].cpu())))
+        case.check.append((f"step_eps0.01_4streams[{r}]", "signed_fused",
+                           (hq_, ks, vs, sel_r, p_r, 0.01,
+                            outs["step_eps0.01_4streams"][r].cpu())))
+        case.check.append((f"serial_4streams[{r}]", "attention",
+                           (hq_, ks, vs, sel_r, outs["serial_4streams"][r].cpu())))
     return case
 
 

@@ -48,6 +48,24 @@ def overlap_run(selector, speculative, finish, select_stream, predict_stream):
     return finish(a, state)
 
 
+def across_streams(fns, streams):
+    """Run independent requests fns[i]() on streams[i % len(streams)] (one
+    fork from the current stream, one join at the end), so that one
+    request's latency-bound kernels can overlap the next one's bandwidth-
+    bound kernels; returns the outputs in order."""
+    main = torch.cuda.current_stream()
+    for s in streams:
+        s.wait_stream(main)
+    outs = []
+    for i, fn in enumerate(fns):
+        with torch.cuda.stream(streams[i % len(streams)]):
+            outs.append(fn())
+    for s in streams:
+        main.wait_stream(s)
+    _record(outs, main)
+    return outs
+
+
 def capture(fn, warmup=3):
     """Warm fn on a side stream, then capture one call into a HIP graph."""
     main = torch.cuda.current_stream()
