@@ -5,7 +5,8 @@
 //   _match_ids :10-19       -> k_match_ids (LDS position map instead of a
 //                              16 x SP equality tile)
 //   _packed_partials :22-52 -> k_states with the slot-skip mode
-//   _groups :64-96          -> k_groups (level-1 merge of 32 positions)
+//   _groups :64-96          -> k_groups_w / k_groups (level-1 merge of 32
+//                              positions)
 //   _reduce :99-108         -> k_groups + k_merge
 #include "common.hpp"
 #include "api.hpp"
@@ -122,6 +123,70 @@ __global__ __launch_bounds__(256) void k_groups(GroupsArgs a) {
   }
 }
 
+// The same level-1 merge with one wave per (head, group of 32 positions)
+// and two dependent memory round trips: (1) the group's slots (repair) and
+// (2) every (m, l) and every u row of the group, all issued before any
+// arithmetic.  A u row of D floats spans LPR = D / 4 lanes (16-byte loads)
+// and one load instruction covers RPI = 64 / LPR rows; each row's source
+// pointer and weight come from the lane that owns the position.
+template <int LPR>
+__global__ __launch_bounds__(256) void k_groups_w(GroupsArgs a) {
+  constexpr int RPI = STK_WAVE / LPR;
+  constexpr int NI = kTileP / RPI;
+  static_assert(LPR >= 2 && LPR <= STK_WAVE && kTileP % RPI == 0, "row layout");
+  const int waves = blockDim.x / STK_WAVE;
+  const int item = blockIdx.x * waves + wave_id();
+  if (item >= a.h * a.groups) return;
+  const int h = item / a.groups, g = item % a.groups;
+  const int lane = lane_id();
+  const int pos = g * kTileP + (lane & (kTileP - 1));
+  const bool in = lane < kTileP && pos < a.s;
+  const int sl = a.slot ? (int)ld_or(a.slot, (int64_t)(a.shared ? 0 : h) * a.s + pos, in, -1)
+                        : -1;
+  const bool hit = in && sl >= 0;
+  const size_t own = (size_t)h * a.s + (in ? pos : 0);
+  const size_t pred = (size_t)h * a.sp + (hit ? sl : 0);
+  // one address per lane, valid either way (no prediction arrays without a
+  // slot table)
+  float m = *(hit ? a.pm + pred : a.m + own);
+  float l = *(hit ? a.pl + pred : a.l + own);
+  if (!in) {
+    m = -INFINITY;
+    l = 0.f;
+  }
+  const float* row = hit ? a.pu + pred * a.d : a.u + own * a.d;
+  const uint64_t rp = reinterpret_cast<uint64_t>(row);
+  float4 uv[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int r = RPI * i + lane / LPR;
+    const uint64_t p = ((uint64_t)(uint32_t)__shfl((int)(rp >> 32), r) << 32) |
+                       (uint32_t)__shfl((int)(uint32_t)rp, r);
+    uv[i] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) +
+                                              4 * (lane % LPR));
+  }
+  const float mx = wave_max_u(m);
+  const float w = wexp(m, mx);
+  const float z = wave_sum_u(w * l);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const float wr = __shfl(w, RPI * i + lane / LPR);
+    acc.x += wr * uv[i].x; acc.y += wr * uv[i].y; acc.z += wr * uv[i].z; acc.w += wr * uv[i].w;
+  }
+#pragma unroll
+  for (int off = LPR; off < STK_WAVE; off <<= 1) {
+    acc.x += __shfl_xor(acc.x, off); acc.y += __shfl_xor(acc.y, off);
+    acc.z += __shfl_xor(acc.z, off); acc.w += __shfl_xor(acc.w, off);
+  }
+  const size_t orow = (size_t)h * a.groups + g;
+  if (lane < LPR) *reinterpret_cast<float4*>(a.ou + orow * a.d + 4 * lane) = acc;
+  if (lane == 0) {
+    a.om[orow] = mx;
+    a.ol[orow] = z;
+  }
+}
+
 }  // namespace stk
 
 using namespace stk;
@@ -139,7 +204,15 @@ static int launch_reduce(const float* m, const float* l, const float* u, const f
   float* ol = w.take<float>((size_t)hq * groups);
   float* ou = w.take<float>((size_t)hq * groups * d);
   GroupsArgs g{m, l, u, pm, pl, pu, slot, shared, hq, s, sp, d, groups, om, ol, ou};
-  hipLaunchKernelGGL(k_groups, dim3(hq, groups), dim3(256), 0, st, g);
+  // wave-per-group kernel for D in {64, 128, 256} with 16-byte aligned rows
+  const uintptr_t al = reinterpret_cast<uintptr_t>(u) | reinterpret_cast<uintptr_t>(ou) |
+                       (pu ? reinterpret_cast<uintptr_t>(pu) : 0);
+  const int lpr = (al & 15) == 0 && (d == 64 || d == 128 || d == 256) ? d / 4 : 0;
+  const int wg = (int)(((int64_t)hq * groups + 3) / 4);
+  if (lpr == 16) hipLaunchKernelGGL((k_groups_w<16>), dim3(wg), dim3(256), 0, st, g);
+  else if (lpr == 32) hipLaunchKernelGGL((k_groups_w<32>), dim3(wg), dim3(256), 0, st, g);
+  else if (lpr == 64) hipLaunchKernelGGL((k_groups_w<64>), dim3(wg), dim3(256), 0, st, g);
+  else hipLaunchKernelGGL(k_groups, dim3(hq, groups), dim3(256), 0, st, g);
   int rc = stk_check_launch("k_groups");
   if (rc) return rc;
   return stk_launch_merge(om, ol, ou, nullptr, hq, groups, d, out, st);

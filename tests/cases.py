@@ -179,7 +179,8 @@ def prediction_rows(selected, blocks, predict_k, hits):
 def hier_cases(dtype):
     """tests/check_gqa_hierarchical.py:15-32 shapes (reduced for the oracle)."""
     gen = torch.Generator().manual_seed(317)
-    for h, hkv, n, b, d, sa in [(24, 2, 1024, 4, 256, 512), (6, 2, 96, 5, 96, 37)]:
+    for h, hkv, n, b, d, sa in [(24, 2, 1024, 4, 256, 512), (6, 2, 96, 5, 96, 37),
+                                (48, 4, 2048, 4, 128, 320), (12, 1, 700, 8, 64, 200)]:
         q = torch.randn((h, d), generator=gen).to(dtype)
         k = torch.randn((hkv, n, b, d), generator=gen).to(dtype)
         v = torch.randn(k.shape, generator=gen).to(dtype)
