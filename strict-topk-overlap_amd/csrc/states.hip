@@ -76,6 +76,14 @@ __global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_states_pack(StatesArg
   states_pack_wg<T, NCH, BB, I>(a, a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x);
 }
 
+// Small blocks, HG query heads of a KV group per wave (one pack load when the
+// heads' IDs agree at the pack).
+template <typename T, int NCH, int BB, typename I, int HG>
+__global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_states_pack_grp(StatesArgs a) {
+  states_pack_grp_wg<T, NCH, BB, I, HG>(a, a.remap ? xcd_remap(blockIdx.x, gridDim.x)
+                                                   : blockIdx.x);
+}
+
 // LSE merge arguments (kernels.py:74-91, merge_partials :437-442).
 struct MergeArgs {
   const float* m; const float* l; const float* u; const uint8_t* inc;
@@ -579,6 +587,27 @@ static int launch_states(StatesArgs& a, int dtype, bool with_v, bool slot, hipSt
     const int pgrid = (int)((packs + 3) / 4);
     a.remap = pgrid >= 8 ? 1 : 0;
     const bool i64 = a.itype == IT_I64;
+    // GQA: four (or two) heads of a KV group per wave
+    const int hg = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
+    if (hg > 1) {
+      const int ggrid = (int)((packs / hg + 3) / 4);
+      a.remap = ggrid >= 8 ? 1 : 0;
+#define STK_PACKG(BBV, HGV)                                                                        \
+      STK_DISPATCH_TOK(dtype, pnch, {                                                              \
+        if (i64)                                                                                   \
+          hipLaunchKernelGGL((k_states_pack_grp<T, NCH, BBV, int64_t, HGV>), dim3(ggrid), dim3(256), \
+                             0, st, a);                                                            \
+        else                                                                                       \
+          hipLaunchKernelGGL((k_states_pack_grp<T, NCH, BBV, int32_t, HGV>), dim3(ggrid), dim3(256), \
+                             0, st, a);                                                            \
+      })
+      if (a.b == 4 && hg == 4) STK_PACKG(4, 4);
+      else if (a.b == 4) STK_PACKG(4, 2);
+      else if (hg == 4) STK_PACKG(8, 4);
+      else STK_PACKG(8, 2);
+#undef STK_PACKG
+      return stk_check_launch("k_states_pack_grp");
+    }
 #define STK_PACK(BBV)                                                                              \
     STK_DISPATCH_TOK(dtype, pnch, {                                                                \
       if (i64)                                                                                     \

@@ -160,6 +160,158 @@ __device__ __forceinline__ void states_pack_wg(const StatesArgs& a, int wg) {
   }
 }
 
+// The same packed states for HG query heads of one KV group per wave.  When
+// the HG heads list the same IDs at the pack's positions (a selection shared
+// by the group, as gqa_hierarchical.repair_saved_shared assumes, or any rows
+// that happen to agree there), the pack's 32 K rows and 32 V rows are loaded
+// once and the heads are computed in turn from registers; otherwise each head
+// loads its own rows.  Items are ordered (KV head, pack, head group), so the
+// waves sharing a pack are adjacent and land on one XCD.
+template <typename T, int NCH, int BB, typename I, int HG>
+__device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) {
+  using TT = TokTile<T, NCH, 2>;
+  static_assert(BB == 4 || BB == 8, "packed blocks hold 4 or 8 tokens");
+  constexpr int PB = TT::CH / BB;        // blocks per pack
+  constexpr int D = TT::D;
+  static_assert(HG * PB <= STK_WAVE, "one ID per lane for the group");
+  const int waves = blockDim.x / STK_WAVE;
+  const int packs = (a.s + PB - 1) / PB;
+  const int G = a.hq / a.hkv;
+  const int hgs = G / HG;
+  const int64_t item = (int64_t)wg * waves + wave_id();
+  if (item >= (int64_t)a.hkv * packs * hgs) return;
+  const int hg = (int)(item % hgs);
+  const int64_t rest = item / hgs;
+  const int pack = (int)(rest % packs);
+  const int kv = (int)(rest / packs);
+  const int h0 = kv * G + hg * HG;
+  const int p0 = pack * PB;
+  const I* ids = reinterpret_cast<const I*>(a.ids);
+  TT t;
+  t.init();
+  // ---- round trip 1: the group's IDs at the pack (lane i * PB + j holds
+  // head h0 + i, position p0 + j), the first head's query row
+  const int gi = lane_id() / PB, gj = lane_id() % PB;
+  const bool gin = lane_id() < HG * PB && p0 + gj < a.s;
+  const int64_t gid = ld_or(ids, (int64_t)(h0 + (gi < HG ? gi : 0)) * a.s + p0 + gj, gin, (I)-1);
+  uint32_t qw[TT::QW];
+  t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)h0 * D, qw);
+  const int64_t ref = __shfl(gid, gj);
+  const bool same = __ballot(lane_id() < HG * PB && gid != ref) == 0ull;
+  const T* K = reinterpret_cast<const T*>(a.k);
+  const T* V = reinterpret_cast<const T*>(a.v);
+  uint32_t kw[2][TT::QW], vw[TT::CH][TT::VW];
+  const float scale = 1.0f / sqrtf((float)D);
+  // K/V rows of the pack for head i's IDs (lanes hold the IDs of their rows)
+  auto load_tile = [&](int i) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int tok = t.slot + 16 * u;
+      const int64_t bid = __shfl(gid, i * PB + tok / BB);
+      const bool ok = bid >= 0 && bid < a.n;
+      const T* row = K + ((((size_t)kv * a.n + (ok ? (size_t)bid : 0)) * BB + tok % BB) * D);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const uint4 x = *reinterpret_cast<const uint4*>(row + t.kdim(c));
+        kw[u][4 * c + 0] = x.x; kw[u][4 * c + 1] = x.y; kw[u][4 * c + 2] = x.z;
+        kw[u][4 * c + 3] = x.w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+      const int64_t bj = __builtin_amdgcn_readlane((int)gid, i * PB + j);   // IDs fit in 32 bits
+      const bool ok = bj >= 0 && bj < a.n;
+      const T* vb = V + (((size_t)kv * a.n + (ok ? (size_t)bj : 0)) * BB) * D + lane_id() * TT::DPL;
+#pragma unroll
+      for (int r = 0; r < BB; ++r) {
+        const T* row = vb + (size_t)r * D;
+        const int x = j * BB + r;
+        if constexpr (TT::DPL * sizeof(T) == 2) {
+          vw[x][0] = *reinterpret_cast<const uint16_t*>(row);
+        } else if constexpr (TT::DPL * sizeof(T) == 4) {
+          vw[x][0] = *reinterpret_cast<const uint32_t*>(row);
+        } else if constexpr (TT::DPL * sizeof(T) == 8) {
+          const uint2 y = *reinterpret_cast<const uint2*>(row);
+          vw[x][0] = y.x; vw[x][1] = y.y;
+        } else {
+          const uint4 y = *reinterpret_cast<const uint4*>(row);
+          vw[x][0] = y.x; vw[x][1] = y.y; vw[x][2] = y.z; vw[x][3] = y.w;
+        }
+      }
+    }
+  };
+  if (same) load_tile(0);
+  for (int i = 0; i < HG; ++i) {
+    const int h = h0 + i;
+    if (!same) load_tile(i);
+    // all of this head's loads are in flight before its arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+    // per-position flags (lane j < PB): write the state, and compute it
+    const int jl = lane_id() < PB ? lane_id() : 0;
+    const int64_t lid = __shfl(gid, i * PB + jl);
+    bool write = lane_id() < PB && p0 + jl < a.s;
+    if (write && a.slot_in)
+      write = a.slot_in[(int64_t)(a.slot_shared ? 0 : h) * a.s + p0 + jl] < 0;
+    bool live = write && lid >= 0 && lid < a.n;
+    if (a.active_kind == 1) live = live && a.active[h] != 0;
+    else if (a.active_kind == 2) live = live && a.active[(int64_t)h * a.s + p0 + jl] != 0;
+    const uint64_t wmask = __ballot(write);
+    const uint64_t lmask = __ballot(live);
+    float s[2];
+    t.scores(qw, kw, 0, TT::CH, scale, s);
+    // the next head's query row, loaded while this head finishes
+    if (i + 1 < HG) t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)(h + 1) * D, qw);
+    if (wmask == 0ull) continue;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = (t.slot + 16 * u) / BB;
+      if (!((lmask >> j) & 1ull)) s[u] = -INFINITY;
+    }
+    float mb[2], w[2], lb[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float x = s[u];
+      x = fmaxf(x, dpp<0x141>(x, x));
+      x = fmaxf(x, dpp<0x140>(x, x));
+      if constexpr (BB == 8) x = fmaxf(x, __shfl_xor(x, 16));
+      mb[u] = x;
+      w[u] = wexp(s[u], x);
+      float y = t.part == 0 ? w[u] : 0.f;
+      y += dpp<0xB1>(0.f, y);
+      y += dpp<0x4E>(0.f, y);
+      y += dpp<0x141>(0.f, y);
+      y += dpp<0x140>(0.f, y);
+      if constexpr (BB == 8) y += __shfl_xor(y, 16);
+      lb[u] = y;
+    }
+    float acc[PB][TT::DPL];
+#pragma unroll
+    for (int j = 0; j < PB; ++j)
+#pragma unroll
+      for (int e = 0; e < TT::DPL; ++e) acc[j][e] = 0.f;
+#pragma unroll
+    for (int x = 0; x < TT::CH; ++x) {
+      const int u = x / 16, src = (x % 16) * 4;
+      const float wt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w[u]), src));
+      float v[TT::DPL];
+      t.vals(vw, x, v);
+#pragma unroll
+      for (int e = 0; e < TT::DPL; ++e) acc[x / BB][e] += wt * v[e];
+    }
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+      if (!((wmask >> j) & 1ull)) continue;
+      const int u = (j * BB) / 16, src = ((j * BB) % 16) * 4;
+      const int64_t row = (int64_t)h * a.s + p0 + j;
+      if (lane_id() == 0) {
+        a.m[row] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mb[u]), src));
+        a.l[row] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lb[u]), src));
+      }
+      t.store(a.u + row * D, acc[j]);
+    }
+  }
+}
+
 // Packed token tile shape for (dtype, D, B): NCH, or 0 when unsupported.
 inline int pack_nch(int dtype, int d, int b, uintptr_t align_bits) {
   if (b != 4 && b != 8) return 0;

@@ -377,24 +377,35 @@ def test_gqa_validation_messages():
 
 
 # ------------------------------------------------- packed small-block states
-@pytest.mark.parametrize("b,d,dtype,itype", [
-    (4, 128, torch.bfloat16, torch.int32),
-    (8, 64, torch.float16, torch.int64),
-    (4, 256, torch.bfloat16, torch.int64),
-    (8, 128, torch.bfloat16, torch.int32),
+@pytest.mark.parametrize("b,d,dtype,itype,hq,shared", [
+    (4, 128, torch.bfloat16, torch.int32, 6, False),
+    (8, 64, torch.float16, torch.int64, 6, False),
+    (4, 256, torch.bfloat16, torch.int64, 6, False),
+    (8, 128, torch.bfloat16, torch.int32, 6, False),
+    (4, 128, torch.bfloat16, torch.int32, 24, True),    # G = 12: four heads per wave
+    (8, 64, torch.float16, torch.int64, 8, False),      # G = 4, rows differ
+    (4, 128, torch.float16, torch.int32, 12, True),     # G = 6: two heads per wave
 ])
-def test_packed_small_block_states(b, d, dtype, itype):
+def test_packed_small_block_states(b, d, dtype, itype, hq, shared):
     """Blocks of 4 or 8 tokens run 32-token packs per wave: per-block states
     against the oracle, with a ragged row, invalid IDs, both active-mask
-    kinds, and the hierarchical exact / saved repair (skip mode) on top."""
+    kinds, and the hierarchical exact / saved repair (skip mode) on top.
+    With G a multiple of 2, a wave serves several heads of a KV group: rows
+    shared by the group (one pack load), with single entries changed so that
+    some packs differ between heads, and rows that differ everywhere."""
     from strict_topk import gqa_hierarchical as hier
     from strict_topk.kernels import block_partials
-    gen = torch.Generator().manual_seed(11 + b + d)
-    hq, hkv, n, s = 6, 2, 300, 37   # 37 positions: the last pack is partial
+    gen = torch.Generator().manual_seed(11 + b + d + hq)
+    hkv, n, s = 2, 300, 37   # 37 positions: the last pack is partial
+    g = hq // hkv
     q = torch.randn((hq, d), generator=gen).to(dtype)
     k = torch.randn((hkv, n, b, d), generator=gen).to(dtype)
     v = torch.randn(k.shape, generator=gen).to(dtype)
-    valid = torch.stack([torch.randperm(n, generator=gen)[:s] for _ in range(hq)]).to(itype)
+    if shared:
+        base = [torch.randperm(n, generator=gen)[:s] for _ in range(hkv)]
+        valid = torch.stack([base[h // g] for h in range(hq)]).to(itype)
+    else:
+        valid = torch.stack([torch.randperm(n, generator=gen)[:s] for _ in range(hq)]).to(itype)
     ids = valid.clone()
     ids[1, 5] = -1
     ids[2, 36] = -1
@@ -420,7 +431,7 @@ def test_packed_small_block_states(b, d, dtype, itype):
     mask[:, ::3] = True
     same(block_partials(qd, kd, vd, idd, mask.to(DEV)),
          O.block_states(qn, kn, vn, C.ids_np(ids), mask.numpy()), "slot mask")
-    head = torch.tensor([True, False, True, True, False, True])
+    head = torch.tensor([h % 3 != 1 for h in range(hq)])
     same(block_partials(qd, kd, vd, idd, head.to(DEV)),
          O.block_states(qn, kn, vn, C.ids_np(ids), head.numpy()), "head mask")
     an = C.ids_np(valid)
