@@ -258,6 +258,37 @@ def main():
                 "traffic_over_algorithmic": tr["traffic_over_algorithmic"] if tr else None,
                 "bytes_per_launch": fb, "us_per_launch": round(front_us, 3)}
 
+    # ---- block metadata (lo/hi from K at prefill, and one decode append) on
+    # c3's K, rotating over the input copies; checked against torch.amin /
+    # amax of the same K
+    from strict_topk import bounds
+    bstate = [0]
+
+    def build():
+        i = bstate[0] % M
+        bstate[0] += 1
+        return bounds.block_bounds(step.sets[i][1])
+
+    g_b, lohi = timing.capture(lambda: [build() for _ in range(M)])
+    timing.warm([g_b], ms=50.0)
+    b_us = min(timing.interval_us(g_b, 5) for _ in range(3)) / M
+    kk = step.sets[M - 1][1]
+    b_exact = bool(torch.equal(lohi[-1][0], kk.amin(dim=2).float()) and
+                   torch.equal(lohi[-1][1], kk.amax(dim=2).float()))
+    knew = kk[:, 0, 0].contiguous()
+    blo, bhi = lohi[-1][0].clone(), lohi[-1][1].clone()
+    g_a, _ = timing.capture(lambda: [bounds.append(blo, bhi, knew, cfg.blocks - 1, 5)
+                                     for _ in range(M)])
+    timing.warm([g_a], ms=20.0)
+    a_us = min(timing.interval_us(g_a, 20) for _ in range(3)) / M
+    b_bytes = kk.numel() * kk.element_size() + 2 * lohi[-1][0].numel() * 4
+    metadata = {"kernel": "k_bounds (lo/hi from K)", "bytes_per_launch": b_bytes,
+                "us_per_launch": round(b_us, 3),
+                "achieved_GBps": round(b_bytes / (b_us * 1e-6) / 1e9, 1),
+                "frac": round(b_bytes / (b_us * 1e-6) / decode.HBM_PEAK, 4),
+                "bit_exact_vs_torch": b_exact, "append_us": round(a_us, 3)}
+    del g_b, g_a, lohi
+
     by = step.bytes()
     full_us = ms_per_step * 1e3
     path = {"algorithmic_bytes": by.full, "kv_bytes": by.kv_full,
@@ -305,6 +336,7 @@ def main():
         "paired_us_per_step": per_step,
         "roofline": roofline,
         "path_roofline": path,
+        "metadata": metadata,
         "configs": configs,
         "parity": parity,
         "wall_ms_timed_region": round(wall_ms, 2),

@@ -196,6 +196,23 @@ int stk_hier_repair(const void* q, const void* k, const void* v, int dtype, int 
                     const float* pl, const float* pu, int shared, float* out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------ block bounds */
+
+/* Block metadata of the bound scorer: lo/hi[Hkv, N, D] FP32 = per-block,
+ * per-dim minimum / maximum of k[Hkv, N, B, D] over the B tokens, as the
+ * reference harness builds them with k.amin(dim=2).float() / k.amax(dim=2)
+ * (benchmarks/critical_path.py:186, benchmarks/run_benchmark.py:43).  NaN
+ * keys give NaN bounds, as torch does.  k: fp32 / fp16 / bf16. */
+int stk_block_bounds(const void* k, int dtype, int hkv, int n, int b, int d, float* lo,
+                     float* hi, void* stream);
+
+/* Decode append: the token k_new[Hkv, D] lands at position `pos` of block
+ * `block`; pos 0 starts the block's bounds over, otherwise they widen.  The
+ * reference has no counterpart (its harness rebuilds lo/hi outside timing);
+ * this is the per-token update a decode loop needs. */
+int stk_bounds_append(const void* k_new, int dtype, int hkv, int n, int d, int block, int pos,
+                      float* lo, float* hi, void* stream);
+
 /* ------------------------------------------------------- fused decode step */
 
 size_t stk_step_workspace_bytes(int hq, int hkv, int n, int d, int topk);

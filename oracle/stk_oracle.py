@@ -107,6 +107,17 @@ def _sub(a, b):
 
 
 # ---------------------------------------------------------------------------
+# block metadata (the reference harness builds it outside the step)
+# ---------------------------------------------------------------------------
+def block_bounds(k):
+    """lo, hi[Hkv, N, D] = per-block minimum / maximum of k[Hkv, N, B, D] over
+    the B tokens (reference harness: k.amin(dim=2).float() / k.amax(dim=2),
+    benchmarks/critical_path.py:186).  NaN propagates, as in torch."""
+    k = np.asarray(k, dtype=np.float64)
+    return k.min(axis=2), k.max(axis=2)
+
+
+# ---------------------------------------------------------------------------
 # A1/A2: min/max query-sign bound score
 # reference strict_topk/selector.py:8-20 (_score) and strict_topk/gqa.py:15-26
 # (_bound_score): score[h,n] = sum_d q_d * (q_d >= 0 ? hi : lo)[h // G, n, d]

@@ -109,6 +109,37 @@ def test_select_nonfinite_bounds():
     assert ids.cpu().numpy().tolist() == ref.tolist()
 
 
+@pytest.mark.parametrize("dtype,b,d", [(torch.bfloat16, 32, 128), (torch.float16, 4, 64),
+                                     (torch.bfloat16, 16, 256), (torch.float32, 8, 48),
+                                     (torch.float16, 5, 13)])
+def test_block_bounds_and_append(dtype, b, d):
+    """Block metadata bit-exact against the oracle (min / max are exact), NaN
+    keys included; appending a block's tokens one by one gives the same
+    bounds as building them from the block."""
+    from strict_topk import bounds
+    gen = torch.Generator().manual_seed(b * d)
+    hkv, n = 3, 41
+    k = (torch.randn((hkv, n, b, d), generator=gen) * 3).to(dtype)
+    k[2, 7, b - 1, d // 2] = float("nan")
+    lo_ref, hi_ref = O.block_bounds(C.f64(k))
+    lo, hi = bounds.block_bounds(k.to(DEV))
+    assert np.array_equal(lo.cpu().numpy(), lo_ref.astype(np.float32), equal_nan=True)
+    assert np.array_equal(hi.cpu().numpy(), hi_ref.astype(np.float32), equal_nan=True)
+    # decode appends into a copy, block by block (positions 0 .. b-1)
+    lo2 = torch.full_like(lo, 123.0)
+    hi2 = torch.full_like(hi, -123.0)
+    kd = k.to(DEV)
+    for blk in (0, 7, n - 1):
+        for t in range(b):
+            bounds.append(lo2, hi2, kd[:, blk, t].contiguous(), blk, t)
+        assert torch.equal(lo2[:, blk].isnan(), lo[:, blk].isnan())
+        fin = ~lo[:, blk].isnan()
+        assert torch.equal(lo2[:, blk][fin], lo[:, blk][fin])
+        assert torch.equal(hi2[:, blk][fin], hi[:, blk][fin])
+    with pytest.raises(ValueError):
+        bounds.append(lo2, hi2, kd[:, 0, 0].contiguous(), n, 0)
+
+
 def test_select_rejects_bad_k():
     from strict_topk import gqa
     q = torch.randn((4, 8), device=DEV)

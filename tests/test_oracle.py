@@ -263,3 +263,22 @@ def test_planted_low_frame_mistake_is_caught(monkeypatch):
         st = O.speculate(q, k, v, p, mode="hybrid", mass_threshold=.05)
         res = O.repair_fused(q, k, v, a, p, st)
         assert not np.allclose(res.output, O.attention(q, k, v, a), rtol=1e-6)
+
+
+def test_block_bounds_pinned_against_torch():
+    """Block metadata: the oracle equals torch.amin / amax over the token axis
+    (the reference harness's own expression, benchmarks/critical_path.py:186)
+    on finite keys and propagates NaN like it; every token lies inside
+    [lo, hi] and both bounds are attained."""
+    gen = torch.Generator().manual_seed(5)
+    k = torch.randn((3, 17, 6, 10), generator=gen).to(torch.bfloat16)
+    k[1, 4, 2, 7] = float("nan")
+    lo, hi = O.block_bounds(k.float().numpy())
+    tl, th = k.amin(dim=2).float().numpy(), k.amax(dim=2).float().numpy()
+    assert np.array_equal(lo, tl, equal_nan=True) and np.array_equal(hi, th, equal_nan=True)
+    assert np.isnan(lo[1, 4, 7]) and np.isnan(hi[1, 4, 7])
+    kf = k.float().numpy()
+    ok = ~np.isnan(lo)
+    assert ((kf >= lo[:, :, None]) | ~ok[:, :, None]).all()
+    assert ((kf <= hi[:, :, None]) | ~ok[:, :, None]).all()
+    assert ((kf == lo[:, :, None]).any(2) | ~ok).all()
