@@ -196,6 +196,25 @@ int stk_hier_repair(const void* q, const void* k, const void* v, int dtype, int 
                     const float* pl, const float* pu, int shared, float* out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------- shared-selection indexer */
+
+size_t stk_indexer_workspace_bytes(int n);
+
+/* The QSA indexer formula of benchmarks/selector_window.py:126-142
+ * (_indexer_scores / qsa_reference_scores): scores[n] = sum_h relu(iq_h .
+ * ik_n) / sqrt(D) over iq[H,D], ik[N,D] (fp32 / fp16 / bf16), H * D <= 4096,
+ * evaluated in FP64 in a fixed order, stored as float32. */
+int stk_indexer_scores(const void* iq, const void* ik, int dtype, int h, int n, int d,
+                       float* scores, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The shared selector of benchmarks/selector_window.py:76-84 (indexer scores,
+ * scores.topk(topk, sorted=False), the row expanded to every query head):
+ * ids[rows, topk] int32, every row the same topk highest-scoring keys, ties
+ * toward the lower index, ascending.  `scores` may be NULL. */
+int stk_indexer_select(const void* iq, const void* ik, int dtype, int h, int n, int d, int topk,
+                       int rows, float* scores, int32_t* ids, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------ block bounds */
 
 /* Block metadata of the bound scorer: lo/hi[Hkv, N, D] FP32 = per-block,

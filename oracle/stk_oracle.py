@@ -107,6 +107,40 @@ def _sub(a, b):
 
 
 # ---------------------------------------------------------------------------
+# shared-selection indexer (QSA formula), reference
+# benchmarks/selector_window.py:126-142 and the shared top-K :76-84
+# ---------------------------------------------------------------------------
+def indexer_scores(iq, ik):
+    """score[n] = sum_h relu(iq_h . ik_n) / sqrt(D), in the build's fixed FP64
+    order: four partial sums over consecutive quarters of the dims (ceil(D/4)
+    each, in order), combined as (s0 + s1) + (s2 + s3); relu keeps NaN; heads
+    summed in order from 0.0; times 1 / sqrt(D) (the reference's D**-.5)."""
+    iq = np.asarray(iq, dtype=np.float64)
+    ik = np.asarray(ik, dtype=np.float64)
+    h, d = iq.shape
+    qd = (d + 3) // 4
+    sc = np.zeros(ik.shape[0])
+    for hh in range(h):
+        parts = []
+        for p in range(4):
+            d0, d1 = min(d, p * qd), min(d, p * qd + qd)
+            acc = np.zeros(ik.shape[0])
+            for i in range(d0, d1):
+                acc = acc + ik[:, i] * iq[hh, i]
+            parts.append(acc)
+        tot = (parts[0] + parts[1]) + (parts[2] + parts[3])
+        sc = sc + np.where((tot > 0) | np.isnan(tot), tot, 0.0)
+    return sc * (1.0 / math.sqrt(d))
+
+
+def indexer_select(iq, ik, topk, rows):
+    """The shared selection: top-K of the indexer scores (ties to the lower
+    index, ascending IDs), the same row for every query head."""
+    ids = topk_ids(indexer_scores(iq, ik)[None, :], topk)[0]
+    return np.repeat(ids[None, :], rows, axis=0)
+
+
+# ---------------------------------------------------------------------------
 # block metadata (the reference harness builds it outside the step)
 # ---------------------------------------------------------------------------
 def block_bounds(k):

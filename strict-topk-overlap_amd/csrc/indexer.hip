@@ -1,0 +1,131 @@
+// Shared-selection indexer scorer: the QSA formula
+//   score[n] = sum_h relu(iq_h . ik_n) / sqrt(D)
+// over H indexer heads and N indexer keys (one per block), then one top-K
+// shared by every query head.
+//
+// Reference: benchmarks/selector_window.py:126-142 (_indexer_scores,
+// qsa_reference_scores) and :76-84 (the shared selector:
+// scores.topk(topk, sorted=False), expanded to every query head).
+//
+// Score contract (so that IDs are bit-exact against the FP64 oracle): four
+// lanes per key; lane p sums dims [p*Q, p*Q + Q), Q = ceil(D / 4), in order,
+// in FP64 (16-bit x 16-bit products are exact there); the four partials
+// combine as (s0 + s1) + (s2 + s3); relu (NaN kept, as torch.relu) per head;
+// heads summed in order from 0.0; times inv = 1 / sqrt(D) (FP64, computed
+// on the host: the reference's D**-.5 factor).  The query is
+// staged in LDS as FP64.  The top-K is the selector's (k_topk: ties toward
+// the lower index, IDs ascending).
+#include <cmath>
+
+#include "score.hpp"
+#include "api.hpp"
+
+namespace stk {
+
+constexpr int kIdxMaxQ = 4096;   // H * D staged in LDS (FP64)
+
+struct IndexerArgs {
+  const void* iq; const void* ik;
+  int h, n, d;
+  double inv;          // 1 / sqrt(D)
+  float* scores;       // may be null
+  uint64_t* keys;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_indexer(IndexerArgs a) {
+  __shared__ double s_q[kIdxMaxQ];
+  const T* iq = reinterpret_cast<const T*>(a.iq);
+  for (int x = threadIdx.x; x < a.h * a.d; x += blockDim.x) s_q[x] = (double)cvt(iq[x]);
+  __syncthreads();
+  const int key = blockIdx.x * (blockDim.x / 4) + threadIdx.x / 4;
+  const int p = threadIdx.x % 4;
+  const bool ok = key < a.n;
+  const int qd = (a.d + 3) / 4;
+  const int d0 = p * qd < a.d ? p * qd : a.d;
+  const int d1 = d0 + qd < a.d ? d0 + qd : a.d;
+  const T* row = reinterpret_cast<const T*>(a.ik) + (size_t)(ok ? key : 0) * a.d;
+  double sc = 0.0;
+  for (int hh = 0; hh < a.h; ++hh) {
+    const double* qh = s_q + hh * a.d;
+    double acc = 0.0;
+    for (int i = d0; i < d1; ++i) acc = fma((double)cvt(row[i]), qh[i], acc);
+    // (s0 + s1) + (s2 + s3): IEEE addition is commutative, so both lanes of
+    // a pair hold the same sum
+    const double pair = acc + __shfl_xor(acc, 1);
+    const double tot = pair + __shfl_xor(pair, 2);
+    sc += (tot > 0.0 || tot != tot) ? tot : 0.0;
+  }
+  sc = sc * a.inv;
+  if (ok && p == 0) {
+    if (a.scores) a.scores[key] = (float)sc;
+    a.keys[key] = score_key(sc);
+  }
+}
+
+// ids[r, :] = ids[0, :] for r in [1, rows)
+__global__ __launch_bounds__(256) void k_rows_copy(int32_t* ids, int rows, int k) {
+  const int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (x >= (int64_t)(rows - 1) * k) return;
+  ids[k + x] = ids[x % k];
+}
+
+}  // namespace stk
+
+using namespace stk;
+
+static StkCheck check_indexer(int dtype, int h, int n, int d) {
+  if (dtype != DT_F32 && dtype != DT_F16 && dtype != DT_BF16) return {false, "unsupported dtype"};
+  if (h <= 0 || n <= 0 || d <= 0) return {false, "bad indexer shape"};
+  if (h * d > kIdxMaxQ) return {false, "indexer heads * dim must be <= 4096"};
+  return {true, ""};
+}
+
+static int launch_indexer(const void* iq, const void* ik, int dtype, int h, int n, int d,
+                          float* scores, uint64_t* keys, hipStream_t st) {
+  IndexerArgs a{iq, ik, h, n, d, 1.0 / std::sqrt((double)d), scores, keys};
+  const dim3 grid((n + 63) / 64), block(256);
+  if (dtype == DT_BF16) hipLaunchKernelGGL(k_indexer<bf16s>, grid, block, 0, st, a);
+  else if (dtype == DT_F16) hipLaunchKernelGGL(k_indexer<f16s>, grid, block, 0, st, a);
+  else hipLaunchKernelGGL(k_indexer<float>, grid, block, 0, st, a);
+  return stk_check_launch("k_indexer");
+}
+
+extern "C" {
+
+STK_API size_t stk_indexer_workspace_bytes(int n) {
+  return n > 0 ? stk_align((size_t)n * sizeof(uint64_t)) : 0;
+}
+
+STK_API int stk_indexer_scores(const void* iq, const void* ik, int dtype, int h, int n, int d,
+                               float* scores, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  STK_REQUIRE(check_indexer(dtype, h, n, d));
+  STK_REQUIRE(iq && ik && scores, "null pointer");
+  STK_REQUIRE(workspace && workspace_bytes >= stk_indexer_workspace_bytes(n),
+              "workspace too small");
+  return launch_indexer(iq, ik, dtype, h, n, d, scores, static_cast<uint64_t*>(workspace),
+                        (hipStream_t)stream);
+}
+
+STK_API int stk_indexer_select(const void* iq, const void* ik, int dtype, int h, int n, int d,
+                               int topk, int rows, float* scores, int32_t* ids, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  STK_REQUIRE(check_indexer(dtype, h, n, d));
+  STK_REQUIRE(iq && ik && ids, "null pointer");
+  STK_REQUIRE(topk >= 1 && topk <= n && rows >= 1, "bad topk or rows");
+  STK_REQUIRE(workspace && workspace_bytes >= stk_indexer_workspace_bytes(n),
+              "workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  uint64_t* keys = static_cast<uint64_t*>(workspace);
+  int rc = launch_indexer(iq, ik, dtype, h, n, d, scores, keys, st);
+  if (rc) return rc;
+  rc = stk_launch_topk(keys, 1, n, topk, ids, st);
+  if (rc || rows == 1) return rc;
+  const int64_t rest = (int64_t)(rows - 1) * topk;
+  hipLaunchKernelGGL(k_rows_copy, dim3((unsigned)((rest + 255) / 256)), dim3(256), 0, st, ids,
+                     rows, topk);
+  return stk_check_launch("k_rows_copy");
+}
+
+}  // extern "C"

@@ -61,6 +61,9 @@ _SIGS = {
                                  P, P, P, P, P, P, Z, P]),
     "stk_step_front": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, P, P, P, P, Z, P]),
     "stk_step_tail": (I, [P, P, P, I, I, I, I, I, I, I, P, I, I, I, P, P, P, P, P, P, Z, P]),
+    "stk_indexer_workspace_bytes": (Z, [I]),
+    "stk_indexer_scores": (I, [P, P, I, I, I, I, P, P, Z, P]),
+    "stk_indexer_select": (I, [P, P, I, I, I, I, I, I, P, P, P, Z, P]),
     "stk_block_bounds": (I, [P, I, I, I, I, I, P, P, P]),
     "stk_bounds_append": (I, [P, I, I, I, I, I, I, P, P, P]),
     "stk_signed_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I, F, F, F, F,

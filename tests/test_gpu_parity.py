@@ -140,6 +140,31 @@ def test_block_bounds_and_append(dtype, b, d):
         bounds.append(lo2, hi2, kd[:, 0, 0].contiguous(), n, 0)
 
 
+@pytest.mark.parametrize("dtype,h,n,d,topk", [(torch.float16, 4, 8192, 128, 2048),
+                                            (torch.bfloat16, 4, 3000, 128, 64),
+                                            (torch.float32, 3, 50, 13, 7),
+                                            (torch.float16, 16, 700, 256, 700)])
+def test_indexer_scores_and_shared_select(dtype, h, n, d, topk):
+    """QSA indexer (benchmarks/selector_window.py:126-142): FP32 scores
+    bit-exact to float32(oracle FP64 score), shared IDs bit-exact in every
+    row; integer-valued keys make many exact ties (lower index wins); a NaN
+    key ranks last."""
+    from strict_topk import indexer
+    gen = torch.Generator().manual_seed(n + d)
+    iq = torch.randn((h, d), generator=gen).to(dtype)
+    ik = torch.randn((n, d), generator=gen).to(dtype)
+    t = min(40, n // 6)
+    ik[n // 3: n // 3 + t] = torch.randint(-1, 2, (t, d), generator=gen).to(dtype)
+    ik[n // 2: n // 2 + t] = ik[n // 3: n // 3 + t]
+    ik[5, 1] = float("nan")
+    ref = O.indexer_scores(C.f64(iq), C.f64(ik))
+    got = indexer.scores(iq.to(DEV), ik.to(DEV))
+    assert np.array_equal(got.cpu().numpy(), ref.astype(np.float32), equal_nan=True)
+    ids = indexer.select_shared(iq.to(DEV), ik.to(DEV), topk, 6)
+    assert ids.shape == (6, topk) and ids.dtype == torch.int32
+    assert ids.cpu().numpy().tolist() == O.indexer_select(C.f64(iq), C.f64(ik), topk, 6).tolist()
+
+
 def test_select_rejects_bad_k():
     from strict_topk import gqa
     q = torch.randn((4, 8), device=DEV)

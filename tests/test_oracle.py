@@ -282,3 +282,28 @@ def test_block_bounds_pinned_against_torch():
     assert ((kf >= lo[:, :, None]) | ~ok[:, :, None]).all()
     assert ((kf <= hi[:, :, None]) | ~ok[:, :, None]).all()
     assert ((kf == lo[:, :, None]).any(2) | ~ok).all()
+
+
+def test_indexer_scores_pinned_against_reference_formula():
+    """QSA indexer: the oracle's fixed-order FP64 scores equal the reference's
+    own formula relu(iq @ ik.T).sum(0) / sqrt(D) (benchmarks/selector_window.py:
+    78-84, its FP64 check) to FP64 rounding, keep NaN like torch.relu, and the
+    shared selection is the brute-force top-K of those scores in every row."""
+    gen = torch.Generator().manual_seed(21)
+    iq = torch.randn((4, 128), generator=gen).half()
+    ik = torch.randn((300, 128), generator=gen).half()
+    ref = (torch.relu(iq.double() @ ik.double().T).sum(0) / 128 ** .5).numpy()
+    got = O.indexer_scores(iq.numpy(), ik.numpy())
+    np.testing.assert_allclose(got, ref, rtol=1e-13, atol=1e-13)
+    # an odd width: quarters of ceil(D / 4) dims
+    iq2 = torch.randn((3, 13), generator=gen).double()
+    ik2 = torch.randn((50, 13), generator=gen).double()
+    np.testing.assert_allclose(O.indexer_scores(iq2.numpy(), ik2.numpy()),
+                               (torch.relu(iq2 @ ik2.T).sum(0) / 13 ** .5).numpy(),
+                               rtol=1e-13, atol=1e-13)
+    ik3 = ik.clone().float()
+    ik3[7, 3] = float("nan")
+    assert np.isnan(O.indexer_scores(iq.float().numpy(), ik3.numpy())[7])
+    ids = O.indexer_select(iq.numpy(), ik.numpy(), 20, 5)
+    order = sorted(range(300), key=lambda j: (-got[j], j))[:20]
+    assert ids.shape == (5, 20) and (ids == np.array(sorted(order))[None, :]).all()
