@@ -112,23 +112,27 @@ def _sub(a, b):
 # ---------------------------------------------------------------------------
 def indexer_scores(iq, ik):
     """score[n] = sum_h relu(iq_h . ik_n) / sqrt(D), in the build's fixed FP64
-    order: four partial sums over consecutive quarters of the dims (ceil(D/4)
-    each, in order), combined as (s0 + s1) + (s2 + s3); relu keeps NaN; heads
-    summed in order from 0.0; times 1 / sqrt(D) (the reference's D**-.5)."""
+    order: 16 partial sums over consecutive sixteenths of the dims
+    (ceil(D/16) each, in order), combined as a pairwise tree ((s0 + s1) +
+    (s2 + s3) and so on); relu keeps NaN; heads summed in order from 0.0;
+    times 1 / sqrt(D) (the reference's D**-.5)."""
     iq = np.asarray(iq, dtype=np.float64)
     ik = np.asarray(ik, dtype=np.float64)
     h, d = iq.shape
-    qd = (d + 3) // 4
+    lanes = 16
+    qd = (d + lanes - 1) // lanes
     sc = np.zeros(ik.shape[0])
     for hh in range(h):
         parts = []
-        for p in range(4):
+        for p in range(lanes):
             d0, d1 = min(d, p * qd), min(d, p * qd + qd)
             acc = np.zeros(ik.shape[0])
             for i in range(d0, d1):
                 acc = acc + ik[:, i] * iq[hh, i]
             parts.append(acc)
-        tot = (parts[0] + parts[1]) + (parts[2] + parts[3])
+        while len(parts) > 1:
+            parts = [parts[i] + parts[i + 1] for i in range(0, len(parts), 2)]
+        tot = parts[0]
         sc = sc + np.where((tot > 0) | np.isnan(tot), tot, 0.0)
     return sc * (1.0 / math.sqrt(d))
 

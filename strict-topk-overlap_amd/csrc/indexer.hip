@@ -7,14 +7,20 @@
 // qsa_reference_scores) and :76-84 (the shared selector:
 // scores.topk(topk, sorted=False), expanded to every query head).
 //
-// Score contract (so that IDs are bit-exact against the FP64 oracle): four
-// lanes per key; lane p sums dims [p*Q, p*Q + Q), Q = ceil(D / 4), in order,
-// in FP64 (16-bit x 16-bit products are exact there); the four partials
-// combine as (s0 + s1) + (s2 + s3); relu (NaN kept, as torch.relu) per head;
-// heads summed in order from 0.0; times inv = 1 / sqrt(D) (FP64, computed
-// on the host: the reference's D**-.5 factor).  The query is
-// staged in LDS as FP64.  The top-K is the selector's (k_topk: ties toward
-// the lower index, IDs ascending).
+// Score contract (so that IDs are bit-exact against the FP64 oracle): 16
+// lanes per key; lane p sums dims [p*Q, p*Q + Q), Q = ceil(D / 16), in
+// order, in FP64 (16-bit x 16-bit and FP32 x FP32 products are exact
+// there); the 16 partials combine as a pairwise tree (the xor butterfly
+// 1, 2, 4, 8: (s0 + s1) + (s2 + s3) and so on); relu (NaN kept, as
+// torch.relu) per head; heads summed in order from 0.0; times
+// inv = 1 / sqrt(D) (FP64, computed on the host: the reference's D**-.5
+// factor).  The top-K is the selector's (ties toward the lower index, IDs
+// ascending).
+//
+// k_indexer_v (16-bit keys, D = 128): each lane holds its 8 dims from one
+// 16-byte load and its query slices in registers, so a key is one coalesced
+// 256-byte row per 16 lanes and the four heads are four independent 8-FMA
+// chains.  k_indexer serves every other shape with the same arithmetic.
 #include <cmath>
 
 #include "score.hpp"
@@ -32,16 +38,30 @@ struct IndexerArgs {
   uint64_t* keys;
 };
 
+constexpr int kIdxLanes = 16;    // lanes per key
+
+// Pairwise tree over the 16 lanes of a key (IEEE addition is commutative,
+// so both lanes of every exchange hold the same sum).
+__device__ __forceinline__ double key_tree(double x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
+}
+
+__device__ __forceinline__ double relu_nan(double x) { return (x > 0.0 || x != x) ? x : 0.0; }
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_indexer(IndexerArgs a) {
   __shared__ double s_q[kIdxMaxQ];
   const T* iq = reinterpret_cast<const T*>(a.iq);
   for (int x = threadIdx.x; x < a.h * a.d; x += blockDim.x) s_q[x] = (double)cvt(iq[x]);
   __syncthreads();
-  const int key = blockIdx.x * (blockDim.x / 4) + threadIdx.x / 4;
-  const int p = threadIdx.x % 4;
+  const int key = blockIdx.x * (blockDim.x / kIdxLanes) + threadIdx.x / kIdxLanes;
+  const int p = threadIdx.x % kIdxLanes;
   const bool ok = key < a.n;
-  const int qd = (a.d + 3) / 4;
+  const int qd = (a.d + kIdxLanes - 1) / kIdxLanes;
   const int d0 = p * qd < a.d ? p * qd : a.d;
   const int d1 = d0 + qd < a.d ? d0 + qd : a.d;
   const T* row = reinterpret_cast<const T*>(a.ik) + (size_t)(ok ? key : 0) * a.d;
@@ -50,12 +70,53 @@ __global__ __launch_bounds__(256) void k_indexer(IndexerArgs a) {
     const double* qh = s_q + hh * a.d;
     double acc = 0.0;
     for (int i = d0; i < d1; ++i) acc = fma((double)cvt(row[i]), qh[i], acc);
-    // (s0 + s1) + (s2 + s3): IEEE addition is commutative, so both lanes of
-    // a pair hold the same sum
-    const double pair = acc + __shfl_xor(acc, 1);
-    const double tot = pair + __shfl_xor(pair, 2);
-    sc += (tot > 0.0 || tot != tot) ? tot : 0.0;
+    sc += relu_nan(key_tree(acc));
   }
+  sc = sc * a.inv;
+  if (ok && p == 0) {
+    if (a.scores) a.scores[key] = (float)sc;
+    a.keys[key] = score_key(sc);
+  }
+}
+
+template <typename T, int H>
+__global__ __launch_bounds__(256) void k_indexer_v(IndexerArgs a) {
+  constexpr int D = 128;
+  const int key = blockIdx.x * (blockDim.x / kIdxLanes) + threadIdx.x / kIdxLanes;
+  const int p = threadIdx.x % kIdxLanes;
+  const bool ok = key < a.n;
+  // this lane's 8 dims of the key row (one 16-byte load) and of every query
+  const uint4 kr = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.ik) +
+                                                   (size_t)(ok ? key : 0) * D + 8 * p);
+  const T* iq = reinterpret_cast<const T*>(a.iq);
+  uint4 qr[H];
+#pragma unroll
+  for (int hh = 0; hh < H; ++hh)
+    qr[hh] = *reinterpret_cast<const uint4*>(iq + (size_t)hh * D + 8 * p);
+  double kv[8];
+  {
+    const uint32_t w[4] = {kr.x, kr.y, kr.z, kr.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      kv[2 * e] = (double)cvt(T{uint16_t(w[e] & 0xffffu)});
+      kv[2 * e + 1] = (double)cvt(T{uint16_t(w[e] >> 16)});
+    }
+  }
+  double part[H];
+#pragma unroll
+  for (int hh = 0; hh < H; ++hh) {
+    const uint32_t w[4] = {qr[hh].x, qr[hh].y, qr[hh].z, qr[hh].w};
+    double acc = 0.0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = fma(kv[2 * e], (double)cvt(T{uint16_t(w[e] & 0xffffu)}), acc);
+      acc = fma(kv[2 * e + 1], (double)cvt(T{uint16_t(w[e] >> 16)}), acc);
+    }
+    part[hh] = acc;
+  }
+  double sc = 0.0;
+#pragma unroll
+  for (int hh = 0; hh < H; ++hh) sc += relu_nan(key_tree(part[hh]));
   sc = sc * a.inv;
   if (ok && p == 0) {
     if (a.scores) a.scores[key] = (float)sc;
@@ -84,8 +145,12 @@ static StkCheck check_indexer(int dtype, int h, int n, int d) {
 static int launch_indexer(const void* iq, const void* ik, int dtype, int h, int n, int d,
                           float* scores, uint64_t* keys, hipStream_t st) {
   IndexerArgs a{iq, ik, h, n, d, 1.0 / std::sqrt((double)d), scores, keys};
-  const dim3 grid((n + 63) / 64), block(256);
-  if (dtype == DT_BF16) hipLaunchKernelGGL(k_indexer<bf16s>, grid, block, 0, st, a);
+  const dim3 grid((n + 15) / 16), block(256);
+  const bool vec = dtype != DT_F32 && d == 128 && h == 4 &&
+                   ((reinterpret_cast<uintptr_t>(iq) | reinterpret_cast<uintptr_t>(ik)) & 15) == 0;
+  if (vec && dtype == DT_BF16) hipLaunchKernelGGL((k_indexer_v<bf16s, 4>), grid, block, 0, st, a);
+  else if (vec) hipLaunchKernelGGL((k_indexer_v<f16s, 4>), grid, block, 0, st, a);
+  else if (dtype == DT_BF16) hipLaunchKernelGGL(k_indexer<bf16s>, grid, block, 0, st, a);
   else if (dtype == DT_F16) hipLaunchKernelGGL(k_indexer<f16s>, grid, block, 0, st, a);
   else hipLaunchKernelGGL(k_indexer<float>, grid, block, 0, st, a);
   return stk_check_launch("k_indexer");

@@ -30,6 +30,8 @@
 namespace stk {
 
 constexpr int kTopkThreads = 256;
+constexpr int kTopkWide = 1024;     // threads of k_topk_wide (16 waves)
+constexpr int kWideRows = 4;        // rows up to which k_topk_wide is used
 template <typename Q, int P, int STEPS, bool FULL, int GT>
 __global__ __launch_bounds__(256) void k_score(ScoreArgs a) {
   score_wg<Q, P, STEPS, FULL, GT>(a, blockIdx.x);
@@ -44,6 +46,17 @@ struct TopkArgs {
 // One workgroup per row (TopkArgs.keys[row, 0..n)), see topk.hpp.
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void k_topk(TopkArgs a) {
+  __shared__ TopkLds s;
+  int32_t* out = a.ids + (size_t)blockIdx.x * a.k;
+  topk_select<KPT>(a.keys + (size_t)blockIdx.x * a.n, a.n, a.k, s,
+                   [&](int pos, int idx) { out[pos] = idx; });
+}
+
+// The same selection with 1024 threads (KPT keys each), for shapes with few
+// rows, where one workgroup per row leaves most of the chip idle and a
+// row's passes are the latency.
+template <int KPT>
+__global__ __launch_bounds__(kTopkWide) void k_topk_wide(TopkArgs a) {
   __shared__ TopkLds s;
   int32_t* out = a.ids + (size_t)blockIdx.x * a.k;
   topk_select<KPT>(a.keys + (size_t)blockIdx.x * a.n, a.n, a.k, s,
@@ -205,9 +218,21 @@ int stk_launch_score(const void* q, int q_dtype, const float* lo, const float* h
   return stk_check_launch("k_score");
 }
 
+// 1024-thread rows for a few long rows (the shared selection's single row):
+// measured on MI355X, 32 rows of 2048 keys are faster at 256 threads.
+static bool wide_topk(int rows, int n) { return rows <= kWideRows && n > 1024 && n <= 16384; }
+
 int stk_launch_topk(const uint64_t* keys, int rows, int n, int k, int32_t* ids, hipStream_t st) {
   TopkArgs t{keys, n, k, ids};
   const dim3 grid(rows), block(kTopkThreads);
+  if (wide_topk(rows, n)) {
+    const dim3 wb(kTopkWide);
+    if (n <= 2048) hipLaunchKernelGGL(k_topk_wide<2>, grid, wb, 0, st, t);
+    else if (n <= 4096) hipLaunchKernelGGL(k_topk_wide<4>, grid, wb, 0, st, t);
+    else if (n <= 8192) hipLaunchKernelGGL(k_topk_wide<8>, grid, wb, 0, st, t);
+    else hipLaunchKernelGGL(k_topk_wide<16>, grid, wb, 0, st, t);
+    return stk_check_launch("k_topk_wide");
+  }
   if (n <= 256) hipLaunchKernelGGL(k_topk<1>, grid, block, 0, st, t);
   else if (n <= 512) hipLaunchKernelGGL(k_topk<2>, grid, block, 0, st, t);
   else if (n <= 1024) hipLaunchKernelGGL(k_topk<4>, grid, block, 0, st, t);

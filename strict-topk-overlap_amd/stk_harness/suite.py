@@ -34,7 +34,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from strict_topk import fused, gqa, gqa_hierarchical, kernels, selector, signed_fused
+from strict_topk import fused, gqa, gqa_hierarchical, indexer, kernels, selector, signed_fused
 from strict_topk import step as step_mod
 
 from . import timing
@@ -161,18 +161,36 @@ def case_c4(dev, seed=20261103):
     g = c.group
     q, k, v, lo, hi = make_qkv(c.hq, c.hkv, c.dim, c.block, c.blocks, c.dtype, c.hot, seed,
                                device=dev)
-    sel = _shared_selection(q, lo, hi, g, c.topk)
+    # the shared selection: the QSA indexer formula over 4 synthetic indexer
+    # heads and one 128-dim indexer key per block (no trained weights), as
+    # the reference's QSA probe does (benchmarks/selector_window.py:76-84)
+    gen = torch.Generator(device=dev).manual_seed(seed + 4)
+    iq = torch.randn((4, 128), generator=gen, device=dev).to(c.dtype)
+    ik = torch.randn((c.blocks, 128), generator=gen, device=dev).to(c.dtype)
+
+    def select():
+        return indexer.select_shared(iq, ik, c.topk, c.hq)
+
+    sel = select()
     prow = perturb(sel[:1].cpu(), c.blocks, c.sp, c.overlaps[0], seed)
     p = prow.expand(c.hq, -1).contiguous().to(dev)
     m = 2
+    ss, ps = torch.cuda.Stream(), torch.cuda.Stream()
 
     def full(i):
+        return timing.overlap_run(
+            select, lambda: gqa_hierarchical.partials(q, k, v, p),
+            lambda a, st: gqa_hierarchical.repair_saved_shared(q, k, v, a, p, st), ss, ps)
+
+    def given(i):
         st = gqa_hierarchical.partials(q, k, v, p)
         return gqa_hierarchical.repair_saved_shared(q, k, v, sel, p, st)
 
     graphs, outs = {}, {}
     for name, fn in (("speculative", full),
-                     ("serial", lambda i: gqa_hierarchical.exact(q, k, v, sel))):
+                     ("serial", lambda i: gqa_hierarchical.exact(q, k, v, select())),
+                     ("speculative_given_selection", given),
+                     ("serial_given_selection", lambda i: gqa_hierarchical.exact(q, k, v, sel))):
         graphs[name], outs[name] = timing.capture(_seq(fn, m))
     tile = 2 * c.block * c.dim * 2
     sa, pa = sel.cpu().numpy(), p.cpu().numpy()
@@ -180,13 +198,18 @@ def case_c4(dev, seed=20261103):
     u_miss = sum(len(np.setdiff1d(sa[x * g], pa[x * g])) for x in range(c.hkv))
     states = c.hq * c.sp * (c.dim + 2) * 4
     hits = sum(len(np.intersect1d(a, b)) for a, b in zip(sa, pa))
-    small = c.hq * c.dim * (2 + 4) + 4 * (sa.size + pa.size)
+    small = c.hq * c.dim * (2 + 4) + 4 * (sa.size + pa.size) + ik.numel() * ik.element_size()
     kv = (u_p + u_miss) * tile
-    case = Case("c4", "gqa_hierarchical.partials(P) -> repair_saved_shared (selection given)",
+    case = Case("c4", "indexer.select_shared || gqa_hierarchical.partials(P) -> "
+                "repair_saved_shared (two streams); serial: select, then gqa_hierarchical.exact",
                 graphs, m, kv + states + hits * (c.dim + 2) * 4 + small, kv,
                 unique_pairs(sa, g) * tile + small, primary="speculative",
-                notes="selection shared by all heads, built outside timing (head-summed "
-                      "bound score); lo/hi not read")
+                notes="selection shared by all heads: QSA indexer formula over 4 synthetic "
+                      "indexer heads (no trained weights); *_given_selection: selection built "
+                      "outside timing",
+                pairs={"with_selection": ("speculative", "serial"),
+                       "selection_given": ("speculative_given_selection",
+                                           "serial_given_selection")})
     hq_, hk_, hv_ = _host(q, k, v)
     for name in graphs:
         case.check.append((name, "attention", (hq_, hk_, hv_, sel.cpu(), outs[name][-1].cpu())))
