@@ -78,7 +78,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU leg (CPU baseline and oracle parity)")
     ap.add_argument("--no-suite", action="store_true", help="time c3 only")
-    ap.add_argument("--suite", default="c1,c2,c4,c5",
+    ap.add_argument("--suite", default="c1,c2,c4,c5,c3sweep",
                     help="comma-separated configs timed beside c3")
     return ap.parse_args()
 
@@ -307,7 +307,7 @@ def main():
             log(f"bench: config {name}")
             case = make(dev, args.seed)
             configs[name] = case.measure(seed=args.seed)
-            case.graphs = {}
+            case.release()   # the graphs, then the device inputs they read
             cases.append(case)
             torch.cuda.synchronize()
             torch.cuda.empty_cache()

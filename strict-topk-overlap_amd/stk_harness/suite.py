@@ -1,4 +1,4 @@
-"""Timed decode steps for configs c1, c2, c4 and c5 (c3 is bench.py's headline).
+"""Timed decode steps for configs c1, c2, c4, c5 and a c3 sweep (c3 is bench.py's headline).
 
 Each case builds its seeded inputs on the device, captures its speculative
 path and the same-work serial path into HIP graphs, and times them with
@@ -22,6 +22,8 @@ config exercises (SURVEY's scope table; BASELINE.json ``configs``):
       gqa.select_blocks || kernels.speculate('hybrid', 0.2, keep_mass=True)
       -> signed_fused.repair_signed_fused with max_extra_mass 0.01 and 0
       (strict); serial = gqa.exact(select) per request.
+  c3 sweep  the fused step against the serial path at every c3 hit rate
+      (overlap 1.0, 0.9, 0.75), three seeds each.
 
 No checking happens here: every case keeps host copies of its inputs and the
 device outputs of its captured graphs, which bench.py's CPU leg compares with
@@ -55,6 +57,18 @@ class Case:
     check: list = field(default_factory=list)   # (label, kind, data) for the CPU leg
     notes: str = ""
     pairs: dict = field(default_factory=dict)   # label -> (speculative, serial) also reported
+    baseline: str = "serial"         # the serial path the primary is compared with
+    # Everything on the device that the graphs read but do not own (inputs,
+    # prediction rows, side streams).  A captured graph holds raw addresses,
+    # not tensor references, and every torch.cuda.graph capture starts with
+    # torch.cuda.empty_cache(): an input dropped after its graph was captured
+    # goes back to the driver at the next capture, and replaying the graph
+    # then reads unmapped memory.  Released together with the graphs.
+    keep: object = None
+
+    def release(self):
+        self.graphs = {}
+        self.keep = None
 
     def measure(self, replays=20, rounds=3, seed=20261103):
         med, _ = timing.paired(self.graphs, replays=replays, rounds=rounds, seed=seed,
@@ -64,7 +78,7 @@ class Case:
         return {
             "strategy": self.strategy, "primary": self.primary,
             "us_per_step": {k: round(v, 3) for k, v in per.items()},
-            "speedup_vs_serial": round(per["serial"] / full, 4),
+            "speedup_vs_serial": round(per[self.baseline] / full, 4),
             **({"speedups": {k: round(per[b] / per[a], 4) for k, (a, b) in self.pairs.items()}}
                if self.pairs else {}),
             "algorithmic_bytes": self.bytes_full, "kv_bytes": self.bytes_kv,
@@ -116,6 +130,7 @@ def case_c1(dev, seed=20261103):
                 "streams; and the fused step)", graphs, m,
                 kv + meta + states + small, kv, meta + unique_pairs(sa, 1) * tile + small,
                 primary="step")
+    case.keep = (q, k, v, lo, hi, sel, p, ss, ps)
     hq_, hk_, hv_ = _host(q, k, v)
     case.check = [("ids", "select", (hq_, *_host(lo, hi), c.topk, sel.cpu()))]
     for name in graphs:
@@ -134,6 +149,7 @@ def case_c2(dev, seed=20261103):
     case = Case("c2", "gqa.select_blocks || gqa.partials -> gqa.repair_saved (composed, two "
                 "streams; and the fused step)", graphs, m, by.full, by.kv_full, by.serial,
                 primary="fused", notes=f"inputs rotated over {m} device copies")
+    case.keep = st
     q, k, v, lo, hi = st.host
     case.check = [("ids", "select", (q, lo, hi, st.cfg.topk, st.selected.cpu()))]
     for name in graphs:
@@ -210,6 +226,7 @@ def case_c4(dev, seed=20261103):
                 pairs={"with_selection": ("speculative", "serial"),
                        "selection_given": ("speculative_given_selection",
                                            "serial_given_selection")})
+    case.keep = (q, k, v, lo, hi, iq, ik, sel, p, ss, ps)
     hq_, hk_, hv_ = _host(q, k, v)
     for name in graphs:
         case.check.append((name, "attention", (hq_, hk_, hv_, sel.cpu(), outs[name][-1].cpu())))
@@ -303,6 +320,7 @@ def case_c5(dev, seed=20261103):
                       "requests spread over four streams",
                 pairs={"sequential": ("step_eps0.01", "serial"),
                        "four_streams": ("step_eps0.01_4streams", "serial_4streams")})
+    case.keep = (reqs, ss, ps, rs)
     for r, (q, k, v, lo, hi, sel, p) in enumerate(reqs):
         hq_, hlo, hhi = _host(q, lo, hi)
         case.check.append((f"ids[{r}]", "select", (hq_, hlo, hhi, cf["topk"], sel.cpu())))
@@ -330,4 +348,41 @@ def case_c5(dev, seed=20261103):
     return case
 
 
-CASES = {"c1": case_c1, "c2": case_c2, "c4": case_c4, "c5": case_c5}
+# ------------------------------------------------------------------ c3 sweep
+def case_c3sweep(dev, seed=20261103):
+    """c3 at every prediction hit rate of its definition (100, 90, 75 %), each
+    over three seeds: the fused step against the serial path, cold (12
+    device copies of the inputs per seed)."""
+    c = CONFIGS["c3"]
+    graphs, outs, pairs, checks, steps = {}, {}, {}, [], []
+    m = 12
+    for ov in c.overlaps:
+        for k_ in range(3):
+            st = GqaStep(c, ov, seed + k_, dev, sets=m)
+            steps.append(st)   # its graphs read its device copies until measured
+            tag = f"{ov:g}/s{k_}"
+            for name, fn in (("fused", st.fused), ("serial", st.serial)):
+                graphs[f"{name}@{tag}"], outs[f"{name}@{tag}"] = timing.capture(_seq(fn, m))
+            pairs[tag] = (f"fused@{tag}", f"serial@{tag}")
+            if ov == 0.9 and k_ == 0:
+                by = st.bytes()
+            q, k, v, lo, hi = st.host
+            sel = st.selected.cpu()
+            need = torch.unique(sel.flatten().long())
+            remap = torch.full((c.blocks,), -1, dtype=torch.int64)
+            remap[need] = torch.arange(len(need))
+            sel_r = remap[sel.long()].to(torch.int32)
+            ks, vs = k[:, need], v[:, need]
+            for name in ("fused", "serial"):
+                checks.append((f"{name}@{tag}", "attention",
+                               (q, ks, vs, sel_r, outs[f"{name}@{tag}"][-1].cpu())))
+    case = Case("c3_sweep", "c3 fused step vs serial at overlap 1.0 / 0.9 / 0.75, seeds "
+                f"{seed}..{seed + 2}", graphs, m, by.full, by.kv_full, by.serial,
+                primary="fused@0.9/s0", baseline="serial@0.9/s0", pairs=pairs,
+                notes="byte counts and fractions: the 0.9 / first-seed case")
+    case.keep = steps
+    case.check = checks
+    return case
+
+
+CASES = {"c1": case_c1, "c2": case_c2, "c4": case_c4, "c5": case_c5, "c3sweep": case_c3sweep}
