@@ -293,6 +293,50 @@ int stk_signed_step(const void* q, const void* k, const void* v, int dtype, int 
                     float* extra, int32_t* positive, int32_t* total, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* ---- Paged, ragged KV and batched steps.
+ * Replaces the page-table indirection of strict_topk/flashinfer_backend.py:35-40
+ * (_pages: page = block + kv_head * N over k.view(hkv * n, b, 1, d), one
+ * request per FlashInfer call) with a native wire format shared by a whole
+ * batch of R requests:
+ *   k_pages, v_pages [pages, B, D]   one page = one KV head's block of B tokens
+ *   lo_pages, hi_pages [pages, D]    FP32 per-dim key min / max of the page
+ *                                    (stk_block_bounds on the pool as
+ *                                    hkv = 1, n = pages)
+ *   block_table [R, Hkv, nb] int32   page of logical block j of (request r,
+ *                                    KV head kvh), valid for j < nblocks[r]
+ *   nblocks [R] int32                blocks per request (device memory)
+ *   q [R, Hq, D]; predicted [R, Hq, sp] int32 logical block IDs.
+ * Per request the results are those of stk_speculative_step /
+ * stk_signed_step on the request's blocks gathered from the pool, except
+ * that a request with fewer blocks than topk selects all of them (the rest
+ * of its ID row is -1).  A table entry outside [0, pages) is an invalid
+ * page: its block scores lowest and has the empty state, and nothing is
+ * read from it.  sp may be 0 (predicted, m, l, u may then be null): the step
+ * is then the serial path, the exact attention over the selected blocks.
+ * Outputs are laid out [R, Hq, ...] like q.  Shapes: those of
+ * stk_step_supported with n = nb and topk, sp <= 256. */
+size_t stk_paged_workspace_bytes(int requests, int hq, int nb);
+
+/* stk_speculative_step over a paged batch (union_mode: repair_union). */
+int stk_paged_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
+                   int requests, int hq, int hkv, int nb, int b, int d, int pages,
+                   const float* lo_pages, const float* hi_pages, const int32_t* block_table,
+                   const int32_t* nblocks, int topk, const int32_t* predicted, int sp,
+                   int union_mode, int32_t* selected, float* m, float* l, float* u, float* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* stk_signed_step over a paged batch. */
+int stk_paged_signed_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
+                          int requests, int hq, int hkv, int nb, int b, int d, int pages,
+                          const float* lo_pages, const float* hi_pages,
+                          const int32_t* block_table, const int32_t* nblocks, int topk,
+                          const int32_t* predicted, int sp, int hybrid, float mass_threshold,
+                          float min_remaining, float cancellation_tol, float max_extra_mass,
+                          int32_t* selected, float* m, float* l, float* u, float* out,
+                          uint8_t* fallback, float* remaining, uint8_t* approx, float* extra,
+                          int32_t* positive, int32_t* total, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

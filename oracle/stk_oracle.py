@@ -906,3 +906,36 @@ def touch_kv(k, v, predicted, tile=1024):
             for t in range(nt):
                 out[r, j, t] = flat[t * tile:(t + 1) * tile].sum()
     return out
+
+
+# ---------------------------------------------------------------------------
+# paged, ragged KV: the wire format's definition.  The reference's only page
+# mapping is FlashInfer's (strict_topk/flashinfer_backend.py:35-40: page =
+# block + kv_head * N over k.view(hkv * n, b, 1, d)), the special case of one
+# request with table[kvh, j] = kvh * N + j.
+# ---------------------------------------------------------------------------
+def gather_pages(pages, table, nblocks, r):
+    """Dense [Hkv, n_r, ...] cache of request r from a page pool
+    pages[P, ...] and block table[R, Hkv, NB] (n_r = nblocks[r])."""
+    pages = np.asarray(pages)
+    t = np.asarray(table, dtype=np.int64)[r, :, :int(nblocks[r])]
+    return pages[t]
+
+
+def paged_select(q, lo_pages, hi_pages, table, nblocks, r, k, invalid=None):
+    """The batched step's selection for request r: the top-min(k, n_r) of the
+    request's blocks (IDs ascending), padded with -1 to k columns.  Blocks on
+    an invalid page (``invalid``: a bool mask [Hkv, n_r]) score lowest, below
+    every finite score (their 64-bit key is that of NaN)."""
+    lo = gather_pages(lo_pages, table, nblocks, r)
+    hi = gather_pages(hi_pages, table, nblocks, r)
+    scores = bound_scores(q, lo, hi)
+    if invalid is not None:
+        g = scores.shape[0] // lo.shape[0]
+        scores = np.where(np.repeat(np.asarray(invalid), g, axis=0), np.nan, scores)
+    n = lo.shape[1]
+    kk = min(int(k), n)
+    ids = topk_ids(scores, kk) if kk > 0 else np.zeros((scores.shape[0], 0), np.int64)
+    out = np.full((scores.shape[0], int(k)), -1, dtype=np.int64)
+    out[:, :kk] = ids
+    return out

@@ -21,7 +21,7 @@ CSRC = ROOT / "csrc"
 OUT = ROOT / "strict_topk" / "libstrict_topk_hip.so"
 BUILD = ROOT / "_build"
 ARCH = "gfx950"
-SOURCES = ["api.cpp", "states.hip", "select.hip", "repair.hip", "signed.hip", "hier.hip", "sstep.hip", "bounds.hip", "indexer.hip",
+SOURCES = ["api.cpp", "states.hip", "select.hip", "repair.hip", "signed.hip", "hier.hip", "sstep.hip", "bounds.hip", "indexer.hip", "paged.hip",
            "step.hip"]
 
 FLAGS = [

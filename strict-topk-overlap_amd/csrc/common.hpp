@@ -95,6 +95,34 @@ __device__ __forceinline__ X ld_or(const X* p, int64_t i, bool ok, X other) {
   return ok ? v : other;
 }
 
+// Paged, batched KV.  A batch of requests is flattened into hq = R * Hq query
+// heads and hkv = R * Hkv KV rows (KV row r * Hkv + kvh: KV head kvh of
+// request r).  K/V live in pages [P, B, D] (one page = one KV head's block of
+// B tokens) and the block bounds in lo/hi pages [P, D];
+// table[kv * n + j] is the page of logical block j of KV row kv (n = the
+// table's row width), valid for j < nblk[kv / hkv_req].  A table entry
+// outside [0, pages) is an invalid page: its block has the empty state and
+// scores lowest, and nothing is read from it.
+struct Paging {
+  const int32_t* table;
+  const int32_t* nblk;
+  int hkv_req;
+  int pages;
+};
+
+// Valid blocks of KV row kv, clamped to [0, n].
+__device__ __forceinline__ int pg_blocks(const Paging& pg, int kv, int n) {
+  const int x = pg.nblk[kv / pg.hkv_req];
+  return x < 0 ? 0 : (x > n ? n : x);
+}
+
+// Page of block j of KV row kv when ok, else -1; the table load is always
+// issued (entry 0 when !ok) so that it never sits under a branch.
+__device__ __forceinline__ int pg_page(const Paging& pg, int kv, int n, int64_t j, bool ok) {
+  const int p = ld_or(pg.table, (int64_t)kv * n + j, ok, -1);
+  return (p >= 0 && p < pg.pages) ? p : -1;
+}
+
 template <typename I>
 __device__ __forceinline__ int64_t ld_id(const void* ids, int64_t i) {
   return (int64_t) reinterpret_cast<const I*>(ids)[i];

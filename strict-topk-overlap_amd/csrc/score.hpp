@@ -104,9 +104,12 @@ __device__ __forceinline__ double score_rowsum(double (&v)[C], int l16) {
 // P = 64-dim passes (D <= 64 * P), STEPS = 4-block wave steps per wave,
 // GT = query heads per LDS stage.  FULL: D % 64 == 0 and q, lo, hi 16-byte
 // aligned (whole passes, vector loads); otherwise dims past D are zeroed
-// element by element.
-template <typename Q, int P, int STEPS, bool FULL, int GT>
-__device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg) {
+// element by element.  PG: paged, batched bounds (lo/hi are pages [P, D],
+// a.n is the block table's row width, a row's blocks past its request's
+// count are not scored, and a block on an invalid page gets key 0).
+template <typename Q, int P, int STEPS, bool FULL, int GT, bool PG = false>
+__device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
+                                         const Paging& pg = Paging{}) {
   constexpr int C = GT * STEPS;           // (head, block) sums per wave
   constexpr int QN = GT * 64 * P;         // staged query values
   __shared__ __align__(16) double s_q[QN];
@@ -120,15 +123,36 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg) {
   const int c = score_lane(l16);              // logical lane
   const int sub = lane >> 4;                  // block within a 4-block step
   const int wave_base = (chunk * kScoreWaves + wave_id()) * (4 * STEPS);
+  // PG: the table entries and the row's block count are requested together
+  // (the entries' loads are bounded by the table width, not by the count)
+  int pgs[PG ? STEPS : 1];
+  if constexpr (PG) {
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int nb = wave_base + 4 * s + sub;
+      pgs[s] = pg_page(pg, kv, a.n, nb, nb < a.n);
+    }
+  }
+  const int nv = PG ? pg_blocks(pg, kv, a.n) : a.n;   // blocks of this row
+  if (PG && chunk * kScoreWaves * 4 * STEPS >= nv) return;   // whole workgroup
   // every lo/hi load of the wave is issued before any arithmetic, with no
   // branch around a load: blocks past n read row 0 and are not stored
   float4 lv[STEPS][P], hv[STEPS][P];
+  int dead = 0;   // PG: bit s set when this lane's block of step s has no page
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     const int nb = wave_base + 4 * s + sub;
-    const bool valid = nb < a.n;
-    const float* lrow = a.lo + ((size_t)kv * a.n + (valid ? nb : 0)) * a.d;
-    const float* hrow = a.hi + ((size_t)kv * a.n + (valid ? nb : 0)) * a.d;
+    const bool valid = nb < nv;
+    size_t row;
+    if constexpr (PG) {
+      const int page = valid ? pgs[s] : -1;
+      dead |= (page < 0) << s;
+      row = page >= 0 ? (size_t)page : 0;
+    } else {
+      row = (size_t)kv * a.n + (valid ? nb : 0);
+    }
+    const float* lrow = a.lo + row * a.d;
+    const float* hrow = a.hi + row * a.d;
 #pragma unroll
     for (int j = 0; j < P; ++j) {
       const int d0 = 64 * j + 4 * c;
@@ -194,11 +218,11 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg) {
     const int combo = l16 >> (4 - LOGC);
     const int gi = combo / STEPS, s = combo % STEPS;
     const int nb = wave_base + 4 * s + sub;
-    if ((l16 & ((16 >> LOGC) - 1)) == 0 && nb < a.n && gb + gi < G) {
+    if ((l16 & ((16 >> LOGC) - 1)) == 0 && nb < nv && gb + gi < G) {
       if (r == 0.0) r = 0.0;
       const size_t o = (size_t)(h0 + gb + gi) * a.n + nb;
       if (a.scores) a.scores[o] = (float)r;
-      if (a.keys) a.keys[o] = score_key(r);
+      if (a.keys) a.keys[o] = (PG && ((dead >> s) & 1)) ? 0ull : score_key(r);
     }
   }
 }

@@ -8,46 +8,9 @@
 // speculate(mode, keep_mass=True)) followed by repair_signed_fused
 // (benchmarks/run_benchmark.py:99-118, strict_topk/signed_fused.py:148-193):
 // nine launches on two streams.
-#include "step.hpp"
-#include "tail_signed.hpp"
-
-namespace stk {
-
-template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
-__global__ __launch_bounds__(kTailThreads) void k_stail(STailArgs a) {
-  stail_head<T, NCH, UP, ONE, KPT, RPT>(a);
-}
-
-}  // namespace stk
+#include "step_launch.hpp"
 
 using namespace stk;
-
-namespace {
-
-template <typename T, int NCH, int UP, bool ONE>
-int launch_stail(const STailArgs& t, const StepShape& s, hipStream_t st) {
-  const dim3 grid(t.kv.hq), block(kTailThreads);
-#define STK_STAIL(KPT)                                                                  \
-  if (s.rpt == 4)                                                                       \
-    hipLaunchKernelGGL((k_stail<T, NCH, UP, ONE, KPT, 4>), grid, block, 0, st, t);      \
-  else                                                                                  \
-    hipLaunchKernelGGL((k_stail<T, NCH, UP, ONE, KPT, 16>), grid, block, 0, st, t);
-  if (s.kpt == 4) { STK_STAIL(4) }
-  else if (s.kpt == 8) { STK_STAIL(8) }
-  else { STK_STAIL(16) }
-#undef STK_STAIL
-  return stk_check_launch("k_stail");
-}
-
-template <typename T, int NCH>
-int launch_stail_t(const STailArgs& t, const StepShape& s, hipStream_t st) {
-  return s.up == 1 ? (s.one ? launch_stail<T, NCH, 1, true>(t, s, st)
-                            : launch_stail<T, NCH, 1, false>(t, s, st))
-                   : (s.one ? launch_stail<T, NCH, 2, true>(t, s, st)
-                            : launch_stail<T, NCH, 2, false>(t, s, st));
-}
-
-}  // namespace
 
 extern "C" {
 
@@ -94,8 +57,7 @@ STK_API int stk_signed_step(const void* q, const void* k, const void* v, int dty
   hipStream_t st = (hipStream_t)stream;
   const int rc = launch_front(dtype, f, s, st);
   if (rc) return rc;
-  STK_DISPATCH_STEP(dtype, s.nch, { return launch_stail_t<T, NCH>(t, s, st); });
-  return STK_EINVAL;
+  return launch::stail<false>(dtype, t, s, st);
 }
 
 }  // extern "C"

@@ -50,9 +50,12 @@ constexpr int kGrpHT = 4;   // heads sharing one loaded tile (generic-tile kerne
 // and the first round trip is one ID instead of the group's rows.
 //
 // ONE (B == CH): the block is one token chunk, loaded once; otherwise the
-// block is streamed chunk by chunk.
-template <typename T, int NCH, int UP, typename I, bool ONE>
-__device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
+// block is streamed chunk by chunk.  PG: paged, batched KV (a.n is the block
+// table's row width; an ID at or past its request's block count, or on an
+// invalid page, gets the empty state).
+template <typename T, int NCH, int UP, typename I, bool ONE, bool PG = false>
+__device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg,
+                                              const Paging& pg = Paging{}) {
   using TT = TokTile<T, NCH, UP>;
   const int waves = blockDim.x / STK_WAVE;
   const int64_t item = (int64_t)wg * waves + wave_id();
@@ -63,12 +66,24 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg) {
   uint32_t qw[TT::QW];
   t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)h * a.d, qw);
   const int64_t bid = reinterpret_cast<const I*>(a.ids)[item];
-  bool enabled = bid >= 0 && bid < a.n;
+  const int kv = h / (a.hq / a.hkv);
+  // PG: the row's block count comes with the ID; the table entry needs only
+  // the ID (bounded by the table width), then the tile needs the page
+  const int nv = PG ? pg_blocks(pg, kv, a.n) : a.n;
+  const bool inrow = bid >= 0 && bid < a.n;
+  bool enabled = inrow && bid < nv;
   if (a.active_kind == 1) enabled = enabled && a.active[h] != 0;
   else if (a.active_kind == 2) enabled = enabled && a.active[item] != 0;
-  const int kv = h / (a.hq / a.hkv);
   const float scale = 1.0f / sqrtf((float)a.d);
-  const size_t off = (((size_t)kv * a.n + (enabled ? (size_t)bid : 0)) * a.b) * a.d;
+  size_t page;
+  if constexpr (PG) {
+    const int pgi = pg_page(pg, kv, a.n, bid, inrow);
+    enabled = enabled && pgi >= 0;
+    page = enabled ? (size_t)pgi : 0;
+  } else {
+    page = (size_t)kv * a.n + (enabled ? (size_t)bid : 0);
+  }
+  const size_t off = (page * a.b) * a.d;
   const T* kb = reinterpret_cast<const T*>(a.k) + off;
   const T* vb = reinterpret_cast<const T*>(a.v) + off;
   float m = -INFINITY, l = 0.f, acc[TT::DPL];

@@ -17,34 +17,7 @@
 //                  blocks' tiles).
 // The arithmetic is that of stk_select_blocks, stk_block_partials and
 // stk_gqa_repair; results are identical up to FP32 reduction order.
-#include "step.hpp"
-#include "topk.hpp"
-#include "tail.hpp"
-
-namespace stk {
-
-template <typename T, int NCH, int UP, bool ONE, int P, int STEPS, int GT>
-__global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_front(FrontArgs a) {
-  // Workgroups are dealt round-robin over the 8 XCDs; roles are interleaved
-  // on an XCD-contiguous logical index, so every XCD gets an even mix of
-  // scoring and speculation work (and, with G query heads per KV head, the
-  // scoring and the states of one KV head land on the same XCD's L2).
-  const int i = xcd_remap(blockIdx.x, gridDim.x);
-  // score workgroups among logical indices [0, i) and [0, i]
-  const int before = (int)(((int64_t)i * a.score_wgs) / a.total_wgs);
-  const int upto = (int)(((int64_t)(i + 1) * a.score_wgs) / a.total_wgs);
-  if (upto > before)
-    score_wg<T, P, STEPS, true, GT>(a.sc, before);
-  else
-    states_tok_wg<T, NCH, UP, int32_t, ONE>(a.st, i - upto);
-}
-
-template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
-__global__ __launch_bounds__(kTailThreads) void k_tail(TailArgs a) {
-  tail_head<T, NCH, UP, ONE, KPT, RPT>(a);
-}
-
-}  // namespace stk
+#include "step_launch.hpp"
 
 namespace stk {
 
@@ -95,59 +68,8 @@ FrontArgs make_front_args(const void* q, const void* k, const void* v, int dtype
 
 using namespace stk;
 
-namespace {
-
-template <typename T, int NCH, int UP, bool ONE, int P, int STEPS>
-int launch_front_gt(const FrontArgs& f, const StepShape& s, hipStream_t st) {
-  const dim3 grid(f.total_wgs), block(256);
-  if (s.gt == 1)
-    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 1>), grid, block, 0, st, f);
-  else if (s.gt == 2)
-    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 2>), grid, block, 0, st, f);
-  else
-    hipLaunchKernelGGL((k_front<T, NCH, UP, ONE, P, STEPS, 4>), grid, block, 0, st, f);
-  return stk_check_launch("k_front");
-}
-
-template <typename T, int NCH, int UP, bool ONE>
-int launch_tail(const TailArgs& t, const StepShape& s, hipStream_t st) {
-  const dim3 grid(t.kv.hq), block(kTailThreads);
-#define STK_TAIL(KPT)                                                                   \
-  if (s.rpt == 4)                                                                       \
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, KPT, 4>), grid, block, 0, st, t);       \
-  else                                                                                  \
-    hipLaunchKernelGGL((k_tail<T, NCH, UP, ONE, KPT, 16>), grid, block, 0, st, t);
-  if (s.kpt == 4) { STK_TAIL(4) }
-  else if (s.kpt == 8) { STK_TAIL(8) }
-  else { STK_TAIL(16) }
-#undef STK_TAIL
-  return stk_check_launch("k_tail");
-}
-
-template <typename T, int NCH>
-int launch_front_t(const FrontArgs& f, const StepShape& s, hipStream_t st) {
-  constexpr int P = NCH * 16 / (int)sizeof(T) * 4 / 64;   // D / 64
-  constexpr int STEPS = P <= 2 ? 2 : 1;
-  // ONE: the whole block is one token chunk (B == 16 * UP)
-  return s.up == 1 ? (s.one ? launch_front_gt<T, NCH, 1, true, P, STEPS>(f, s, st)
-                            : launch_front_gt<T, NCH, 1, false, P, STEPS>(f, s, st))
-                   : (s.one ? launch_front_gt<T, NCH, 2, true, P, STEPS>(f, s, st)
-                            : launch_front_gt<T, NCH, 2, false, P, STEPS>(f, s, st));
-}
-
-template <typename T, int NCH>
-int launch_tail_t(const TailArgs& t, const StepShape& s, hipStream_t st) {
-  return s.up == 1 ? (s.one ? launch_tail<T, NCH, 1, true>(t, s, st)
-                            : launch_tail<T, NCH, 1, false>(t, s, st))
-                   : (s.one ? launch_tail<T, NCH, 2, true>(t, s, st)
-                            : launch_tail<T, NCH, 2, false>(t, s, st));
-}
-
-}  // namespace
-
 int stk::launch_front(int dtype, const FrontArgs& f, const StepShape& s, hipStream_t st) {
-  STK_DISPATCH_STEP(dtype, s.nch, { return launch_front_t<T, NCH>(f, s, st); });
-  return STK_EINVAL;
+  return launch::front<false>(dtype, f, s, st);
 }
 
 extern "C" {
@@ -198,8 +120,7 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
     if (rc) return rc;
   }
   if (!tail) return STK_OK;
-  STK_DISPATCH_STEP(dtype, s.nch, { return launch_tail_t<T, NCH>(t, s, st); });
-  return STK_EINVAL;
+  return launch::tail<false>(dtype, t, s, st);
 }
 
 STK_API int stk_speculative_step(const void* q, const void* k, const void* v, int dtype, int hq,

@@ -14,6 +14,7 @@ struct FrontArgs {
   ScoreArgs sc;
   StatesArgs st;
   int score_wgs, total_wgs;
+  Paging pg;             // paged, batched KV (the PG kernels only)
 };
 
 // Compile-time shape choices of one fused step.

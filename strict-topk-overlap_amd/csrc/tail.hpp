@@ -37,11 +37,17 @@ struct TailArgs {
   const float* pm; const float* pl; const float* pu;   // predicted states
   int uni;                                // repair_union instead of saved
   float* out;                             // [hq, d]
+  Paging pg;                              // PG: paged, batched KV
 };
 
 // KPT keys per thread (n <= 512 * KPT); RPT predicted-state rows per thread,
 // four columns each (sp <= RPT * 2048 / D); ONE: a block is one token chunk.
-template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
+// PG: paged, batched KV.  a.kv.n is then the key rows' and block table's
+// width; the head's request has n <= a.kv.n blocks, of which min(k, n) are
+// selected (the rest of the ID row is -1).  The pages of the row's blocks are
+// loaded with the keys, so a selected block's page is known the moment the
+// top-K names it, with no extra round trip before its tile.
+template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT, bool PG = false>
 __device__ __forceinline__ void tail_head(const TailArgs& a) {
   using TT = TokTile<T, NCH, UP>;
   constexpr int D = TT::D;
@@ -55,13 +61,26 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   __shared__ float s_hmax[kTailWaves], s_hl[kTailWaves];
   __shared__ __align__(16) float s_hu[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_wu[kTailWaves][D];
+  __shared__ int spg[PG ? kTailMaxK : 1];   // PG: pages of the selected blocks
   const int h = blockIdx.x;
-  const int n = a.kv.n, sp = a.sp;
+  const int nrow = a.kv.n, sp = a.sp;
   const int tid = threadIdx.x, w = wave_id();
   const int G = a.kv.hq / a.kv.hkv;
   // ---- round trip 1: every load that does not depend on the top-K
   uint64_t key[KPT];
-  topk_load<KPT>(a.keys + (size_t)h * n, n, key);
+  topk_load<KPT>(a.keys + (size_t)h * nrow, nrow, key);
+  // PG: the pages of this thread's blocks and the row's block count come
+  // with the keys (the dense step computes its KV head later, off the path
+  // of the entry loads)
+  const int kvp = PG ? h / G : 0;
+  int pgk[PG ? KPT : 1];
+  if constexpr (PG) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i)
+      pgk[i] = pg_page(a.pg, kvp, nrow, tid * KPT + i, tid * KPT + i < nrow);
+  }
+  const int n = PG ? pg_blocks(a.pg, kvp, nrow) : nrow;   // blocks of the row
+  const int kk = PG ? (a.k < n ? a.k : n) : a.k;           // selected
   const int pid = (int)ld_or(a.p, (int64_t)h * sp + tid, tid < sp, (int32_t)-1);
   TT t;
   t.init();
@@ -81,7 +100,10 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   }
   // ---- membership map: max predicted slot + 1 per block ID
   for (int i = tid; i < n; i += kTailThreads) map[i] = 0;
-  if (tid < sp) {
+  // every slot entry is written (empty past sp): the row sums below read
+  // entries past sp with zero weight, and LDS holds whatever an earlier
+  // workgroup left there (NaN patterns included, and 0 * NaN is NaN)
+  if (tid < kTailMaxK) {
     pids[tid] = pid;
     s_pm[tid] = pmv;
     s_pl[tid] = plv;
@@ -89,33 +111,39 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   __syncthreads();
   if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
   // ---- exact top-K (its first barrier orders the map writes above)
-  topk_select_keys<KPT>(key, n, a.k, tl, [&](int pos, int idx) {
-    sel[pos] = idx;
-    atomicOr(&map[idx], kSelFlag);
-  });
+  if (!PG || kk > 0)
+    topk_select_keys<KPT>(key, n, kk, tl, [&](int pos, int idx, int i) {
+      sel[pos] = idx;
+      if constexpr (PG) spg[pos] = pgk[i];
+      atomicOr(&map[idx], kSelFlag);
+    });
   __syncthreads();
   // ---- misses (selected, not predicted) in ascending block order, listed
   // by every wave for itself: wave w keeps misses w, w + 8, ... (its own
   // entries of the list, read back only by it) and the count
+  // (PG: a miss on an invalid page has the empty state and is not listed;
+  // the list holds the misses' pages instead of their IDs)
   int nm = 0;
-  for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
+  for (int p0 = 0; p0 < kk; p0 += STK_WAVE) {
     const int p = p0 + lane_id();
-    const bool in = p < a.k;
+    const bool in = p < kk;
     const int id = in ? sel[p] : 0;
-    const bool ms = in && (map[id] & ~kSelFlag) == 0;
+    const int mp = PG ? (in ? spg[p] : -1) : id;
+    const bool ms = in && (map[id] & ~kSelFlag) == 0 && (!PG || mp >= 0);
     const uint64_t bal = __ballot(ms);
     const int x = nm + (int)__popcll(bal & lanemask_lt());
-    if (ms && x % kTailWaves == w) miss[x] = id;
+    if (ms && x % kTailWaves == w) miss[x] = mp;
     nm += (int)__popcll(bal);
   }
   // ---- round trip 2: wave w streams misses w, w + 8, ...; the first
   // tile's loads are issued before the hits' arithmetic
-  const int kvh = h / G;
+  const int kvh = PG ? kvp : h / G;
   const float scale = 1.0f / sqrtf((float)D);
   const T* K = reinterpret_cast<const T*>(a.kv.k);
   const T* V = reinterpret_cast<const T*>(a.kv.v);
   auto tile = [&](int x) {
-    return (((size_t)kvh * n + miss[x]) * a.kv.b) * D;
+    const size_t page = PG ? (size_t)miss[x] : (size_t)kvh * n + miss[x];
+    return (page * a.kv.b) * D;
   };
   uint32_t kw[UP][TT::QW], vw[TT::CH][TT::VW];
   // the entry loads (u rows, query) returned during the top-K
@@ -123,7 +151,8 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   if (ONE && w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
   // the selected IDs go out behind the tile loads (stores count in the same
   // vector memory counter, so stores issued before the drain would hold it)
-  for (int i = tid; i < a.k; i += kTailThreads) a.ids[(size_t)h * a.k + i] = sel[i];
+  for (int i = tid; i < a.k; i += kTailThreads)
+    a.ids[(size_t)h * a.k + i] = (!PG || i < kk) ? sel[i] : -1;
   // ---- the hits' (or, for union, every predicted row's) partial LSE sums:
   // saved mode takes slot p when P[p] is selected and p is the highest slot
   // holding that block; union mode takes every slot.  Each wave sums its
@@ -148,8 +177,10 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   for (int j = 0; j < RPT; ++j) {
     const int r = rg + RG * j;
     const float wt = used[j] ? wexp(um[j], hm) : 0.f;
+    // rows past sp were loaded from row 0 (or a stand-in buffer): zero them
+    const float4 ur = r < sp ? uu[j] : make_float4(0.f, 0.f, 0.f, 0.f);
     hl += wt * s_pl[r < kTailMaxK ? r : 0];
-    hu.x += wt * uu[j].x; hu.y += wt * uu[j].y; hu.z += wt * uu[j].z; hu.w += wt * uu[j].w;
+    hu.x += wt * ur.x; hu.y += wt * ur.y; hu.z += wt * ur.z; hu.w += wt * ur.w;
   }
   // fold the row groups of this wave (lanes with the same columns)
   static_assert(TPR <= STK_WAVE, "state rows wider than a wave");

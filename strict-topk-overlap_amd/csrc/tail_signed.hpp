@@ -59,9 +59,12 @@ struct STailArgs {
   uint8_t* bad; float* remain;            // [hq]
   uint8_t* approx; float* extra;          // [hq] or null when eps == 0
   int32_t* pos; int32_t* total;           // [hq] job counts
+  Paging pg;                              // PG: paged, batched KV
 };
 
-template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT>
+// PG: paged, batched KV, as in tail_head (min(k, n) selected of the
+// request's n blocks; pages loaded with the keys).
+template <typename T, int NCH, int UP, bool ONE, int KPT, int RPT, bool PG = false>
 __device__ __forceinline__ void stail_head(const STailArgs& a) {
   using TT = TokTileW<T, NCH, UP>;
   constexpr int D = TT::D;
@@ -87,14 +90,27 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   __shared__ __align__(16) float s_su[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves];
   __shared__ float s_wu[kTailWaves][D];
+  __shared__ int spg[PG ? kTailMaxK : 1];   // PG: pages of the selected blocks
   const int h = blockIdx.x;
-  const int n = a.kv.n, sp = a.sp;
+  const int nrow = a.kv.n, sp = a.sp;
   const int tid = threadIdx.x, w = wave_id();
   const int G = a.kv.hq / a.kv.hkv;
   const bool hybrid = a.hybrid != 0;
   // ---- round trip 1: every load that does not depend on the top-K
   uint64_t key[KPT];
-  topk_load<KPT>(a.keys + (size_t)h * n, n, key);
+  topk_load<KPT>(a.keys + (size_t)h * nrow, nrow, key);
+  // PG: the pages of this thread's blocks and the row's block count come
+  // with the keys (the dense step computes its KV head later, off the path
+  // of the entry loads)
+  const int kvp = PG ? h / G : 0;
+  int pgk[PG ? KPT : 1];
+  if constexpr (PG) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i)
+      pgk[i] = pg_page(a.pg, kvp, nrow, tid * KPT + i, tid * KPT + i < nrow);
+  }
+  const int n = PG ? pg_blocks(a.pg, kvp, nrow) : nrow;   // blocks of the row
+  const int kk = PG ? (a.k < n ? a.k : n) : a.k;           // selected
   const int pid = (int)ld_or(a.p, (int64_t)h * sp + tid, tid < sp, (int32_t)-1);
   TT t;
   t.init();
@@ -112,7 +128,10 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   }
   // ---- membership map: max predicted slot + 1 per block ID
   for (int i = tid; i < n; i += kTailThreads) map[i] = 0;
-  if (tid < sp) {
+  // every slot entry is written (empty past sp): the row sums below read
+  // entries past sp with zero weight, and LDS holds whatever an earlier
+  // workgroup left there (NaN patterns included, and 0 * NaN is NaN)
+  if (tid < kTailMaxK) {
     pids[tid] = pid;
     s_pm[tid] = pmv;
     s_pl[tid] = plv;
@@ -121,10 +140,12 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   __syncthreads();
   if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
   // ---- exact top-K (its first barrier orders the map writes above)
-  topk_select_keys<KPT>(key, n, a.k, tl, [&](int pos, int idx) {
-    sel[pos] = idx;
-    atomicOr(&map[idx], kSelFlag);
-  });
+  if (!PG || kk > 0)
+    topk_select_keys<KPT>(key, n, kk, tl, [&](int pos, int idx, int i) {
+      sel[pos] = idx;
+      if constexpr (PG) spg[pos] = pgk[i];
+      atomicOr(&map[idx], kSelFlag);
+    });
   __syncthreads();
   // ---- per-slot work (wave 0), lane l holding slots l, l + 64, ...; SWN
   // slot words, one when SP <= 64 (a single wave runs this part alone, so
@@ -245,24 +266,30 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   // by every wave for itself: wave w keeps misses w, w + 8, ... (its own
   // entries of the list, read back only by it) and the count, so its tile
   // loads go out before the per-slot work and the barrier below
+  // (PG: a miss on an invalid page has the empty state and is not listed;
+  // the list holds the misses' pages instead of their IDs)
   int nm = 0;
-  for (int p0 = 0; p0 < a.k; p0 += STK_WAVE) {
+  for (int p0 = 0; p0 < kk; p0 += STK_WAVE) {
     const int p = p0 + lane_id();
-    const bool in = p < a.k;
+    const bool in = p < kk;
     const int id = in ? sel[p] : 0;
-    const bool ms = in && (map[id] & ~kSelFlag) == 0;
+    const int mp = PG ? (in ? spg[p] : -1) : id;
+    const bool ms = in && (map[id] & ~kSelFlag) == 0 && (!PG || mp >= 0);
     const uint64_t bal = __ballot(ms);
     const int x = nm + (int)__popcll(bal & lanemask_lt());
-    if (ms && x % kTailWaves == w) miss[x] = id;
+    if (ms && x % kTailWaves == w) miss[x] = mp;
     nm += (int)__popcll(bal);
   }
   // ---- round trip 2: wave w streams misses w, w + 8, ..., two tiles in
   // flight when they fit
-  const int kvh = h / G;
+  const int kvh = PG ? kvp : h / G;
   const float scale = 1.0f / sqrtf((float)D);
   const T* K = reinterpret_cast<const T*>(a.kv.k);
   const T* V = reinterpret_cast<const T*>(a.kv.v);
-  auto tile = [&](int x) { return (((size_t)kvh * n + miss[x]) * a.kv.b) * D; };
+  auto tile = [&](int x) {
+    const size_t page = PG ? (size_t)miss[x] : (size_t)kvh * n + miss[x];
+    return (page * a.kv.b) * D;
+  };
   uint32_t kw[UP][TT::QW];
   uint4 vw[TT::NV];
   uint32_t kw2[UP][TT::QW];
@@ -274,7 +301,8 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   if (DB && w + kTailWaves < nm)
     t.load(K + tile(w + kTailWaves), V + tile(w + kTailWaves), 0, kw2, vw2);
   // the selected IDs go out behind the tile loads
-  for (int i = tid; i < a.k; i += kTailThreads) a.ids[(size_t)h * a.k + i] = sel[i];
+  for (int i = tid; i < a.k; i += kTailThreads)
+    a.ids[(size_t)h * a.k + i] = (!PG || i < kk) ? sel[i] : -1;
   if (w == 0) {
     if (sp <= STK_WAVE) slots(std::integral_constant<int, 1>{});
     else slots(std::integral_constant<int, SW>{});
@@ -307,15 +335,17 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     const float wl = lo ? wexp(pm, lowm) : 0.f;
     const float wn = wr ? wl : 0.f;
     const float ws = us ? wexp(pm, mu) : 0.f;
+    // rows past sp were loaded from row 0 (or a stand-in buffer): zero them
+    const float4 u4 = r < sp ? uu[j] : make_float4(0.f, 0.f, 0.f, 0.f);
     hl += wk * pl;
     nl += wn * pl;
     sl += ws * pl;
-    hu.x += wk * uu[j].x; hu.y += wk * uu[j].y; hu.z += wk * uu[j].z; hu.w += wk * uu[j].w;
-    lu.x += wl * uu[j].x; lu.y += wl * uu[j].y; lu.z += wl * uu[j].z; lu.w += wl * uu[j].w;
-    la.x += wl * fabsf(uu[j].x); la.y += wl * fabsf(uu[j].y);
-    la.z += wl * fabsf(uu[j].z); la.w += wl * fabsf(uu[j].w);
-    nu.x += wn * uu[j].x; nu.y += wn * uu[j].y; nu.z += wn * uu[j].z; nu.w += wn * uu[j].w;
-    su.x += ws * uu[j].x; su.y += ws * uu[j].y; su.z += ws * uu[j].z; su.w += ws * uu[j].w;
+    hu.x += wk * u4.x; hu.y += wk * u4.y; hu.z += wk * u4.z; hu.w += wk * u4.w;
+    lu.x += wl * u4.x; lu.y += wl * u4.y; lu.z += wl * u4.z; lu.w += wl * u4.w;
+    la.x += wl * fabsf(u4.x); la.y += wl * fabsf(u4.y);
+    la.z += wl * fabsf(u4.z); la.w += wl * fabsf(u4.w);
+    nu.x += wn * u4.x; nu.y += wn * u4.y; nu.z += wn * u4.z; nu.w += wn * u4.w;
+    su.x += ws * u4.x; su.y += ws * u4.y; su.z += ws * u4.z; su.w += ws * u4.w;
   }
   // fold the row groups of this wave (lanes with the same columns)
 #pragma unroll

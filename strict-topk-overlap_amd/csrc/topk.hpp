@@ -18,6 +18,8 @@
 // digits through ballots first.)
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace stk {
@@ -134,7 +136,12 @@ __device__ __forceinline__ void topk_select_keys(const uint64_t (&key)[KPT], int
     const bool e = valid && km == prefix;
     const bool sel = valid && (km > prefix || (e && eq_before < need));
     eq_before += e;
-    if (sel) emit(pos++, base + i);
+    if (sel) {
+      // emit(rank, index) or emit(rank, index, i): i is the key's slot in
+      // this thread's registers (a compile-time index once unrolled)
+      if constexpr (std::is_invocable_v<EMIT, int, int, int>) emit(pos++, base + i, i);
+      else emit(pos++, base + i);
+    }
   }
 }
 

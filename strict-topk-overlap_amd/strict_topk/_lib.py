@@ -68,6 +68,11 @@ _SIGS = {
     "stk_bounds_append": (I, [P, I, I, I, I, I, I, P, P, P]),
     "stk_signed_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I, F, F, F, F,
                             P, P, P, P, P, P, P, P, P, P, P, P, Z, P]),
+    "stk_paged_workspace_bytes": (Z, [I, I, I]),
+    "stk_paged_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, I, P, I, I,
+                           P, P, P, P, P, P, Z, P]),
+    "stk_paged_signed_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, I, P, I, I,
+                                  F, F, F, F, P, P, P, P, P, P, P, P, P, P, P, P, Z, P]),
 }
 
 EXPORTS = tuple(_SIGS)

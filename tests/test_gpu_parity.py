@@ -602,6 +602,7 @@ def test_touch_kv_checksums():
     (8, 2, 400, 64, 128, 32, 0.9, torch.bfloat16, False),     # B = 64: two streamed chunks
     (4, 2, 300, 48, 64, 16, 0.75, torch.float16, False),      # B = 48: three 16-token chunks
     (32, 2, 1000, 32, 128, 64, 0.9, torch.bfloat16, True),    # G = 16: G * SP = 1024
+    (8, 2, 200, 16, 64, 20, 0.75, torch.float16, True),       # state rows past SP (D = 64)
 ])
 def test_speculative_step(hq, hkv, n, b, d, topk, overlap, dtype, union):
     """speculative_step: selected IDs bit-exact, prediction states and the
@@ -695,3 +696,167 @@ def test_speculative_step_composed_fallback(dtype, b):
     res = step.speculative_step(qd, kd, vd, lod, hid, pd, 6)
     assert res.selected.cpu().numpy().tolist() == ref_ids.tolist()
     check(res.output, O.attention(qn, kn, vn, ref_ids), "composed step")
+
+
+# ------------------------------------------------- paged, batched decode steps
+def _paged_batch(hq, hkv, b, d, counts, dtype, seed, topk, sp, overlap=0.75, spare=5):
+    """Seeded requests packed into one page pool in a shuffled page order;
+    per request: host q, k, v, lo, hi, predicted rows [Hq, sp] and whether
+    the dense fused step can serve it (n_r >= topk)."""
+    from stk_harness.configs import make_qkv, perturb
+    from strict_topk import paged
+    reqs = []
+    for r, n in enumerate(counts):
+        q, k, v, lo, hi = make_qkv(hq, hkv, d, b, n, dtype, True, seed + 97 * r)
+        g = torch.Generator().manual_seed(seed + r)
+        if n >= topk + sp:
+            ref = O.select_blocks(C.f64(q), lo.numpy(), hi.numpy(), topk)
+            p = perturb(torch.from_numpy(ref), n, sp, overlap, seed + r)
+        else:
+            # short request: unique in-range IDs where possible, one slot past
+            # the request's blocks (empty state)
+            p = torch.stack([torch.randperm(max(n, sp), generator=g)[:sp] for _ in range(hq)])
+            p = p.to(torch.int32)
+        reqs.append(dict(q=q, k=k, v=v, lo=lo, hi=hi, p=p.to(torch.int32), n=n))
+    total = hkv * sum(counts)
+    order = torch.randperm(total, generator=torch.Generator().manual_seed(seed))
+    kv = paged.pack([(r_["k"].to(DEV), r_["v"].to(DEV)) for r_ in reqs], order=order,
+                    spare=spare)
+    q = torch.stack([r_["q"] for r_ in reqs]).to(DEV)
+    p = torch.stack([r_["p"] for r_ in reqs]).to(DEV)
+    return reqs, kv, q, p
+
+
+def _oracle_ids(p, n):
+    pn = C.ids_np(p).copy()
+    pn[pn >= n] = -1
+    return pn
+
+
+@pytest.mark.parametrize("hq,hkv,b,d,counts,topk,sp,dtype,union", [
+    (32, 8, 32, 128, (1000, 64, 40, 2100, 300), 64, 64, torch.bfloat16, False),  # c5-like
+    (8, 2, 16, 64, (200, 17, 700), 20, 24, torch.float16, True),        # union, B = 16
+    (12, 1, 64, 128, (130, 500), 32, 32, torch.bfloat16, False),        # G = 12, B = 64
+])
+def test_paged_step(hq, hkv, b, d, counts, topk, sp, dtype, union):
+    """The batched paged step: per request, IDs bit-exact against the oracle
+    (a short request selects all its blocks, then -1), states and output
+    bit-identical to the dense fused step on the request's own blocks where
+    that step applies, and the output against FP64 attention over the
+    selected blocks (or the oracle's union repair) everywhere."""
+    from strict_topk import paged, step
+    reqs, kv, q, p = _paged_batch(hq, hkv, b, d, counts, dtype, 20261215 + hq, topk, sp)
+    res = paged.speculative_step(q, kv, p, topk, union=union)
+    torch.cuda.synchronize()
+    assert res.selected.shape == (len(counts), hq, topk)
+    for r, rq in enumerate(reqs):
+        qn, kn, vn = np_(rq["q"], rq["k"], rq["v"])
+        n = rq["n"]
+        pn = _oracle_ids(rq["p"], n)
+        lo_p, hi_p = (t.cpu().numpy() for t in (kv.lo_pages, kv.hi_pages))
+        tab, nbk = kv.block_table.cpu().numpy(), kv.nblocks.cpu().numpy()
+        ids = O.paged_select(qn, lo_p, hi_p, tab, nbk, r, topk)
+        assert res.selected[r].cpu().numpy().tolist() == ids.tolist(), r
+        st = O.block_states(qn, kn, vn, pn)
+        np.testing.assert_allclose(res.state.m[r].cpu().double().numpy(), st.m, rtol=1e-5,
+                                   atol=1e-5)
+        np.testing.assert_allclose(res.state.l[r].cpu().double().numpy(), st.l, rtol=1e-4,
+                                   atol=1e-5)
+        sel = [row[row >= 0] for row in ids]
+        if union:
+            expected = O.gqa_repair(qn, kn, vn, np.stack(sel), pn, st, union=True)
+        else:
+            expected = O.attention(qn, kn, vn, sel)
+        check(res.output[r], expected, ("paged", r, n))
+        if n >= topk:
+            qd, kd, vd, lod, hid, pd = dev(rq["q"], rq["k"], rq["v"], rq["lo"], rq["hi"],
+                                           rq["p"])
+            dense = step.speculative_step(qd, kd, vd, lod, hid, pd, topk, union=union)
+            assert torch.equal(dense.selected, res.selected[r])
+            assert torch.equal(dense.state.m, res.state.m[r])
+            assert torch.equal(dense.state.l, res.state.l[r])
+            assert torch.equal(dense.state.u, res.state.u[r])
+            assert torch.equal(dense.output, res.output[r]), ("dense vs paged", r)
+
+
+@pytest.mark.parametrize("eps", [0.01, 0.0])
+def test_paged_signed_step(eps):
+    """The batched signed step against the dense signed step (bit-identical
+    fields) and, for a request shorter than K, against the oracle's
+    select || speculate -> repair_signed_fused over all its blocks."""
+    from strict_topk import paged, step
+    hq, hkv, b, d, topk, sp, tau = 32, 8, 32, 128, 64, 32, 0.2
+    counts = (900, 40, 2500, 256)
+    reqs, kv, q, p = _paged_batch(hq, hkv, b, d, counts, torch.bfloat16, 20261222, topk, sp,
+                                  overlap=0.6)
+    res = paged.speculative_signed_step(q, kv, p, topk, "hybrid", tau, max_extra_mass=eps)
+    torch.cuda.synchronize()
+    out = res.result
+    for r, rq in enumerate(reqs):
+        n = rq["n"]
+        if n >= topk:
+            qd, kd, vd, lod, hid, pd = dev(rq["q"], rq["k"], rq["v"], rq["lo"], rq["hi"],
+                                           rq["p"])
+            dn = step.speculative_signed_step(qd, kd, vd, lod, hid, pd, topk, "hybrid", tau,
+                                              max_extra_mass=eps)
+            assert torch.equal(dn.selected, res.selected[r])
+            assert torch.equal(dn.state.u, res.state.u[r])
+            for f in ("output", "fallback", "remaining", "positive_jobs", "total_jobs"):
+                assert torch.equal(getattr(dn.result, f), getattr(out, f)[r]), (r, f)
+            if eps > 0:
+                assert torch.equal(dn.result.approximate_heads, out.approximate_heads[r])
+                assert torch.equal(dn.result.extra_mass_bound, out.extra_mass_bound[r])
+        qn, kn, vn = np_(rq["q"], rq["k"], rq["v"])
+        pn = C.ids_np(rq["p"])
+        sel = np.tile(np.arange(n), (hq, 1)) if n < topk else \
+            O.select_blocks(qn, rq["lo"].numpy(), rq["hi"].numpy(), topk)
+        assert res.selected[r, :, :min(n, topk)].cpu().numpy().tolist() == sel.tolist()
+        pred = O.speculate(qn, kn, vn, pn, "hybrid", tau, keep_mass=True)
+        ref = O.repair_signed_fused(qn, kn, vn, sel, pn, pred, max_extra_mass=eps)
+        assert out.fallback[r].cpu().numpy().tolist() == ref.fallback.tolist(), r
+        check(out.output[r], ref.output, ("paged signed", r, n))
+
+
+def test_paged_exact_invalid_pages_and_graph():
+    """The serial path over a paged batch (no prediction); invalid pages
+    (-1 and past the pool) are never read and score lowest; one captured
+    graph serves new block counts and tables written on the device between
+    replays."""
+    from strict_topk import paged
+    hq, hkv, b, d, topk = 8, 2, 32, 128, 16
+    counts = (120, 9, 300)
+    reqs, kv, q, _ = _paged_batch(hq, hkv, b, d, counts, torch.bfloat16, 20261229, topk, 8)
+
+    def expect(r, sel_ids, tab, nbk, invalid=None):
+        rq = reqs[r]
+        qn, kn, vn = np_(rq["q"], rq["k"], rq["v"])
+        ids = O.paged_select(qn, *(t.cpu().numpy() for t in (kv.lo_pages, kv.hi_pages)), tab,
+                             nbk, r, topk, invalid=invalid)
+        assert sel_ids.cpu().numpy().tolist() == ids.tolist(), r
+        n = int(nbk[r])
+        return O.attention(qn, kn[:, :n], vn[:, :n], [row[row >= 0] for row in ids])
+
+    sel, out = paged.exact(q, kv, topk)
+    tab, nbk = kv.block_table.cpu().numpy(), kv.nblocks.cpu().numpy()
+    for r in range(len(counts)):
+        check(out[r], expect(r, sel[r], tab, nbk), ("exact", r))
+    # invalid pages in request 2: block 5 of KV head 1 (-1), block 2 of KV
+    # head 0 (past the pool); they must never be chosen, nor read
+    kv.block_table[2, 1, 5] = -1
+    kv.block_table[2, 0, 2] = kv.pages + 7
+    inv = np.zeros((hkv, counts[2]), bool)
+    inv[1, 5] = inv[0, 2] = True
+    sel, out = paged.exact(q, kv, topk)
+    tab = kv.block_table.cpu().numpy()
+    tab_ok = tab.copy()
+    tab_ok[tab_ok < 0] = 0
+    tab_ok[tab_ok >= kv.pages] = 0
+    check(out[2], expect(2, sel[2], tab_ok, nbk, invalid=inv), "invalid pages")
+    # graph: capture once, then shorten request 0 and lengthen nothing else
+    g, (gsel, gout) = _capture(lambda: paged.exact(q, kv, topk))
+    for n0 in (120, 50, 16, 5):
+        kv.nblocks[0] = n0
+        g.replay()
+        torch.cuda.synchronize()
+        nbk = kv.nblocks.cpu().numpy()
+        check(gout[0], expect(0, gsel[0], tab_ok, nbk), ("graph", n0))

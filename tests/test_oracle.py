@@ -307,3 +307,60 @@ def test_indexer_scores_pinned_against_reference_formula():
     ids = O.indexer_select(iq.numpy(), ik.numpy(), 20, 5)
     order = sorted(range(300), key=lambda j: (-got[j], j))[:20]
     assert ids.shape == (5, 20) and (ids == np.array(sorted(order))[None, :]).all()
+
+
+def _pack_np(caches, rng, spare=3):
+    """Pack dense caches [(k [Hkv, n_r, B, D]), ...] into pages in a random
+    order (numpy, independent of the product's packer)."""
+    hkv = caches[0].shape[0]
+    total = hkv * sum(c.shape[1] for c in caches)
+    width = max(c.shape[1] for c in caches)
+    slot = rng.permutation(total)
+    pages = np.zeros((total + spare,) + caches[0].shape[2:])
+    table = np.full((len(caches), hkv, width), -1, np.int64)
+    base = 0
+    for r, c in enumerate(caches):
+        n = c.shape[1]
+        idx = slot[base:base + hkv * n]
+        pages[idx] = c.reshape((hkv * n,) + c.shape[2:])
+        table[r, :, :n] = idx.reshape(hkv, n)
+        base += hkv * n
+    return pages, table, np.array([c.shape[1] for c in caches])
+
+
+def test_paged_gather_and_select_pinned():
+    """The paged wire format: gathering a request's pages gives back its dense
+    cache (any page order); FlashInfer's mapping (flashinfer_backend.py:35-40,
+    page = block + kv_head * N over k.view(hkv * n, b, 1, d)) is the
+    one-request table kvh * N + j; the paged selection equals the dense one
+    for n_r >= k, is every block plus -1 padding for n_r < k, and never takes
+    a block on an invalid page while valid ones remain (brute force)."""
+    rng = np.random.default_rng(5)
+    hkv, g, b, d = 2, 3, 4, 8
+    ks = [rng.standard_normal((hkv, n, b, d)) for n in (9, 3, 14)]
+    pages, table, nb = _pack_np(ks, rng)
+    for r, k in enumerate(ks):
+        assert np.array_equal(O.gather_pages(pages, table, nb, r), k)
+    k = ks[2]
+    fi = (np.arange(hkv)[:, None] * k.shape[1] + np.arange(k.shape[1])[None, :])[None]
+    assert np.array_equal(O.gather_pages(k.reshape(-1, b, d), fi, [k.shape[1]], 0), k)
+    lo_p, hi_p = pages.min(1), pages.max(1)
+    q = rng.standard_normal((3, hkv * g, d))
+    for r, k in enumerate(ks):
+        n = k.shape[1]
+        for kk in (1, 3, 5, 14):
+            got = O.paged_select(q[r], lo_p, hi_p, table, nb, r, kk)
+            if kk <= n:
+                assert np.array_equal(got, O.select_blocks(q[r], k.min(2), k.max(2), kk))
+            else:
+                assert np.array_equal(got[:, :n], np.tile(np.arange(n), (hkv * g, 1)))
+                assert (got[:, n:] == -1).all()
+    # invalid pages: blocks 0 and 5 of KV head 1 of request 2
+    inv = np.zeros((hkv, 14), bool)
+    inv[1, [0, 5]] = True
+    got = O.paged_select(q[2], lo_p, hi_p, table, nb, 2, 6, invalid=inv)
+    sc = O.bound_scores(q[2], ks[2].min(2), ks[2].max(2))
+    for h in range(hkv * g):
+        bad = inv[h // g]
+        order = sorted((j for j in range(14) if not bad[j]), key=lambda j: (-sc[h, j], j))[:6]
+        assert got[h].tolist() == sorted(order)
