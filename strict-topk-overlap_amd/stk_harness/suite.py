@@ -21,7 +21,9 @@ config exercises (SURVEY's scope table; BASELINE.json ``configs``):
   c5  16 requests with 8K-128K contexts and overlap U[0.5, 1]: per request
       gqa.select_blocks || kernels.speculate('hybrid', 0.2, keep_mass=True)
       -> signed_fused.repair_signed_fused with max_extra_mass 0.01 and 0
-      (strict); serial = gqa.exact(select) per request.
+      (strict); serial = gqa.exact(select) per request; and the whole batch
+      in one page pool (strict_topk.paged: the batched signed step against the
+      batched serial path, two launches each), the primary pair.
   c3 sweep  the fused step against the serial path at every c3 hit rate
       (overlap 1.0, 0.9, 0.75), three seeds each.
 
@@ -36,7 +38,8 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from strict_topk import fused, gqa, gqa_hierarchical, indexer, kernels, selector, signed_fused
+from strict_topk import (fused, gqa, gqa_hierarchical, indexer, kernels, paged, selector,
+                         signed_fused)
 from strict_topk import step as step_mod
 
 from . import timing
@@ -291,11 +294,26 @@ def case_c5(dev, seed=20261103):
                                                                        cf["topk"]))
              for r in reqs], rs)
 
+    # the whole batch in one paged pool: every request's front in one grid,
+    # every (request, head) tail in one launch, for the speculative step and
+    # for the serial path (top-K, then exact attention) alike
+    kvp = paged.pack([(k, v) for _, k, v, _, _, _, _ in reqs])
+    qb = torch.stack([r[0] for r in reqs])
+    pb = torch.stack([r[6] for r in reqs])
+
+    def paged_step(eps):
+        return lambda i: paged.speculative_signed_step(qb, kvp, pb, cf["topk"], "hybrid", 0.2,
+                                                       max_extra_mass=eps).result.output
+
+    def paged_serial(i):
+        return paged.exact(qb, kvp, cf["topk"])[1]
+
     graphs, outs = {}, {}
     for name, fn in (("step_eps0.01", fused_step(0.01)), ("step_strict", fused_step(0.0)),
                      ("signed_eps0.01", full(0.01)), ("signed_strict", full(0.0)),
                      ("serial", serial), ("step_eps0.01_4streams", fused_step_conc(0.01)),
-                     ("serial_4streams", serial_conc)):
+                     ("serial_4streams", serial_conc), ("paged_step_eps0.01", paged_step(0.01)),
+                     ("paged_step_strict", paged_step(0.0)), ("paged_serial", paged_serial)):
         graphs[name], outs[name] = timing.capture(lambda fn=fn: fn(0))
     g = cf["hq"] // cf["hkv"]
     tile = 2 * cf["block"] * cf["dim"] * 2
@@ -314,13 +332,16 @@ def case_c5(dev, seed=20261103):
     case = Case("c5", "per request: gqa.select_blocks || kernels.speculate('hybrid', 0.2, "
                 "keep_mass) -> signed_fused.repair_signed_fused (eps 0.01 and strict): the "
                 "fused two-launch step (step_*) and the two-stream composition (signed_*)",
-                graphs, 1, full_b, kv_b, ser_b, primary="step_eps0.01",
+                graphs, 1, full_b, kv_b, ser_b, primary="paged_step_eps0.01",
+                baseline="paged_serial",
                 notes=f"16 requests, contexts {int(blocks.min()) * 32}-{int(blocks.max()) * 32} "
                       "tokens; one graph replay = one batched decode step; *_4streams: the "
-                      "requests spread over four streams",
+                      "requests spread over four streams; paged_*: the whole batch in one page "
+                      "pool, two launches per step (strict_topk.paged)",
                 pairs={"sequential": ("step_eps0.01", "serial"),
-                       "four_streams": ("step_eps0.01_4streams", "serial_4streams")})
-    case.keep = (reqs, ss, ps, rs)
+                       "four_streams": ("step_eps0.01_4streams", "serial_4streams"),
+                       "batched_paged": ("paged_step_eps0.01", "paged_serial")})
+    case.keep = (reqs, ss, ps, rs, kvp, qb, pb)
     for r, (q, k, v, lo, hi, sel, p) in enumerate(reqs):
         hq_, hlo, hhi = _host(q, lo, hi)
         case.check.append((f"ids[{r}]", "select", (hq_, hlo, hhi, cf["topk"], sel.cpu())))
@@ -345,6 +366,12 @@ def case_c5(dev, seed=20261103):
                             outs["step_eps0.01_4streams"][r].cpu())))
         case.check.append((f"serial_4streams[{r}]", "attention",
                            (hq_, ks, vs, sel_r, outs["serial_4streams"][r].cpu())))
+        case.check.append((f"paged_step_eps0.01[{r}]", "signed_fused",
+                           (hq_, ks, vs, sel_r, p_r, 0.01, outs["paged_step_eps0.01"][r].cpu())))
+        case.check.append((f"paged_step_strict[{r}]", "attention",
+                           (hq_, ks, vs, sel_r, outs["paged_step_strict"][r].cpu())))
+        case.check.append((f"paged_serial[{r}]", "attention",
+                           (hq_, ks, vs, sel_r, outs["paged_serial"][r].cpu())))
     return case
 
 
