@@ -317,6 +317,19 @@ int stk_signed_step(const void* q, const void* k, const void* v, int dtype, int 
  * stk_step_supported with n = nb and topk, sp <= 256. */
 size_t stk_paged_workspace_bytes(int requests, int hq, int nb);
 
+/* One decode token per request into the pool: k_new, v_new [R, Hkv, D] go to
+ * token position positions[r] (block pos / B, offset pos % B) of the page
+ * block_table[r, kvh, pos / B]; that page's lo/hi are widened by the new key
+ * (offset 0 starts them over, as stk_bounds_append does for the dense layout)
+ * and nblocks[r] becomes pos / B + 1.  A position outside [0, nb * B) or an
+ * invalid page writes nothing.  The reference has no decode append (its
+ * harness builds the bounds once, benchmarks/critical_path.py:186); this is
+ * the paged form of stk_bounds_append plus the K/V write. */
+int stk_paged_append(const void* k_new, const void* v_new, int dtype, int requests, int hkv,
+                     int nb, int b, int d, int pages, void* k_pages, void* v_pages,
+                     float* lo_pages, float* hi_pages, const int32_t* block_table,
+                     int32_t* nblocks, const int32_t* positions, void* stream);
+
 /* stk_speculative_step over a paged batch (union_mode: repair_union). */
 int stk_paged_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
                    int requests, int hq, int hkv, int nb, int b, int d, int pages,

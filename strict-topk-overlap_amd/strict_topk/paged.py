@@ -15,10 +15,11 @@ explicit per (request, KV head), so requests share one pool and one launch:
 ``speculative_step`` and ``speculative_signed_step`` run the fused steps of
 ``strict_topk.step`` over the whole batch in two launches, and ``exact`` is
 the serial path (top-K, then exact attention over the selected blocks) in
-the same two launches with no prediction.  Per request the results are those
-of the dense steps on the request's own blocks, bit for bit, except that a
-request with fewer blocks than ``topk`` selects all of them (the rest of its
-ID row is -1).  A table entry outside [0, P) is an invalid page: its block
+the same two launches with no prediction; ``append`` writes one decode token
+per request into its page and widens that page's bounds.  Per request the
+results are those of the dense steps on the request's own blocks, bit for
+bit, except that a request with fewer blocks than ``topk`` selects all of them
+(the rest of its ID row is -1).  A table entry outside [0, P) is an invalid page: its block
 scores lowest and has the empty state, and nothing is read from it.
 """
 from __future__ import annotations
@@ -105,6 +106,35 @@ def pack(caches, width=None, order=None, spare=0):
     lo, hi = block_bounds(k_pages.unsqueeze(0))
     return PagedKV(k_pages, v_pages, lo[0], hi[0], table.to(dev),
                    torch.tensor(counts, dtype=torch.int32, device=dev))
+
+
+def append(kv, k_new, v_new, positions):
+    """Write one decode token per request in place: k_new, v_new [R, Hkv, D]
+    at token position positions[r] (block pos // B, offset pos % B) of that
+    block's page; the page's lo/hi are widened by the new key (offset 0 starts
+    them over) and nblocks[r] becomes pos // B + 1, in one launch.  positions
+    is an int32 tensor on the device, so a captured graph can advance it.  A
+    position outside [0, NB * B), or a block without a valid page, writes
+    nothing."""
+    if not isinstance(kv, PagedKV):
+        raise TypeError("kv must be a PagedKV")
+    shape = (kv.requests, kv.hkv, kv.dim)
+    if k_new.shape != shape or v_new.shape != shape:
+        raise ValueError("expected K_NEW/V_NEW[R,Hkv,D] matching the pool")
+    if positions.shape != (kv.requests,) or positions.dtype != torch.int32:
+        raise ValueError("expected int32 positions[R]")
+    if k_new.dtype != kv.k_pages.dtype or v_new.dtype != kv.k_pages.dtype:
+        raise ValueError("K_NEW/V_NEW must match the pages' dtype")
+    ts = (k_new, v_new, positions, kv.k_pages, kv.v_pages, kv.lo_pages, kv.hi_pages,
+          kv.block_table, kv.nblocks)
+    if any(t.device != kv.k_pages.device or not t.is_contiguous() for t in ts):
+        raise ValueError("all tensors must be contiguous and on one CUDA device")
+    _lib.call("stk_paged_append", _lib.ptr(k_new), _lib.ptr(v_new), _lib.dtype_code(k_new),
+              kv.requests, kv.hkv, kv.width, kv.block, kv.dim, kv.pages, _lib.ptr(kv.k_pages),
+              _lib.ptr(kv.v_pages), _lib.ptr(kv.lo_pages), _lib.ptr(kv.hi_pages),
+              _lib.ptr(kv.block_table), _lib.ptr(kv.nblocks), _lib.ptr(positions),
+              _lib.stream(k_new.device))
+    return kv
 
 
 def _check(q, kv, predicted, topk):

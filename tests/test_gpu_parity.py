@@ -111,7 +111,8 @@ def test_select_nonfinite_bounds():
 
 @pytest.mark.parametrize("dtype,b,d", [(torch.bfloat16, 32, 128), (torch.float16, 4, 64),
                                      (torch.bfloat16, 16, 256), (torch.float32, 8, 48),
-                                     (torch.float16, 5, 13)])
+                                     (torch.float16, 5, 13), (torch.bfloat16, 32, 256),
+                                     (torch.float16, 7, 192), (torch.bfloat16, 100, 128)])
 def test_block_bounds_and_append(dtype, b, d):
     """Block metadata bit-exact against the oracle (min / max are exact), NaN
     keys included; appending a block's tokens one by one gives the same
@@ -860,3 +861,60 @@ def test_paged_exact_invalid_pages_and_graph():
         torch.cuda.synchronize()
         nbk = kv.nblocks.cpu().numpy()
         check(gout[0], expect(0, gsel[0], tab_ok, nbk), ("graph", n0))
+
+
+def test_paged_append_matches_packing():
+    """Decode appends into a paged pool: writing each request's last block
+    token by token (one launch per token for the whole batch, the positions a
+    device tensor advanced between the calls of one captured graph) leaves
+    the pages, the lo/hi pages and the block counts equal to packing the
+    complete caches; after a partial block, that page's bounds are the
+    min / max of its tokens so far."""
+    from strict_topk import paged
+    hkv, b, d = 2, 16, 64
+    counts = (5, 2, 9)
+    gen = torch.Generator().manual_seed(77)
+    full = [(torch.randn((hkv, n, b, d), generator=gen).half(),
+             torch.randn((hkv, n, b, d), generator=gen).half()) for n in counts]
+    order = torch.randperm(hkv * sum(counts), generator=gen)
+    ref = paged.pack([(k.to(DEV), v.to(DEV)) for k, v in full], order=order, spare=3)
+    # the same pool with every last block zeroed and the counts one short
+    part = []
+    for k, v in full:
+        k2, v2 = k.clone(), v.clone()
+        k2[:, -1].zero_()
+        v2[:, -1].zero_()
+        part.append((k2.to(DEV), v2.to(DEV)))
+    kv = paged.pack(part, order=order, spare=3)
+    kv.nblocks.sub_(1)
+    start = torch.tensor([(n - 1) * b for n in counts], dtype=torch.int32, device=DEV)
+    pos = start.clone()
+    kn = torch.empty((len(counts), hkv, d), dtype=torch.float16, device=DEV)
+    vn = torch.empty_like(kn)
+
+    def feed(t):
+        kn.copy_(torch.stack([k[:, -1, t] for k, _ in full]))
+        vn.copy_(torch.stack([v[:, -1, t] for _, v in full]))
+
+    feed(0)
+    g, _ = _capture(lambda: paged.append(kv, kn, vn, pos))   # writes token 0 (capture + replay)
+    for t in range(1, b):
+        pos.copy_(start + t)
+        feed(t)
+        g.replay()
+        torch.cuda.synchronize()
+        if t == 6:
+            for r, n in enumerate(counts):
+                for h in range(hkv):
+                    page = int(kv.block_table[r, h, n - 1])
+                    toks = full[r][0][h, -1, :t + 1].float()
+                    assert torch.equal(kv.lo_pages[page].cpu(), toks.amin(0))
+                    assert torch.equal(kv.hi_pages[page].cpu(), toks.amax(0))
+    assert kv.nblocks.cpu().tolist() == list(counts)
+    assert torch.equal(kv.k_pages, ref.k_pages) and torch.equal(kv.v_pages, ref.v_pages)
+    assert torch.equal(kv.lo_pages, ref.lo_pages) and torch.equal(kv.hi_pages, ref.hi_pages)
+    # a position past the table writes nothing
+    before = kv.k_pages.clone()
+    paged.append(kv, kn, vn, torch.full_like(pos, max(counts) * b))
+    torch.cuda.synchronize()
+    assert torch.equal(before, kv.k_pages)
