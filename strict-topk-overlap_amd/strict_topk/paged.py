@@ -127,7 +127,8 @@ def append(kv, k_new, v_new, positions):
         raise ValueError("K_NEW/V_NEW must match the pages' dtype")
     ts = (k_new, v_new, positions, kv.k_pages, kv.v_pages, kv.lo_pages, kv.hi_pages,
           kv.block_table, kv.nblocks)
-    if any(t.device != kv.k_pages.device or not t.is_contiguous() for t in ts):
+    if not kv.k_pages.is_cuda or any(t.device != kv.k_pages.device or not t.is_contiguous()
+                                     for t in ts):
         raise ValueError("all tensors must be contiguous and on one CUDA device")
     _lib.call("stk_paged_append", _lib.ptr(k_new), _lib.ptr(v_new), _lib.dtype_code(k_new),
               kv.requests, kv.hkv, kv.width, kv.block, kv.dim, kv.pages, _lib.ptr(kv.k_pages),
@@ -155,14 +156,14 @@ def _check(q, kv, predicted, topk):
         raise ValueError("lo and hi pages must be FP32")
     if kv.block_table.dtype != torch.int32 or kv.nblocks.dtype != torch.int32:
         raise ValueError("block_table and nblocks must be int32")
-    ts = [q, kv.k_pages, kv.v_pages, kv.lo_pages, kv.hi_pages, kv.block_table, kv.nblocks]
-    if predicted is not None:
-        ts.append(predicted)
-    if any(t.device != q.device or not t.is_contiguous() for t in ts):
-        raise ValueError("all tensors must be contiguous and on one CUDA device")
     topk = int(topk)
     if not 1 <= topk <= 256:
         raise ValueError("topk must be in [1, 256]")
+    ts = [q, kv.k_pages, kv.v_pages, kv.lo_pages, kv.hi_pages, kv.block_table, kv.nblocks]
+    if predicted is not None:
+        ts.append(predicted)
+    if not q.is_cuda or any(t.device != q.device or not t.is_contiguous() for t in ts):
+        raise ValueError("all tensors must be contiguous and on one CUDA device")
     return r, hq, topk
 
 

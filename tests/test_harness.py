@@ -28,3 +28,53 @@ def test_every_case_keeps_the_device_inputs_its_graphs_read():
 def test_bench_releases_graphs_with_their_inputs():
     src = (ROOT / "bench.py").read_text()
     assert "case.release()" in src and "case.graphs = {}" not in src
+
+
+def test_paged_api_validates_on_the_host():
+    """The paged entry points reject malformed batches before any launch
+    (no GPU needed): wrong Q / prediction shapes, dtypes, widths and topk."""
+    import sys
+    import pytest
+    import torch
+    sys.path.insert(0, str(ROOT / "strict-topk-overlap_amd"))
+    from strict_topk import paged
+    r, hkv, nb, b, d, pages = 2, 2, 5, 4, 64, 30
+    kv = paged.PagedKV(torch.zeros((pages, b, d), dtype=torch.bfloat16),
+                       torch.zeros((pages, b, d), dtype=torch.bfloat16),
+                       torch.zeros((pages, d)), torch.zeros((pages, d)),
+                       torch.zeros((r, hkv, nb), dtype=torch.int32),
+                       torch.full((r,), nb, dtype=torch.int32))
+    assert (kv.requests, kv.hkv, kv.width, kv.pages, kv.block, kv.dim) == (r, hkv, nb, pages, b, d)
+    q = torch.zeros((r, 4, d), dtype=torch.bfloat16)
+    p = torch.zeros((r, 4, 3), dtype=torch.int32)
+    with pytest.raises(ValueError, match="Q\\[R,Hq,D\\]"):
+        paged.speculative_step(q[:1], kv, p, 2)
+    with pytest.raises(ValueError, match="divisible"):
+        paged.speculative_step(torch.zeros((r, 3, d), dtype=torch.bfloat16), kv, p[:, :3], 2)
+    with pytest.raises(ValueError, match="P\\[R,Hq,SP\\]"):
+        paged.speculative_step(q, kv, p[:, :2], 2)
+    with pytest.raises(ValueError, match="int32"):
+        paged.speculative_step(q, kv, p.long(), 2)
+    with pytest.raises(ValueError, match="dtype"):
+        paged.exact(q.half(), kv, 2)
+    with pytest.raises(ValueError, match="topk"):
+        paged.exact(q, kv, 0)
+    with pytest.raises(ValueError, match="topk"):
+        paged.exact(q, kv, 300)
+    with pytest.raises(ValueError):
+        paged.speculative_signed_step(q, kv, p, 2, mode="compact")
+    with pytest.raises(ValueError):
+        paged.speculative_signed_step(q, kv, p, 2, mass_threshold=2.0)
+    with pytest.raises(TypeError):
+        paged.exact(q, (kv.k_pages, kv.v_pages), 2)
+    kn = torch.zeros((r, hkv, d), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="K_NEW"):
+        paged.append(kv, kn[:, :1], kn, torch.zeros((r,), dtype=torch.int32))
+    with pytest.raises(ValueError, match="positions"):
+        paged.append(kv, kn, kn, torch.zeros((r,), dtype=torch.int64))
+    with pytest.raises(ValueError, match="CUDA"):
+        paged.speculative_step(q, kv, p, 2)   # a well-formed batch, but on the CPU
+    with pytest.raises(ValueError, match="CUDA"):
+        paged.append(kv, kn, kn, torch.zeros((r,), dtype=torch.int32))
+    with pytest.raises(ValueError, match="narrower"):
+        paged.pack([(torch.zeros((hkv, 6, b, d)), torch.zeros((hkv, 6, b, d)))], width=3)
