@@ -172,7 +172,11 @@ __global__ __launch_bounds__(256) void k_groups_w(GroupsArgs a) {
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const float wr = __shfl(w, RPI * i + lane / LPR);
-    acc.x += wr * uv[i].x; acc.y += wr * uv[i].y; acc.z += wr * uv[i].z; acc.w += wr * uv[i].w;
+    // a zero weight takes nothing from its row: positions past the group's
+    // end load row 0 of the scratch states, which is never written when
+    // position 0 is a hit (and 0 * NaN would be NaN)
+    const float4 ur = wr != 0.f ? uv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    acc.x += wr * ur.x; acc.y += wr * ur.y; acc.z += wr * ur.z; acc.w += wr * ur.w;
   }
 #pragma unroll
   for (int off = LPR; off < STK_WAVE; off <<= 1) {

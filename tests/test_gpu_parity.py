@@ -918,3 +918,43 @@ def test_paged_append_matches_packing():
     paged.append(kv, kn, vn, torch.full_like(pos, max(counts) * b))
     torch.cuda.synchronize()
     assert torch.equal(before, kv.k_pages)
+
+
+def test_poisoned_workspace(monkeypatch):
+    """Every workspace handed to the library is filled with 0xFF bytes (NaN as
+    floats, the highest key as integers) instead of left as it comes: a
+    kernel that read scratch it did not write, even with a zero weight,
+    would turn the output into NaN here.  Covers the hierarchical repairs
+    (a partial last group of positions), the fused and signed steps and a
+    paged batch."""
+    from stk_harness.configs import make_qkv, perturb
+    from strict_topk import _lib, gqa_hierarchical as impl, paged, step
+    monkeypatch.setattr(_lib, "workspace", lambda nbytes, device: torch.full(
+        (max(int(nbytes), 1),), 255, dtype=torch.uint8, device=device))
+    for (h, hkv, n, b, d, sa), *ts in C.hier_cases(torch.bfloat16):
+        qn, kn, vn, an = np_(*ts)
+        expected = O.attention(qn, kn, vn, an)
+        q, k, v, a = dev(*ts)
+        check(impl.exact(q, k, v, a), expected, ("poisoned exact", n, sa))
+        for hits in (1, sa // 2, sa):
+            p = C.prediction_rows(a.cpu(), n, sa, hits).to(DEV)
+            check(impl.repair_saved(q, k, v, a, p, impl.partials(q, k, v, p)), expected,
+                  ("poisoned saved", n, sa, hits))
+    for hq, hkv, n, b, d, topk, dt in [(32, 8, 2048, 32, 128, 64, torch.bfloat16),
+                                       (8, 2, 200, 16, 64, 20, torch.float16)]:
+        q, k, v, lo, hi = make_qkv(hq, hkv, d, b, n, dt, True, 99 + n)
+        qn, kn, vn = np_(q, k, v)
+        ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), topk)
+        p = perturb(torch.from_numpy(ids), n, topk, 0.75, 5)
+        qd, kd, vd, lod, hid, pd = dev(q, k, v, lo, hi, p)
+        res = step.speculative_step(qd, kd, vd, lod, hid, pd, topk)
+        check(res.output, O.attention(qn, kn, vn, ids), ("poisoned step", n))
+        sres = step.speculative_signed_step(qd, kd, vd, lod, hid, pd, topk, "hybrid", 0.2,
+                                            max_extra_mass=0.01)
+        assert torch.isfinite(sres.result.output).all()
+    reqs, kv, q, p = _paged_batch(8, 2, 16, 64, (200, 17, 700), torch.float16, 4242, 20, 24)
+    sel, out = paged.exact(q, kv, 20)
+    assert torch.isfinite(out).all()
+    res = paged.speculative_step(q, kv, p, 20)
+    assert torch.isfinite(res.output).all()
+    assert torch.equal(res.selected, sel)
