@@ -141,3 +141,13 @@ def test_hip_matches_tiny_fixture():
         res = step.speculative_step(q, k, v, lo, hi, p, topk, union=union)
         np.testing.assert_array_equal(res.selected.cpu().numpy(), fx["selected"])
         _check(res.output, fx[key], ("tiny step", key))
+    # the same request as a one-request paged batch, its pages in reverse order
+    from strict_topk import paged
+    hkv, n = k.shape[:2]
+    order = torch.arange(hkv * n - 1, -1, -1)
+    kv = paged.pack([(k, v)], order=order, spare=2)
+    for union, key in ((False, "saved"), (True, "union")):
+        res = paged.speculative_step(q.unsqueeze(0).contiguous(), kv, p.unsqueeze(0).contiguous(),
+                                     topk, union=union)
+        np.testing.assert_array_equal(res.selected[0].cpu().numpy(), fx["selected"])
+        _check(res.output[0], fx[key], ("tiny paged step", key))
