@@ -168,7 +168,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         sys.exit("bench.py: this path runs on one GPU; --gpus %d is not supported "
-                 "(the decode step shards by KV head with no exchange; see DESIGN.md)" % args.gpus)
+                 "(the decode step would shard by KV head, with no exchange between GPUs)" % args.gpus)
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         sys.exit("bench.py: multi-rank launch is not supported; run with one GPU")
     if not torch.cuda.is_available():

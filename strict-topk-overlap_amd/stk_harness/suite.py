@@ -3,7 +3,7 @@
 Each case builds its seeded inputs on the device, captures its speculative
 path and the same-work serial path into HIP graphs, and times them with
 randomized ABBA pairs (``timing.paired``).  The reference strategy each
-config exercises (SURVEY's scope table; BASELINE.json ``configs``):
+config exercises (BASELINE.json ``configs``):
 
   c1  selector.select_blocks || kernels.speculate('saved') -> kernels.repair,
       the same with fused.repair_fused (two streams, the drop-in
