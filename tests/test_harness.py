@@ -30,6 +30,17 @@ def test_bench_releases_graphs_with_their_inputs():
     assert "case.release()" in src and "case.graphs = {}" not in src
 
 
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU's share; asked for several GPUs it exits
+    with a message before touching any device."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300, cwd=ROOT)
+    assert r.returncode != 0
+    assert "one GPU" in r.stderr and not r.stdout.strip()
+
+
 def test_paged_api_validates_on_the_host():
     """The paged entry points reject malformed batches before any launch
     (no GPU needed): wrong Q / prediction shapes, dtypes, widths and topk."""
