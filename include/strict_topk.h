@@ -305,6 +305,12 @@ int stk_signed_step(const void* q, const void* k, const void* v, int dtype, int 
  *   block_table [R, Hkv, nb] int32   page of logical block j of (request r,
  *                                    KV head kvh), valid for j < nblocks[r]
  *   nblocks [R] int32                blocks per request (device memory)
+ *   ntokens [R] int32 or null        tokens per request (device memory): token
+ *                                    t of block j holds data when
+ *                                    j * B + t < ntokens[r], so a request's
+ *                                    last block may be partly filled (its
+ *                                    other tokens get no weight, whatever the
+ *                                    page holds); null: every block is full
  *   q [R, Hq, D]; predicted [R, Hq, sp] int32 logical block IDs.
  * Per request the results are those of stk_speculative_step /
  * stk_signed_step on the request's blocks gathered from the pool, except
@@ -321,29 +327,34 @@ size_t stk_paged_workspace_bytes(int requests, int hq, int nb);
  * token position positions[r] (block pos / B, offset pos % B) of the page
  * block_table[r, kvh, pos / B]; that page's lo/hi are widened by the new key
  * (offset 0 starts them over, as stk_bounds_append does for the dense layout)
- * and nblocks[r] becomes pos / B + 1.  A position outside [0, nb * B) or an
- * invalid page writes nothing.  The reference has no decode append (its
+ * and nblocks[r] becomes pos / B + 1, ntokens[r] (when not null) pos + 1.
+ * A position outside [0, nb * B) writes nothing; an invalid page writes
+ * nothing for its KV head, and the counts change only when the block has a
+ * valid page for every KV head.  The reference has no decode append (its
  * harness builds the bounds once, benchmarks/critical_path.py:186); this is
  * the paged form of stk_bounds_append plus the K/V write. */
 int stk_paged_append(const void* k_new, const void* v_new, int dtype, int requests, int hkv,
                      int nb, int b, int d, int pages, void* k_pages, void* v_pages,
                      float* lo_pages, float* hi_pages, const int32_t* block_table,
-                     int32_t* nblocks, const int32_t* positions, void* stream);
+                     int32_t* nblocks, int32_t* ntokens, const int32_t* positions,
+                     void* stream);
 
 /* stk_speculative_step over a paged batch (union_mode: repair_union). */
 int stk_paged_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
                    int requests, int hq, int hkv, int nb, int b, int d, int pages,
                    const float* lo_pages, const float* hi_pages, const int32_t* block_table,
-                   const int32_t* nblocks, int topk, const int32_t* predicted, int sp,
-                   int union_mode, int32_t* selected, float* m, float* l, float* u, float* out,
-                   void* workspace, size_t workspace_bytes, void* stream);
+                   const int32_t* nblocks, const int32_t* ntokens, int topk,
+                   const int32_t* predicted, int sp, int union_mode, int32_t* selected, float* m,
+                   float* l, float* u, float* out, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 /* stk_signed_step over a paged batch. */
 int stk_paged_signed_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
                           int requests, int hq, int hkv, int nb, int b, int d, int pages,
                           const float* lo_pages, const float* hi_pages,
-                          const int32_t* block_table, const int32_t* nblocks, int topk,
-                          const int32_t* predicted, int sp, int hybrid, float mass_threshold,
+                          const int32_t* block_table, const int32_t* nblocks,
+                          const int32_t* ntokens, int topk, const int32_t* predicted, int sp,
+                          int hybrid, float mass_threshold,
                           float min_remaining, float cancellation_tol, float max_extra_mass,
                           int32_t* selected, float* m, float* l, float* u, float* out,
                           uint8_t* fallback, float* remaining, uint8_t* approx, float* extra,

@@ -233,9 +233,19 @@ def select_blocks(q, lo, hi, k):
 # attention over ID sets: tests/check_correctness.py:12-17,
 # tests/check_gqa.py:10-17, benchmarks/critical_path.py:16-25 (include mask)
 # ---------------------------------------------------------------------------
-def attention(q, k, v, ids, include=None):
+def _live(rows, b, tokens):
+    """[S, B] mask of the tokens that hold data: token t of block j when
+    j * B + t < tokens (every token when tokens is None)."""
+    if tokens is None:
+        return np.ones((len(rows), b), bool)
+    return (np.asarray(rows, np.int64)[:, None] * b + np.arange(b)[None, :]) < int(tokens)
+
+
+def attention(q, k, v, ids, include=None, tokens=None):
     """FP64 softmax attention of each head over its ID row (rows may differ
-    in length when ``ids`` is a list)."""
+    in length when ``ids`` is a list).  ``tokens``: the sequence's token
+    count, for a partly filled last block (the paged format's ntokens);
+    tokens at or past it get no weight and their values are ignored."""
     q, k, v = _f64(q), _f64(k), _f64(v)
     rows = [np.asarray(r, dtype=np.int64) for r in ids]
     g = _group(q, k)
@@ -245,6 +255,9 @@ def attention(q, k, v, ids, include=None):
         kk = k[h // g][rows[h]]
         vv = v[h // g][rows[h]]
         logits = (kk @ q[h]) / math.sqrt(d)
+        live = _live(rows[h], k.shape[2], tokens)
+        logits = np.where(live, logits, NEG_INF)
+        vv = np.where(live[..., None], vv, 0.0)
         if include is not None:
             logits = np.where(np.asarray(include[h], bool)[:, None], logits, NEG_INF)
         mx = logits.max()
@@ -258,14 +271,21 @@ def attention(q, k, v, ids, include=None):
 # A5/A11: per-block softmax states
 # reference strict_topk/kernels.py:42-71 (_partial), gqa.py:29-59
 # ---------------------------------------------------------------------------
-def _one_state(qh, kb, vb, d):
+def _one_state(qh, kb, vb, d, live=None):
     s = (kb @ qh) * _scale(d)
+    if live is not None:
+        if not live.any():
+            return NEG_INF, 0.0, np.zeros(d)
+        s = np.where(live, s, NEG_INF)
+        vb = np.where(live[:, None], vb, 0.0)
     m = s.max()
     w = np.exp(s - m)
     return m, w.sum(), w @ vb
 
 
-def block_states(q, k, v, ids, active=None, with_values=True):
+def block_states(q, k, v, ids, active=None, with_values=True, tokens=None):
+    """Per-block states of every (head, listed block); ``tokens`` as in
+    ``attention`` (a block with no token holding data has the empty state)."""
     q, k, v = _f64(q), _f64(k), _f64(v)
     ids = np.asarray(ids, dtype=np.int64)
     g = _group(q, k)
@@ -284,7 +304,8 @@ def block_states(q, k, v, ids, active=None, with_values=True):
             b = ids[h, j]
             if b < 0:
                 continue
-            mm, ll, uu = _one_state(q[h], k[h // g, b], v[h // g, b], d)
+            live = None if tokens is None else _live([b], k.shape[2], tokens)[0]
+            mm, ll, uu = _one_state(q[h], k[h // g, b], v[h // g, b], d, live)
             m[h, j], l[h, j] = mm, ll
             if with_values:
                 u[h, j] = uu

@@ -177,8 +177,11 @@ __global__ __launch_bounds__(256) void k_bounds_append(AppendArgs a) {
 // paged.hip): thread (r, kvh, dim) writes K/V element dim of KV head kvh at
 // token position positions[r] (block pos / B, offset pos % B) into that
 // block's page, widens the page's lo/hi by it (offset 0 starts them over),
-// and one thread per request sets nblocks[r] = pos / B + 1.  A position
-// outside [0, nb * B) or a block on an invalid page writes nothing.
+// and one thread per request sets nblocks[r] = pos / B + 1 and (when given)
+// ntokens[r] = pos + 1, after checking that the block has a valid page for
+// every KV head.  A position outside [0, nb * B) writes nothing; a block on an
+// invalid page writes nothing for that KV head and leaves the counts as
+// they were.
 struct PagedAppendArgs {
   const void* k_new; const void* v_new;   // [R, Hkv, D]
   int requests, hkv, nb, b, d, pages;
@@ -186,6 +189,7 @@ struct PagedAppendArgs {
   float* lo; float* hi;                   // [P, D]
   const int32_t* table;                   // [R, Hkv, nb]
   int32_t* nblocks;                       // [R]
+  int32_t* ntokens;                       // [R] or null
   const int32_t* positions;               // [R]
 };
 
@@ -199,7 +203,17 @@ __global__ __launch_bounds__(256) void k_paged_append(PagedAppendArgs a) {
   const int pos = a.positions[r];
   if (pos < 0 || pos >= a.nb * a.b) return;
   const int blk = pos / a.b, off = pos % a.b;
-  if (rk % a.hkv == 0 && dim == 0) a.nblocks[r] = blk + 1;
+  if (rk % a.hkv == 0 && dim == 0) {
+    bool ok = true;
+    for (int kh = 0; kh < a.hkv; ++kh) {
+      const int pk = a.table[((int64_t)rk + kh) * a.nb + blk];
+      ok = ok && pk >= 0 && pk < a.pages;
+    }
+    if (ok) {
+      a.nblocks[r] = blk + 1;
+      if (a.ntokens) a.ntokens[r] = pos + 1;
+    }
+  }
   const int page = a.table[(int64_t)rk * a.nb + blk];
   if (page < 0 || page >= a.pages) return;
   const T kv = reinterpret_cast<const T*>(a.k_new)[x];
@@ -273,7 +287,7 @@ STK_API int stk_bounds_append(const void* k_new, int dtype, int hkv, int n, int 
 STK_API int stk_paged_append(const void* k_new, const void* v_new, int dtype, int requests,
                              int hkv, int nb, int b, int d, int pages, void* k_pages,
                              void* v_pages, float* lo_pages, float* hi_pages,
-                             const int32_t* block_table, int32_t* nblocks,
+                             const int32_t* block_table, int32_t* nblocks, int32_t* ntokens,
                              const int32_t* positions, void* stream) {
   STK_REQUIRE(k_new && v_new && k_pages && v_pages && lo_pages && hi_pages && block_table &&
                   nblocks && positions,
@@ -283,7 +297,7 @@ STK_API int stk_paged_append(const void* k_new, const void* v_new, int dtype, in
   STK_REQUIRE((int64_t)nb * b <= 0x7fffffff && (int64_t)requests * hkv * d <= 0x7fffffff,
               "shape too large");
   PagedAppendArgs a{k_new, v_new, requests, hkv, nb, b, d, pages, k_pages, v_pages,
-                    lo_pages, hi_pages, block_table, nblocks, positions};
+                    lo_pages, hi_pages, block_table, nblocks, ntokens, positions};
   const int64_t n = (int64_t)requests * hkv * d;
   const dim3 grid((unsigned)((n + 255) / 256));
   hipStream_t st = (hipStream_t)stream;

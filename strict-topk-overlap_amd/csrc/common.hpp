@@ -102,18 +102,35 @@ __device__ __forceinline__ X ld_or(const X* p, int64_t i, bool ok, X other) {
 // table[kv * n + j] is the page of logical block j of KV row kv (n = the
 // table's row width), valid for j < nblk[kv / hkv_req].  A table entry
 // outside [0, pages) is an invalid page: its block has the empty state and
-// scores lowest, and nothing is read from it.
+// scores lowest, and nothing is read from it.  ntok (optional) holds each
+// request's token count: token t of block j holds data when j * B + t <
+// ntok[r], so a request's last block may be partly filled (the tokens past
+// the count are never weighted, whatever the page holds there); without it
+// every block holds B tokens.
 struct Paging {
   const int32_t* table;
   const int32_t* nblk;
   int hkv_req;
   int pages;
+  const int32_t* ntok;
 };
 
 // Valid blocks of KV row kv, clamped to [0, n].
 __device__ __forceinline__ int pg_blocks(const Paging& pg, int kv, int n) {
   const int x = pg.nblk[kv / pg.hkv_req];
   return x < 0 ? 0 : (x > n ? n : x);
+}
+
+// Token count of KV row kv's request (INT32_MAX without ntok: every block
+// full); one load, meant to be issued beside the row's other entry loads.
+__device__ __forceinline__ int pg_row_tokens(const Paging& pg, int kv) {
+  return pg.ntok ? pg.ntok[kv / pg.hkv_req] : 0x7fffffff;
+}
+
+// Tokens of block j holding data, in [0, b], given the row's token count.
+__device__ __forceinline__ int pg_block_tokens(int row_tokens, int64_t j, int b) {
+  const int64_t x = (int64_t)row_tokens - j * b;
+  return x <= 0 ? 0 : (x >= b ? b : (int)x);
 }
 
 // Page of block j of KV row kv when ok, else -1; the table load is always

@@ -5,7 +5,9 @@
 // (request, query head).  K/V live in a page pool [P, B, D] (one page = one
 // KV head's block of B tokens), the block bounds in lo/hi pages [P, D], and
 // block_table[r, kvh, j] names the page of logical block j of (request r,
-// KV head kvh) for j < nblocks[r].  The batch is flattened into R * Hq query
+// KV head kvh) for j < nblocks[r]; ntokens[r] (optional) is the request's
+// token count, so its last block may be partly filled (tokens past the count
+// get no weight).  The batch is flattened into R * Hq query
 // heads over R * Hkv KV rows, so the kernels are the dense step's with the
 // page indirection compiled in (PG = true): a page index is validated before
 // every use, and an invalid one contributes the empty state.
@@ -55,9 +57,10 @@ STK_API size_t stk_paged_workspace_bytes(int requests, int hq, int nb) {
 static int paged_common(const void* q, const void* k_pages, const void* v_pages, int dtype,
                         int requests, int hq, int hkv, int nb, int b, int d, int pages,
                         const float* lo_pages, const float* hi_pages, const int32_t* table,
-                        const int32_t* nblocks, int topk, const int32_t* predicted, int sp,
-                        float* m, float* l, float* u, void* workspace, size_t workspace_bytes,
-                        FrontArgs* f, PagedPlan* plan, uint64_t** keys, const void** dummy) {
+                        const int32_t* nblocks, const int32_t* ntokens, int topk,
+                        const int32_t* predicted, int sp, float* m, float* l, float* u,
+                        void* workspace, size_t workspace_bytes, FrontArgs* f, PagedPlan* plan,
+                        uint64_t** keys, const void** dummy) {
   STK_REQUIRE(check_paged(dtype, requests, hq, hkv, nb, b, d, pages, topk, sp));
   STK_REQUIRE(q && k_pages && v_pages && lo_pages && hi_pages && table && nblocks,
               "null pointer");
@@ -79,24 +82,24 @@ static int paged_common(const void* q, const void* k_pages, const void* v_pages,
            stk_align((size_t)requests * hq * nb * sizeof(uint64_t));
   *f = make_front_args(q, k_pages, v_pages, dtype, plan->hq, plan->hkv, nb, b, d, lo_pages,
                        hi_pages, predicted, sp, m, l, u, *keys, plan->s);
-  f->pg = Paging{table, nblocks, hkv, pages};
+  f->pg = Paging{table, nblocks, hkv, pages, ntokens};
   return STK_OK;
 }
 
 STK_API int stk_paged_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
                            int requests, int hq, int hkv, int nb, int b, int d, int pages,
                            const float* lo_pages, const float* hi_pages,
-                           const int32_t* block_table, const int32_t* nblocks, int topk,
-                           const int32_t* predicted, int sp, int union_mode, int32_t* selected,
-                           float* m, float* l, float* u, float* out, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+                           const int32_t* block_table, const int32_t* nblocks,
+                           const int32_t* ntokens, int topk, const int32_t* predicted, int sp,
+                           int union_mode, int32_t* selected, float* m, float* l, float* u,
+                           float* out, void* workspace, size_t workspace_bytes, void* stream) {
   FrontArgs f{};
   PagedPlan plan{};
   uint64_t* keys = nullptr;
   const void* dummy = nullptr;
   int rc = paged_common(q, k_pages, v_pages, dtype, requests, hq, hkv, nb, b, d, pages, lo_pages,
-                        hi_pages, block_table, nblocks, topk, predicted, sp, m, l, u, workspace,
-                        workspace_bytes, &f, &plan, &keys, &dummy);
+                        hi_pages, block_table, nblocks, ntokens, topk, predicted, sp, m, l, u,
+                        workspace, workspace_bytes, &f, &plan, &keys, &dummy);
   if (rc) return rc;
   STK_REQUIRE(selected && out, "null pointer");
   TailArgs t{};
@@ -119,9 +122,9 @@ STK_API int stk_paged_step(const void* q, const void* k_pages, const void* v_pag
 STK_API int stk_paged_signed_step(const void* q, const void* k_pages, const void* v_pages,
                                   int dtype, int requests, int hq, int hkv, int nb, int b, int d,
                                   int pages, const float* lo_pages, const float* hi_pages,
-                                  const int32_t* block_table, const int32_t* nblocks, int topk,
-                                  const int32_t* predicted, int sp, int hybrid,
-                                  float mass_threshold, float min_remaining,
+                                  const int32_t* block_table, const int32_t* nblocks,
+                                  const int32_t* ntokens, int topk, const int32_t* predicted,
+                                  int sp, int hybrid, float mass_threshold, float min_remaining,
                                   float cancellation_tol, float max_extra_mass,
                                   int32_t* selected, float* m, float* l, float* u, float* out,
                                   uint8_t* fallback, float* remaining, uint8_t* approx,
@@ -132,8 +135,8 @@ STK_API int stk_paged_signed_step(const void* q, const void* k_pages, const void
   uint64_t* keys = nullptr;
   const void* dummy = nullptr;
   int rc = paged_common(q, k_pages, v_pages, dtype, requests, hq, hkv, nb, b, d, pages, lo_pages,
-                        hi_pages, block_table, nblocks, topk, predicted, sp, m, l, u, workspace,
-                        workspace_bytes, &f, &plan, &keys, &dummy);
+                        hi_pages, block_table, nblocks, ntokens, topk, predicted, sp, m, l, u,
+                        workspace, workspace_bytes, &f, &plan, &keys, &dummy);
   if (rc) return rc;
   STK_REQUIRE(selected && out && fallback && remaining && positive && total, "null pointer");
   STK_REQUIRE(!(max_extra_mass > 0.f) || (approx && extra),

@@ -70,8 +70,12 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg,
   // PG: the row's block count comes with the ID; the table entry needs only
   // the ID (bounded by the table width), then the tile needs the page
   const int nv = PG ? pg_blocks(pg, kv, a.n) : a.n;
+  const int rtok = PG ? pg_row_tokens(pg, kv) : 0;
   const bool inrow = bid >= 0 && bid < a.n;
-  bool enabled = inrow && bid < nv;
+  // PG: tokens of the block holding data (the request's last block may be
+  // partly filled; a block with none has the empty state)
+  const int bval = PG ? pg_block_tokens(rtok, bid, a.b) : a.b;
+  bool enabled = inrow && bid < nv && (!PG || bval > 0);
   if (a.active_kind == 1) enabled = enabled && a.active[h] != 0;
   else if (a.active_kind == 2) enabled = enabled && a.active[item] != 0;
   const float scale = 1.0f / sqrtf((float)a.d);
@@ -95,11 +99,15 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg,
     // all of the tile's loads are issued before any arithmetic (the
     // scheduler would otherwise sink the V loads below the Q.K products)
     __builtin_amdgcn_sched_barrier(0);
-    if (enabled) t.template update<false, false>(qw, kw, vw, 0, a.b, scale, m, l, acc);
+    if (enabled) {
+      if (PG && bval < a.b) t.update_part(qw, kw, vw, 0, bval, scale, m, l, acc);
+      else t.template update<false, false>(qw, kw, vw, 0, a.b, scale, m, l, acc);
+    }
   } else if (enabled) {
-    for (int t0 = 0; t0 < a.b; t0 += TT::CH) {
+    for (int t0 = 0; t0 < bval; t0 += TT::CH) {
       t.load(kb, vb, t0, kw, vw);
-      t.template update<false, false>(qw, kw, vw, t0, a.b, scale, m, l, acc);
+      if (PG && t0 + TT::CH > bval) t.update_part(qw, kw, vw, t0, bval, scale, m, l, acc);
+      else t.template update<false, false>(qw, kw, vw, t0, a.b, scale, m, l, acc);
     }
   }
   if (lane_id() == 0) {

@@ -62,6 +62,7 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   __shared__ __align__(16) float s_hu[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_wu[kTailWaves][D];
   __shared__ int spg[PG ? kTailMaxK : 1];   // PG: pages of the selected blocks
+  __shared__ int mtk[PG ? kTailMaxK : 1];   // PG: tokens of each listed miss
   const int h = blockIdx.x;
   const int nrow = a.kv.n, sp = a.sp;
   const int tid = threadIdx.x, w = wave_id();
@@ -80,6 +81,7 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
       pgk[i] = pg_page(a.pg, kvp, nrow, tid * KPT + i, tid * KPT + i < nrow);
   }
   const int n = PG ? pg_blocks(a.pg, kvp, nrow) : nrow;   // blocks of the row
+  const int rtok = PG ? pg_row_tokens(a.pg, kvp) : 0;     // PG: tokens of the request
   const int kk = PG ? (a.k < n ? a.k : n) : a.k;           // selected
   const int pid = (int)ld_or(a.p, (int64_t)h * sp + tid, tid < sp, (int32_t)-1);
   TT t;
@@ -121,18 +123,23 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   // ---- misses (selected, not predicted) in ascending block order, listed
   // by every wave for itself: wave w keeps misses w, w + 8, ... (its own
   // entries of the list, read back only by it) and the count
-  // (PG: a miss on an invalid page has the empty state and is not listed;
-  // the list holds the misses' pages instead of their IDs)
+  // (PG: a miss on an invalid page or with no tokens has the empty state and
+  // is not listed; the list holds the misses' pages instead of their IDs, and
+  // their token counts beside them)
   int nm = 0;
   for (int p0 = 0; p0 < kk; p0 += STK_WAVE) {
     const int p = p0 + lane_id();
     const bool in = p < kk;
     const int id = in ? sel[p] : 0;
     const int mp = PG ? (in ? spg[p] : -1) : id;
-    const bool ms = in && (map[id] & ~kSelFlag) == 0 && (!PG || mp >= 0);
+    const int mt = PG ? pg_block_tokens(rtok, id, a.kv.b) : 0;
+    const bool ms = in && (map[id] & ~kSelFlag) == 0 && (!PG || (mp >= 0 && mt > 0));
     const uint64_t bal = __ballot(ms);
     const int x = nm + (int)__popcll(bal & lanemask_lt());
-    if (ms && x % kTailWaves == w) miss[x] = mp;
+    if (ms && x % kTailWaves == w) {
+      miss[x] = mp;
+      if constexpr (PG) mtk[x] = mt;
+    }
     nm += (int)__popcll(bal);
   }
   // ---- round trip 2: wave w streams misses w, w + 8, ...; the first
@@ -200,13 +207,17 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
 #pragma unroll
   for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
   for (int x = w; x < nm; x += kTailWaves) {
+    // PG: a partly filled block weights only its first mtk[x] tokens
+    const int lim = PG ? mtk[x] : a.kv.b;
     if constexpr (ONE) {
       if (x != w) t.load(K + tile(x), V + tile(x), 0, kw, vw);
-      t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+      if (PG && lim < a.kv.b) t.update_part(qw, kw, vw, 0, lim, scale, m, l, acc);
+      else t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
     } else {
-      for (int t0 = 0; t0 < a.kv.b; t0 += TT::CH) {
+      for (int t0 = 0; t0 < lim; t0 += TT::CH) {
         t.load(K + tile(x), V + tile(x), t0, kw, vw);
-        t.template update<false, false>(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
+        if (PG && t0 + TT::CH > lim) t.update_part(qw, kw, vw, t0, lim, scale, m, l, acc);
+        else t.template update<false, false>(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
       }
     }
   }

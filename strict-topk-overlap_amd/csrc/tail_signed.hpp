@@ -91,6 +91,7 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves];
   __shared__ float s_wu[kTailWaves][D];
   __shared__ int spg[PG ? kTailMaxK : 1];   // PG: pages of the selected blocks
+  __shared__ int mtk[PG ? kTailMaxK : 1];   // PG: tokens of each listed miss
   const int h = blockIdx.x;
   const int nrow = a.kv.n, sp = a.sp;
   const int tid = threadIdx.x, w = wave_id();
@@ -110,6 +111,7 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
       pgk[i] = pg_page(a.pg, kvp, nrow, tid * KPT + i, tid * KPT + i < nrow);
   }
   const int n = PG ? pg_blocks(a.pg, kvp, nrow) : nrow;   // blocks of the row
+  const int rtok = PG ? pg_row_tokens(a.pg, kvp) : 0;     // PG: tokens of the request
   const int kk = PG ? (a.k < n ? a.k : n) : a.k;           // selected
   const int pid = (int)ld_or(a.p, (int64_t)h * sp + tid, tid < sp, (int32_t)-1);
   TT t;
@@ -266,18 +268,23 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   // by every wave for itself: wave w keeps misses w, w + 8, ... (its own
   // entries of the list, read back only by it) and the count, so its tile
   // loads go out before the per-slot work and the barrier below
-  // (PG: a miss on an invalid page has the empty state and is not listed;
-  // the list holds the misses' pages instead of their IDs)
+  // (PG: a miss on an invalid page or with no tokens has the empty state and
+  // is not listed; the list holds the misses' pages instead of their IDs, and
+  // their token counts beside them)
   int nm = 0;
   for (int p0 = 0; p0 < kk; p0 += STK_WAVE) {
     const int p = p0 + lane_id();
     const bool in = p < kk;
     const int id = in ? sel[p] : 0;
     const int mp = PG ? (in ? spg[p] : -1) : id;
-    const bool ms = in && (map[id] & ~kSelFlag) == 0 && (!PG || mp >= 0);
+    const int mt = PG ? pg_block_tokens(rtok, id, a.kv.b) : 0;
+    const bool ms = in && (map[id] & ~kSelFlag) == 0 && (!PG || (mp >= 0 && mt > 0));
     const uint64_t bal = __ballot(ms);
     const int x = nm + (int)__popcll(bal & lanemask_lt());
-    if (ms && x % kTailWaves == w) miss[x] = mp;
+    if (ms && x % kTailWaves == w) {
+      miss[x] = mp;
+      if constexpr (PG) mtk[x] = mt;
+    }
     nm += (int)__popcll(bal);
   }
   // ---- round trip 2: wave w streams misses w, w + 8, ..., two tiles in
@@ -383,14 +390,20 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   float m = -INFINITY, l = 0.f, acc[TT::ACC];
 #pragma unroll
   for (int e = 0; e < TT::ACC; ++e) acc[e] = 0.f;
+  // one whole-block tile of miss x (PG: a partly filled block weights only
+  // its first mtk[x] tokens)
+  auto upd1 = [&](int x, const uint32_t (&kx)[UP][TT::QW], const uint4 (&vx)[TT::NV]) {
+    if (PG && mtk[x] < a.kv.b) t.template update<true>(qw, kx, vx, 0, mtk[x], scale, m, l, acc);
+    else t.update(qw, kx, vx, 0, a.kv.b, scale, m, l, acc);
+  };
   if constexpr (DB) {
     // two register buffers: tile x computes while tile x + 8 is in flight
     for (int x = w; x < nm; x += 2 * kTailWaves) {
-      t.update(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+      upd1(x, kw, vw);
       if (x + 2 * kTailWaves < nm)
         t.load(K + tile(x + 2 * kTailWaves), V + tile(x + 2 * kTailWaves), 0, kw, vw);
       if (x + kTailWaves < nm) {
-        t.update(qw, kw2, vw2, 0, a.kv.b, scale, m, l, acc);
+        upd1(x + kTailWaves, kw2, vw2);
         if (x + 3 * kTailWaves < nm)
           t.load(K + tile(x + 3 * kTailWaves), V + tile(x + 3 * kTailWaves), 0, kw2, vw2);
       }
@@ -398,13 +411,15 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   } else if constexpr (ONE) {
     for (int x = w; x < nm; x += kTailWaves) {
       if (x != w) t.load(K + tile(x), V + tile(x), 0, kw, vw);
-      t.update(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+      upd1(x, kw, vw);
     }
   } else {
     for (int x = w; x < nm; x += kTailWaves) {
-      for (int t0 = 0; t0 < a.kv.b; t0 += TT::CH) {
+      const int lim = PG ? mtk[x] : a.kv.b;
+      for (int t0 = 0; t0 < lim; t0 += TT::CH) {
         t.load(K + tile(x), V + tile(x), t0, kw, vw);
-        t.update(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
+        if (PG && t0 + TT::CH > lim) t.template update<true>(qw, kw, vw, t0, lim, scale, m, l, acc);
+        else t.update(qw, kw, vw, t0, a.kv.b, scale, m, l, acc);
       }
     }
   }

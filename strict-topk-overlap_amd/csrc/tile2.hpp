@@ -140,11 +140,13 @@ struct TokTile {
   // Online-softmax update of (m, l, acc) with one chunk whose scaled logits
   // s (this lane's slot, scores()) are known.  FIXED keeps m as the exponent
   // frame (no rescaling; the caller guarantees it).  ABS also accumulates
-  // sum |w * v| (low-group envelope).
-  template <bool FIXED, bool ABS>
+  // sum |w * v| (low-group envelope).  MASKV: tokens vlim .. CH-1 of the
+  // chunk hold no data (their logits must be -inf); their values are taken
+  // as zero, so whatever the memory holds there (NaN included) adds nothing.
+  template <bool FIXED, bool ABS, bool MASKV = false>
   __device__ __forceinline__ void accumulate(const float (&s)[UP], const uint32_t (&vw)[CH][VW],
                                              float& m, float& l, float* acc,
-                                             float* aacc = nullptr) const {
+                                             float* aacc = nullptr, int vlim = CH) const {
     if constexpr (!FIXED) {
       float cm = s[0];
 #pragma unroll
@@ -168,6 +170,10 @@ struct TokTile {
       float wt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w[u]), src));
       float v[DPL];
       vals(vw, i, v);
+      if constexpr (MASKV) {
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) v[e] = i < vlim ? v[e] : 0.f;
+      }
       l += wt;
 #pragma unroll
       for (int e = 0; e < DPL; ++e) {
@@ -187,6 +193,17 @@ struct TokTile {
     float s[UP];
     scores(qw, kw, t0, B, scale, s);
     accumulate<FIXED, ABS>(s, vw, m, l, acc, aacc);
+  }
+
+  // update() for a chunk of a partly filled block: tokens t0 + j with
+  // t0 + j >= valid hold no data (no weight, values taken as zero)
+  __device__ __forceinline__ void update_part(const uint32_t* qw, const uint32_t (&kw)[UP][QW],
+                                              const uint32_t (&vw)[CH][VW], int t0, int valid,
+                                              float scale, float& m, float& l,
+                                              float* acc) const {
+    float s[UP];
+    scores(qw, kw, t0, valid, scale, s);
+    accumulate<false, false, true>(s, vw, m, l, acc, nullptr, valid - t0);
   }
 
   // this lane's DPL dims of a D-vector
@@ -237,7 +254,10 @@ struct TokTileW : TokTile<T, NCH, UP> {
     for (int i = 0; i < NV; ++i) vw[i] = *reinterpret_cast<const uint4*>(vrow + (size_t)i * RPI * D);
   }
 
-  // Online softmax over one chunk (token t0 + j valid when < B).
+  // Online softmax over one chunk (token t0 + j valid when < Bn).  MASKV:
+  // the tokens at or past Bn hold no data and their values are taken as
+  // zero (a partly filled block; whatever the memory holds adds nothing).
+  template <bool MASKV = false>
   __device__ __forceinline__ void update(const uint32_t* qw, const uint32_t (&kw)[UP][QW],
                                          const uint4 (&vw)[NV], int t0, int Bn, float scale,
                                          float& m, float& l, float (&acc)[ACC]) const {
@@ -267,7 +287,12 @@ struct TokTileW : TokTile<T, NCH, UP> {
       const int u = (RPI * i) / TPP;                       // same pass for the whole load
       const int tk = (RPI * i) % TPP + lane_id() / LPR;    // token slot within the pass
       const float wt = __shfl(w[u], tk * LPT);
-      const uint32_t x[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+      uint32_t x[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+      if constexpr (MASKV) {
+        const bool live = t0 + RPI * i + lane_id() / LPR < Bn;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = live ? x[e] : 0u;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         acc[2 * e] += wt * Elem<T>::lo(x[e]);

@@ -69,10 +69,10 @@ _SIGS = {
     "stk_signed_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I, F, F, F, F,
                             P, P, P, P, P, P, P, P, P, P, P, P, Z, P]),
     "stk_paged_workspace_bytes": (Z, [I, I, I]),
-    "stk_paged_append": (I, [P, P, I, I, I, I, I, I, I, P, P, P, P, P, P, P, P]),
-    "stk_paged_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, I, P, I, I,
+    "stk_paged_append": (I, [P, P, I, I, I, I, I, I, I, P, P, P, P, P, P, P, P, P]),
+    "stk_paged_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, P, I, P, I, I,
                            P, P, P, P, P, P, Z, P]),
-    "stk_paged_signed_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, I, P, I, I,
+    "stk_paged_signed_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, P, I, P, I, I,
                                   F, F, F, F, P, P, P, P, P, P, P, P, P, P, P, P, Z, P]),
 }
 

@@ -38,6 +38,8 @@ def append(lo, hi, k_new, block, pos):
         raise ValueError("expected LO/HI[Hkv,N,D] matching K_NEW")
     if lo.dtype != torch.float32 or hi.dtype != torch.float32:
         raise ValueError("lo and hi must be FP32")
+    if any(not x.is_cuda or x.device != k_new.device or not x.is_contiguous() for x in (lo, hi)):
+        raise ValueError("lo and hi must be contiguous and on K_NEW's CUDA device")
     n = lo.shape[1]
     _lib.call("stk_bounds_append", _lib.ptr(k_new), _lib.dtype_code(k_new), hkv, n, d,
               int(block), int(pos), _lib.ptr(lo), _lib.ptr(hi), _lib.stream(k_new.device))

@@ -1,4 +1,4 @@
-"""Single-launch repair for the prediction states in kernels.py.
+"""The whole repair of a kernels.speculate prediction in one launch.
 
 Drop-in for the reference ``strict_topk/fused.py`` (``repair_fused``
 :176-220, kernel semantics :48-173): one workgroup per query head performs
@@ -14,12 +14,14 @@ from .kernels import RepairResult, _args, _shape, prediction_args
 def repair_fused(q, k, v, selected, predicted, prediction,
                  min_remaining=1.e-3, cancellation_tol=1.e-5,
                  max_extra_mass=0.):
-    """Repair finite Q/K/V with valid, unique IDs, using one workgroup per head.
+    """One workgroup per query head repairs the prediction to the selected set.
 
-    The cancellation and remaining-mass guards operate in the original
-    low-group exponent frame, before scaling to the retained or new maximum.
-    A positive max_extra_mass opts into retaining wrong low blocks if their
-    estimated share of the output softmax is within that budget.
+    Inputs: finite Q/K/V, ID rows of unique in-range blocks.  The guards
+    (remaining low mass, per-coordinate cancellation) are evaluated in the
+    low group's own exponent frame, before any rescaling to the final
+    maximum.  With max_extra_mass > 0, wrong low blocks may stay in the
+    output when their bounded share of the softmax mass is at most that
+    value (the head is then reported as approximate).
     """
     h, n, b, d, sa = _shape(q, k, v, selected)
     _, _, _, _, sp = _shape(q, k, v, predicted)

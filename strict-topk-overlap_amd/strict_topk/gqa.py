@@ -1,8 +1,9 @@
-"""Split-block sparse attention for native grouped-query KV layouts.
+"""Block-sparse attention over grouped-query KV (no head expansion).
 
-Q is [query_heads, dim]. K and V are [kv_heads, blocks, tokens, dim].
-Adjacent query heads share a KV head. Each row of IDs contains a nonempty
-set of unique, valid block IDs. Inputs are contiguous and finite.
+Layouts: queries [Hq, D]; keys and values [Hkv, N, B, D], query head h
+reading KV head h // (Hq // Hkv).  ID rows are nonempty, hold distinct
+in-range block numbers and have one row per query head; every tensor is
+contiguous with finite values.
 
 Drop-in for the reference ``strict_topk/gqa.py`` (``partials`` :128-137,
 ``exact`` :140-142, ``select_blocks`` :145-161, ``repair_saved`` :186-188,
@@ -39,7 +40,7 @@ def _shape(q, k, v, ids):
 
 
 def partials(q, k, v, ids):
-    """Compute one FP32 softmax partial per query head and block."""
+    """FP32 softmax state (m, l, u) of every (query head, listed block)."""
     hq, n, b, d, group, sa = _shape(q, k, v, ids)
     state = _allocate_state(hq, sa, d, q.device)
     _lib.call("stk_block_partials", *_args(q, k, v), _lib.ptr(ids), _lib.id_code(ids), sa, None, 0,
@@ -48,7 +49,7 @@ def partials(q, k, v, ids):
 
 
 def exact(q, k, v, selected):
-    """Attend to the selected blocks using parallel partials and a merge."""
+    """Attention over the selected blocks: per-block states, then one LSE merge."""
     hq, n, b, d, group, sa = _shape(q, k, v, selected)
     out = torch.empty((hq, d), device=q.device, dtype=torch.float32)
     ws = _lib.workspace(_lib.size("stk_exact_workspace_bytes", hq, sa, d), q.device)
@@ -58,7 +59,7 @@ def exact(q, k, v, selected):
 
 
 def select_blocks(q, lo, hi, topk):
-    """Select min/max bound top-k using native FP32 metadata [Hkv,N,D]."""
+    """Top-k blocks per query head by the bound score on FP32 LO/HI[Hkv,N,D]."""
     if q.ndim != 2 or lo.ndim != 3 or hi.shape != lo.shape:
         raise ValueError("expected Q[Hq,D] and LO/HI[Hkv,N,D]")
     hkv, n, d = lo.shape
@@ -88,10 +89,10 @@ def _repair(q, k, v, selected, predicted, state, union):
 
 
 def repair_saved(q, k, v, selected, predicted, state):
-    """Reuse predicted hits and compute only selected misses."""
+    """Strict output: predicted states of selected blocks, new states for the rest."""
     return _repair(q, k, v, selected, predicted, state, union=False)
 
 
 def repair_union(q, k, v, selected, predicted, state):
-    """Attend to the union of selected and predicted blocks, once each."""
+    """Output over selected and predicted blocks together, each block counted once."""
     return _repair(q, k, v, selected, predicted, state, union=True)

@@ -1,4 +1,4 @@
-"""Bounded-tile reduction for large per-block GQA state arrays.
+"""GQA attention over many small blocks, states reduced in two levels.
 
 Drop-in for the reference ``strict_topk/gqa_hierarchical.py`` (``partials``
 :55-61, ``exact`` :111-112, ``repair_saved`` :133-134,
@@ -45,10 +45,11 @@ def repair_saved(q, k, v, selected, predicted, state):
 
 
 def repair_saved_shared(q, k, v, selected, predicted, state):
-    """QSA-style shared selection: every head must have identical ordered IDs.
+    """repair_saved for a selection shared by all heads (an indexer's).
 
-    Both selected and predicted arrays must obey this caller-validated
-    contract. Only the first row is used to construct the membership map.
-    Attention arithmetic and states remain independent for every query head.
+    The caller guarantees that every row of ``selected`` is the same list in
+    the same order, and likewise for ``predicted``; this is not checked.
+    Hits and misses are looked up from row 0 only, while each query head
+    still has its own states and output.
     """
     return _repair(q, k, v, selected, predicted, state, True)

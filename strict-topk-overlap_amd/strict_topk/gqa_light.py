@@ -1,4 +1,4 @@
-"""Single-launch saved-state repair for native GQA with few late misses.
+"""GQA saved-state repair in one launch, for steps with few misses per head.
 
 Drop-in for the reference ``strict_topk/gqa_light.py`` (``repair_saved_light``
 :63-77, ``repair_saved_auto`` :80-92).
@@ -24,11 +24,13 @@ def repair_saved_light(q, k, v, selected, predicted, state):
 
 
 def repair_saved_auto(q, k, v, selected, predicted, state, expected_miss_fraction):
-    """Choose a repair schedule using an external estimate from past steps.
+    """Pick the one-launch or the split repair from a caller's miss estimate.
 
-    The threshold of two expected misses per head and at least 16 query
-    heads is a static scheduling hypothesis. Both schedules compute the
-    strict selected set even when the estimate is inaccurate.
+    The one-launch repair is taken when there are at least 16 query heads
+    and at most two misses per head are expected (a fixed rule, so the
+    choice is made on the host and a captured graph stays valid).  Either
+    repair returns the exact output over the selected set, whatever the
+    estimate.
     """
     if not 0 <= expected_miss_fraction <= 1:
         raise ValueError("expected_miss_fraction must be in [0, 1]")

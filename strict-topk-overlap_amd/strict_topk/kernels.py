@@ -67,17 +67,26 @@ def _args(q, k, v):
     return (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.dtype_code(q), q.shape[0], hkv, n, b, d)
 
 
+def _check_mask(mask, device, name):
+    """A mask is read by the kernels as one byte per entry on the device."""
+    if not isinstance(mask, torch.Tensor) or not mask.is_cuda or mask.device != device:
+        raise ValueError(f"{name} must be a tensor on the query's CUDA device")
+    if mask.dtype not in (torch.bool, torch.uint8, torch.int8):
+        raise ValueError(f"{name} must be a bool mask")
+
+
 def _allocate_state(h, s, d, device):
     m = torch.empty((h, s), device=device, dtype=torch.float32)
     return PartialState(m, torch.empty_like(m), torch.empty((h, s, d), device=device, dtype=torch.float32))
 
 
 def block_partials(q, k, v, ids, active=None):
-    """Each block's m, sum exp(logit-m), sum exp(logit-m)*V (all FP32)."""
+    """Per listed block: m = max logit, l = sum exp(logit - m), u = sum exp(logit - m) V."""
     h, n, b, d, s = _shape(q, k, v, ids)
     state = _allocate_state(h, s, d, q.device)
     kind = 0
     if active is not None:
+        _check_mask(active, q.device, "active")
         assert active.is_contiguous() and active.shape in ((h,), (h, s))
         kind = 1 if active.ndim == 1 else 2
         active = active.to(torch.bool) if active.dtype != torch.bool else active
@@ -89,6 +98,11 @@ def block_partials(q, k, v, ids, active=None):
 
 def merge_partials(state, include=None):
     h, s, d = state.u.shape
+    if include is not None:
+        _check_mask(include, state.u.device, "include")
+        if include.shape != (h, s) or not include.is_contiguous():
+            raise ValueError("include must be a contiguous [H, S] mask")
+        include = include.to(torch.bool) if include.dtype != torch.bool else include
     out = torch.empty((h, d), device=state.u.device, dtype=torch.float32)
     _lib.call("stk_merge_partials", _lib.ptr(state.m), _lib.ptr(state.l), _lib.ptr(state.u),
               _lib.ptr(include), h, s, d, _lib.ptr(out), _lib.stream(state.u.device))
@@ -96,7 +110,7 @@ def merge_partials(state, include=None):
 
 
 def exact_attention(q, k, v, selected):
-    """Split-block, selected-set baseline, with the same FP32 accumulation."""
+    """Serial baseline: attention over the selected blocks through per-block states."""
     h, n, b, d, s = _shape(q, k, v, selected)
     out = torch.empty((h, d), device=q.device, dtype=torch.float32)
     ws = _lib.workspace(_lib.size("stk_exact_workspace_bytes", h, s, d), q.device)
@@ -111,15 +125,16 @@ def compact_capacity(s, mass_threshold):
 
 
 def speculate(q, k, v, predicted, mode='saved', mass_threshold=0.1, *, keep_mass=False):
-    """Speculate using CURRENT Q. Threshold uses actual predicted-set mass.
+    """Prediction states for the predicted blocks, computed with this step's query.
 
+    The mass threshold is relative to the mass of the predicted set itself.
     saved: per-block states of the predicted blocks.  hybrid: additionally a
     per-block high/low split at ``mass_threshold`` of the predicted-set mass
     and one low aggregate (m, l, u) with its absolute envelope.  compact: a
     K-only mass pass, capacity-bounded retained states (IDs in rank order,
     padded with -1, overflow flag) and a low aggregate accumulated per token
-    in the low frame.  keep_mass exposes the FP32 block maxima and
-    normalizers in predicted-ID order.
+    in the low frame.  keep_mass: also return every predicted block's FP32
+    (m, l), in the order of the predicted row.
     """
     if mode not in ('saved', 'hybrid', 'compact'):
         raise ValueError(mode)
@@ -174,12 +189,15 @@ def prediction_args(prediction, q):
 
 
 def repair(q, k, v, selected, predicted, prediction, min_remaining=1.e-3, cancellation_tol=1.e-5):
-    """Restore exact selected-set semantics; conservative guards recompute QKV.
+    """Bring a prediction back to the exact output over the selected set.
 
-    Remaining is residual low-group denominator / original low denominator.
-    A wholly rejected low group is discarded directly without subtraction.
-    cancellation_tol checks each residual numerator coordinate against a
-    low-group absolute sum. This is a heuristic, not a forward-error certificate.
+    remaining = (low denominator after removing wrong blocks) / (low
+    denominator before).  A low group none of whose blocks is selected is
+    dropped whole, with no subtraction.  The cancellation guard compares
+    every coordinate of the remaining low numerator with the low group's
+    absolute sum times cancellation_tol; it is a rounding heuristic, not an
+    error bound.  Heads that fail a guard are recomputed over the selected
+    blocks directly.
     """
     h, n, b, d, sa = _shape(q, k, v, selected)
     sp = predicted.shape[1]
@@ -197,7 +215,8 @@ def repair(q, k, v, selected, predicted, prediction, min_remaining=1.e-3, cancel
 
 
 def touch_kv(k, v, predicted):
-    """Read predicted KV with a checksum side effect; cache residency not assured."""
+    """Stream the predicted blocks' K/V once, returning per-tile checksums (a
+    prefetch baseline; nothing guarantees the data stay cached)."""
     h, n, b, d = k.shape
     s = predicted.shape[1]
     nt = (b * d + 1023) // 1024

@@ -7,6 +7,11 @@ Wire format (one pool shared by a batch of requests of different lengths):
   block_table       [R, Hkv, NB]   int32 page of logical block j of (request r,
                                    KV head h), valid for j < nblocks[r]
   nblocks           [R] int32      blocks per request, on the device
+  ntokens           [R] int32      tokens per request, on the device (optional):
+                                   token t of block j holds data when
+                                   j * B + t < ntokens[r], so the last block
+                                   may be partly filled; its other tokens get
+                                   no weight, whatever the page holds there
 
 The reference reaches a paged cache only through FlashInfer's page table
 (``strict_topk/flashinfer_backend.py:35-40``: page = block + kv_head * N over
@@ -42,6 +47,7 @@ class PagedKV:
     hi_pages: torch.Tensor      # [P, D] float32
     block_table: torch.Tensor   # [R, Hkv, NB] int32
     nblocks: torch.Tensor       # [R] int32
+    ntokens: torch.Tensor | None = None   # [R] int32; None: every block full
 
     @property
     def requests(self):
@@ -68,13 +74,15 @@ class PagedKV:
         return self.k_pages.shape[2]
 
 
-def pack(caches, width=None, order=None, spare=0):
+def pack(caches, width=None, order=None, spare=0, tokens=None):
     """Pack dense per-request caches [(k, v), ...] (k, v: [Hkv, N_r, B, D])
     into one pool, building lo/hi pages on the device (``bounds.block_bounds``
     on the pool).  ``order``: an optional permutation of the pages (pages are
     placed in that order, to exercise the indirection); ``spare`` extra
     zeroed pages at the end of the pool; ``width``: the table's row width
-    (default: the longest request)."""
+    (default: the longest request); ``tokens``: each request's token count
+    ((N_r - 1) * B < tokens[r] <= N_r * B; default N_r * B), the bounds of a
+    partly filled last block taken over its tokens that hold data."""
     from .bounds import block_bounds
     if not caches:
         raise ValueError("expected at least one request")
@@ -84,6 +92,12 @@ def pack(caches, width=None, order=None, spare=0):
     for k, v in caches:
         if k.shape[0] != hkv or k.shape[2:] != (b, d) or v.shape != k.shape or k.dtype != k0.dtype:
             raise ValueError("every request needs K/V [Hkv, N_r, B, D] of one shape and dtype")
+    if tokens is None:
+        tokens = [n * b for n in counts]
+    tokens = [int(t) for t in tokens]
+    if len(tokens) != len(counts) or any(not (n - 1) * b < t <= n * b
+                                         for n, t in zip(counts, tokens)):
+        raise ValueError("tokens[r] must end inside request r's last block")
     width = max(counts) if width is None else int(width)
     if width < max(counts):
         raise ValueError("the table is narrower than the longest request")
@@ -104,18 +118,27 @@ def pack(caches, width=None, order=None, spare=0):
         table[r, :, :n] = idx.view(hkv, n).to(torch.int32).cpu()
         base += hkv * n
     lo, hi = block_bounds(k_pages.unsqueeze(0))
-    return PagedKV(k_pages, v_pages, lo[0], hi[0], table.to(dev),
-                   torch.tensor(counts, dtype=torch.int32, device=dev))
+    lo, hi = lo[0], hi[0]
+    for r, (n, t) in enumerate(zip(counts, tokens)):
+        part = t - (n - 1) * b
+        if part < b:
+            pages = table[r, :, n - 1].to(dev).long()
+            lo[pages] = k_pages[pages, :part].amin(1).float()
+            hi[pages] = k_pages[pages, :part].amax(1).float()
+    return PagedKV(k_pages, v_pages, lo, hi, table.to(dev),
+                   torch.tensor(counts, dtype=torch.int32, device=dev),
+                   torch.tensor(tokens, dtype=torch.int32, device=dev))
 
 
 def append(kv, k_new, v_new, positions):
     """Write one decode token per request in place: k_new, v_new [R, Hkv, D]
     at token position positions[r] (block pos // B, offset pos % B) of that
     block's page; the page's lo/hi are widened by the new key (offset 0 starts
-    them over) and nblocks[r] becomes pos // B + 1, in one launch.  positions
-    is an int32 tensor on the device, so a captured graph can advance it.  A
-    position outside [0, NB * B), or a block without a valid page, writes
-    nothing."""
+    them over), nblocks[r] becomes pos // B + 1 and ntokens[r] pos + 1, in
+    one launch.  positions is an int32 tensor on the device, so a captured
+    graph can advance it.  A position outside [0, NB * B) writes nothing; a
+    block without a valid page for some KV head writes nothing for that head
+    and leaves the counts unchanged."""
     if not isinstance(kv, PagedKV):
         raise TypeError("kv must be a PagedKV")
     shape = (kv.requests, kv.hkv, kv.dim)
@@ -125,16 +148,21 @@ def append(kv, k_new, v_new, positions):
         raise ValueError("expected int32 positions[R]")
     if k_new.dtype != kv.k_pages.dtype or v_new.dtype != kv.k_pages.dtype:
         raise ValueError("K_NEW/V_NEW must match the pages' dtype")
-    ts = (k_new, v_new, positions, kv.k_pages, kv.v_pages, kv.lo_pages, kv.hi_pages,
-          kv.block_table, kv.nblocks)
+    ts = [k_new, v_new, positions, kv.k_pages, kv.v_pages, kv.lo_pages, kv.hi_pages,
+          kv.block_table, kv.nblocks]
+    if kv.ntokens is not None:
+        ts.append(kv.ntokens)
     if not kv.k_pages.is_cuda or any(t.device != kv.k_pages.device or not t.is_contiguous()
                                      for t in ts):
         raise ValueError("all tensors must be contiguous and on one CUDA device")
+    if kv.ntokens is not None and (kv.ntokens.dtype != torch.int32 or
+                                   kv.ntokens.shape != (kv.requests,)):
+        raise ValueError("ntokens must be int32 [R]")
     _lib.call("stk_paged_append", _lib.ptr(k_new), _lib.ptr(v_new), _lib.dtype_code(k_new),
               kv.requests, kv.hkv, kv.width, kv.block, kv.dim, kv.pages, _lib.ptr(kv.k_pages),
               _lib.ptr(kv.v_pages), _lib.ptr(kv.lo_pages), _lib.ptr(kv.hi_pages),
-              _lib.ptr(kv.block_table), _lib.ptr(kv.nblocks), _lib.ptr(positions),
-              _lib.stream(k_new.device))
+              _lib.ptr(kv.block_table), _lib.ptr(kv.nblocks), _lib.ptr(kv.ntokens),
+              _lib.ptr(positions), _lib.stream(k_new.device))
     return kv
 
 
@@ -156,12 +184,17 @@ def _check(q, kv, predicted, topk):
         raise ValueError("lo and hi pages must be FP32")
     if kv.block_table.dtype != torch.int32 or kv.nblocks.dtype != torch.int32:
         raise ValueError("block_table and nblocks must be int32")
+    if kv.ntokens is not None and (kv.ntokens.dtype != torch.int32 or
+                                   kv.ntokens.shape != (kv.requests,)):
+        raise ValueError("ntokens must be int32 [R]")
     topk = int(topk)
     if not 1 <= topk <= 256:
         raise ValueError("topk must be in [1, 256]")
     ts = [q, kv.k_pages, kv.v_pages, kv.lo_pages, kv.hi_pages, kv.block_table, kv.nblocks]
     if predicted is not None:
         ts.append(predicted)
+    if kv.ntokens is not None:
+        ts.append(kv.ntokens)
     if not q.is_cuda or any(t.device != q.device or not t.is_contiguous() for t in ts):
         raise ValueError("all tensors must be contiguous and on one CUDA device")
     return r, hq, topk
@@ -183,8 +216,8 @@ def _common(q, kv, predicted, topk):
     ws = _lib.workspace(_lib.size("stk_paged_workspace_bytes", r, hq, kv.width), dev)
     head = (_lib.ptr(q), _lib.ptr(kv.k_pages), _lib.ptr(kv.v_pages), _lib.dtype_code(q), r, hq,
             kv.hkv, kv.width, kv.block, d, kv.pages, _lib.ptr(kv.lo_pages),
-            _lib.ptr(kv.hi_pages), _lib.ptr(kv.block_table), _lib.ptr(kv.nblocks), topk,
-            _lib.ptr(predicted), sp)
+            _lib.ptr(kv.hi_pages), _lib.ptr(kv.block_table), _lib.ptr(kv.nblocks),
+            _lib.ptr(kv.ntokens), topk, _lib.ptr(predicted), sp)
     st = (None, None, None) if state is None else (_lib.ptr(state.m), _lib.ptr(state.l),
                                                    _lib.ptr(state.u))
     return head, selected, state, st, out, ws

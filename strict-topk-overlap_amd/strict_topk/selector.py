@@ -1,4 +1,4 @@
-"""Fused min/max block scoring for the synthetic selector.
+"""Block selection by the query-sign min/max bound of every block's keys.
 
 Drop-in for the reference ``strict_topk/selector.py`` (same names, argument
 meaning and ValueError messages, :23-43).  Scores are evaluated in FP64 on the
@@ -26,7 +26,7 @@ def _check(q, lo, hi):
 
 
 def block_scores(q, lo, hi):
-    """Compute FP32 min/max bound scores for contiguous CUDA inputs."""
+    """scores[h, n] = sum_d q[h,d] * (hi if q[h,d] >= 0 else lo)[h,n,d], as FP32."""
     h, n, d = _check(q, lo, hi)
     scores = torch.empty((h, n), device=q.device, dtype=torch.float32)
     _lib.call("stk_block_scores", _lib.ptr(q), _lib.dtype_code(q), _lib.ptr(lo), _lib.ptr(hi),
@@ -35,7 +35,7 @@ def block_scores(q, lo, hi):
 
 
 def select_blocks(q, lo, hi, topk):
-    """Return the int32 block IDs of the top-k bound scores."""
+    """int32 [H, topk]: the blocks with the highest bound scores, per head."""
     h, n, d = _check(q, lo, hi)
     return select_ids(q, lo, hi, topk, h, h, n, d)
 

@@ -1,4 +1,4 @@
-"""Signed block correction with a shared low-group scale and inline fallback.
+"""Signed repair whose corrections share one launch and whose fallback is inline.
 
 Drop-in for the reference ``strict_topk/signed_fused.py``
 (``repair_signed_fused`` :148-193): three launches — job schedule, one
@@ -11,10 +11,9 @@ from .signed_repair import SignedRepairResult, _signed  # noqa: F401
 
 def repair_signed_fused(q, k, v, selected, predicted, prediction, min_remaining=1.e-3,
                         cancellation_tol=1.e-5, max_extra_mass=0.):
-    """One shared add/erase KV kernel, followed by guarded finalization.
-
-    Uses three launches: queue metadata; parallel signed KV computation;
-    output merge and optional strict fallback.
-    """
+    """Repair by signed block corrections, in three launches: the job
+    schedule, the added (missed) and subtracted (wrong low) blocks' states in
+    one parallel kernel, then the guarded merge, which also recomputes the
+    strict selected set for heads whose guards fail."""
     return _signed(q, k, v, selected, predicted, prediction, min_remaining, cancellation_tol,
                    max_extra_mass, True, "max_extra_mass must be in [0,1]")

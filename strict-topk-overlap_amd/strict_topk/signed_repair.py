@@ -1,4 +1,4 @@
-"""Parallel signed corrections for saved, hybrid and compact prediction states.
+"""Signed repair of saved, hybrid or compact predictions, corrections in parallel.
 
 Drop-in for the reference ``strict_topk/signed_repair.py``
 (``SignedRepairResult`` :12-15, ``repair_signed`` :175-232): schedule a
@@ -55,12 +55,14 @@ def _signed(q, k, v, selected, predicted, prediction, min_remaining, cancellatio
 
 def repair_signed(q, k, v, selected, predicted, prediction, min_remaining=1.e-3,
                   cancellation_tol=1.e-5, max_extra_mass=0.):
-    """Repair using one parallel partials kernel for both signs of correction.
+    """Signed repair in four launches (schedule, corrections, merge, fallback).
 
-    The queue packs missed selected blocks first and then wrong low blocks.
-    A guarded merge evaluates the subtraction in the original low exponent
-    frame. The fallback recomputes the strict selected set on flagged heads.
-    Positive and total job counts describe the correction queue before fallback.
+    Each head's job list holds its missed selected blocks, then its wrong
+    low blocks; one kernel computes every job's state.  The merge removes
+    the subtracted states in the low group's exponent frame under the
+    guards, and heads that fail a guard are recomputed over the selected set
+    alone.  positive_jobs / total_jobs count the list as scheduled, before
+    any fallback.
     """
     return _signed(q, k, v, selected, predicted, prediction, min_remaining, cancellation_tol,
                    max_extra_mass, False, "max_extra_mass must be in [0, 1]")

@@ -385,8 +385,9 @@ def test_gqa_paths(hq):
     (8, 8, 400, 16, 128, 24, 24, 12, torch.bfloat16),     # G = 1, one 16-token chunk
 ])
 def test_gqa_states_and_repair_shapes(hq, hkv, n, b, d, sa, sp, hits, dtype):
-    """Deduplicated GQA states (one tile read per KV group) and the
-    single-launch saved / union / light repair against the oracle."""
+    """GQA states (one wave per (query head, slot); heads of a KV group that
+    list the same block each read its tile) and the single-launch saved /
+    union / light repair against the oracle."""
     from strict_topk import gqa, gqa_light
     gen = torch.Generator().manual_seed(hq * 7 + n)
     q = torch.randn((hq, d), generator=gen).to(dtype)
@@ -958,3 +959,159 @@ def test_poisoned_workspace(monkeypatch):
     res = paged.speculative_step(q, kv, p, 20)
     assert torch.isfinite(res.output).all()
     assert torch.equal(res.selected, sel)
+
+
+def _poisoned_caches(hq, hkv, b, d, counts, tokens, dtype, seed, hot_last=True):
+    """Per request q, k, v with every token at or past its token count set to
+    NaN (so any weight on such a token would show), the partly filled last
+    block's live keys pointed along the query so that it ranks high."""
+    from stk_harness.configs import make_qkv
+    out = []
+    for r, (n, t) in enumerate(zip(counts, tokens)):
+        q, k, v, _, _ = make_qkv(hq, hkv, d, b, n, dtype, True, seed + 31 * r)
+        part = t - (n - 1) * b
+        if hot_last:
+            qm = q.float().view(hkv, hq // hkv, d).mean(1)
+            k[:, n - 1, :part] = (k[:, n - 1, :part].float() +
+                                  60.0 * (qm / qm.norm(dim=-1, keepdim=True))[:, None]).to(dtype)
+        k[:, n - 1, part:] = float("nan")
+        v[:, n - 1, part:] = float("nan")
+        out.append((q, k, v, n, t))
+    return out
+
+
+def test_paged_partial_last_block():
+    """A request whose last block is partly filled (ntokens): the tokens past
+    its count hold NaN and must get no weight anywhere -- the pool's bounds,
+    the selection, the predicted states (the last block is a hit for some
+    heads and a miss for others), the serial path, the saved step and the
+    strict signed step all match the oracle restricted to the live tokens."""
+    from strict_topk import paged
+    hq, hkv, b, d, topk, sp = 8, 2, 32, 128, 16, 16
+    counts = (60, 20, 130)
+    tokens = (59 * 32 + 5, 19 * 32 + 31, 129 * 32 + 1)
+    reqs = _poisoned_caches(hq, hkv, b, d, counts, tokens, torch.bfloat16, 20261301)
+    order = torch.randperm(hkv * sum(counts), generator=torch.Generator().manual_seed(3))
+    kv = paged.pack([(k.to(DEV), v.to(DEV)) for _, k, v, _, _ in reqs], order=order, spare=2,
+                    tokens=tokens)
+    assert kv.ntokens.cpu().tolist() == list(tokens)
+    gen = torch.Generator().manual_seed(8)
+    preds = []
+    for _, _, _, n, _ in reqs:
+        rows = []
+        for h in range(hq):
+            row = torch.randperm(n - 1, generator=gen)[:sp - 1]
+            # the partial block predicted for even heads only
+            extra = n - 1 if h % 2 == 0 else int(torch.randperm(n - 1, generator=gen)[0])
+            while h % 2 and extra in row.tolist():
+                extra = (extra + 1) % (n - 1)
+            rows.append(torch.cat([row, torch.tensor([extra])]))
+        preds.append(torch.stack(rows).to(torch.int32))
+    q = torch.stack([r[0] for r in reqs]).to(DEV)
+    p = torch.stack(preds).to(DEV)
+    lo_p, hi_p = (t.cpu().numpy() for t in (kv.lo_pages, kv.hi_pages))
+    tab, nbk = kv.block_table.cpu().numpy(), kv.nblocks.cpu().numpy()
+    sel_x, out_x = paged.exact(q, kv, topk)
+    res = paged.speculative_step(q, kv, p, topk)
+    sres = paged.speculative_signed_step(q, kv, p, topk, "hybrid", 0.2)
+    torch.cuda.synchronize()
+    for r, (qh, k, v, n, t) in enumerate(reqs):
+        qn, kn, vn = np_(qh, k, v)
+        part = t - (n - 1) * b
+        for h in range(hkv):
+            page = int(tab[r, h, n - 1])
+            np.testing.assert_array_equal(lo_p[page], kn[h, n - 1, :part].min(0))
+            np.testing.assert_array_equal(hi_p[page], kn[h, n - 1, :part].max(0))
+        ids = O.paged_select(qn, lo_p, hi_p, tab, nbk, r, topk)
+        assert (ids == n - 1).any(), "the partial block should be selected somewhere"
+        expected = O.attention(qn, kn, vn, ids, tokens=t)
+        assert sel_x[r].cpu().numpy().tolist() == ids.tolist(), r
+        assert res.selected[r].cpu().numpy().tolist() == ids.tolist(), r
+        check(out_x[r], expected, ("paged exact, partial block", r))
+        check(res.output[r], expected, ("paged step, partial block", r))
+        check(sres.result.output[r], expected, ("paged signed strict, partial block", r))
+        st = O.block_states(qn, kn, vn, C.ids_np(preds[r]), tokens=t)
+        np.testing.assert_allclose(res.state.m[r].cpu().double().numpy(), st.m, rtol=1e-5,
+                                   atol=1e-5)
+        np.testing.assert_allclose(res.state.l[r].cpu().double().numpy(), st.l, rtol=1e-4,
+                                   atol=1e-5)
+        np.testing.assert_allclose(res.state.u[r].cpu().double().numpy(), st.u, rtol=1e-4,
+                                   atol=1e-4)
+
+
+def test_paged_append_then_step_on_a_partial_block():
+    """Decode loop: append six tokens into a fresh last block (the rest of its
+    page holds NaN), then run the serial path and the saved step: both equal
+    the oracle over the live tokens, and the counts say six tokens."""
+    from strict_topk import paged
+    hq, hkv, b, d, topk = 4, 2, 16, 64, 8
+    counts = (40, 12)
+    gen = torch.Generator().manual_seed(21)
+    full = [(torch.randn((hkv, n, b, d), generator=gen).half(),
+             torch.randn((hkv, n, b, d), generator=gen).half()) for n in counts]
+    q = torch.randn((len(counts), hq, d), generator=gen).half()
+    part = []
+    for k, v in full:
+        k2, v2 = k.clone(), v.clone()
+        k2[:, -1] = float("nan")
+        v2[:, -1] = float("nan")
+        part.append((k2.to(DEV), v2.to(DEV)))
+    kv = paged.pack(part)
+    kv.nblocks.sub_(1)
+    kv.ntokens.copy_(kv.nblocks * b)
+    kn_ = torch.empty((len(counts), hkv, d), dtype=torch.float16, device=DEV)
+    vn_ = torch.empty_like(kn_)
+    live = 6
+    for t in range(live):
+        kn_.copy_(torch.stack([k[:, -1, t] for k, _ in full]))
+        vn_.copy_(torch.stack([v[:, -1, t] for _, v in full]))
+        pos = torch.tensor([(n - 1) * b + t for n in counts], dtype=torch.int32, device=DEV)
+        paged.append(kv, kn_, vn_, pos)
+    torch.cuda.synchronize()
+    assert kv.nblocks.cpu().tolist() == list(counts)
+    assert kv.ntokens.cpu().tolist() == [(n - 1) * b + live for n in counts]
+    lo_p, hi_p = (t.cpu().numpy() for t in (kv.lo_pages, kv.hi_pages))
+    tab, nbk = kv.block_table.cpu().numpy(), kv.nblocks.cpu().numpy()
+    qd = q.to(DEV)
+    p = torch.stack([torch.stack([torch.randperm(n, generator=gen)[:topk] for _ in range(hq)])
+                     for n in (min(counts),) * len(counts)]).to(torch.int32)
+    p[:, 0, 0] = torch.tensor([n - 1 for n in counts], dtype=torch.int32)   # predicted partial
+    p[:, 0, 1:] = torch.arange(1, topk, dtype=torch.int32)
+    sel, out = paged.exact(qd, kv, topk)
+    res = paged.speculative_step(qd, kv, p.to(DEV), topk)
+    torch.cuda.synchronize()
+    for r, (k, v) in enumerate(full):
+        n = counts[r]
+        tok = (n - 1) * b + live
+        qn = C.f64(q[r])
+        kn, vn = C.f64(k), C.f64(v)
+        ids = O.paged_select(qn, lo_p, hi_p, tab, nbk, r, topk)
+        expected = O.attention(qn, kn, vn, ids, tokens=tok)
+        assert sel[r].cpu().numpy().tolist() == ids.tolist()
+        assert res.selected[r].cpu().numpy().tolist() == ids.tolist()
+        check(out[r], expected, ("append then exact", r))
+        check(res.output[r], expected, ("append then step", r))
+
+
+def test_masks_and_bounds_reject_host_tensors():
+    """Masks and bound arrays that are not on the query's device (or not
+    contiguous) are rejected before any launch."""
+    from strict_topk import bounds, kernels
+    gen = torch.Generator().manual_seed(2)
+    q = torch.randn((2, 64), generator=gen).half().to(DEV)
+    k = torch.randn((2, 6, 16, 64), generator=gen).half().to(DEV)
+    ids = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32, device=DEV)
+    with pytest.raises(ValueError, match="active"):
+        kernels.block_partials(q, k, k, ids, active=torch.ones((2,), dtype=torch.bool))
+    st = kernels.block_partials(q, k, k, ids)
+    with pytest.raises(ValueError, match="include"):
+        kernels.merge_partials(st, include=torch.ones((2, 2), dtype=torch.bool))
+    with pytest.raises(ValueError, match="include"):
+        kernels.merge_partials(st, include=torch.ones((2, 4), dtype=torch.bool,
+                                                      device=DEV)[:, ::2])
+    lo, hi = bounds.block_bounds(k)
+    with pytest.raises(ValueError, match="lo and hi"):
+        bounds.append(lo.cpu(), hi.cpu(), k[:, 0, 0].contiguous(), 0, 0)
+    with pytest.raises(ValueError, match="lo and hi"):
+        bounds.append(lo.transpose(0, 1).contiguous().transpose(0, 1), hi,
+                      k[:, 0, 0].contiguous(), 0, 0)

@@ -89,3 +89,32 @@ def test_paged_api_validates_on_the_host():
         paged.append(kv, kn, kn, torch.zeros((r,), dtype=torch.int32))
     with pytest.raises(ValueError, match="narrower"):
         paged.pack([(torch.zeros((hkv, 6, b, d)), torch.zeros((hkv, 6, b, d)))], width=3)
+
+
+def test_masks_and_token_counts_validate_on_the_host():
+    """Masks and token counts are checked before any launch: a mask that is
+    not on the CUDA device, a token count that does not end inside the last
+    block, an ntokens tensor of the wrong dtype."""
+    import sys
+    import pytest
+    import torch
+    sys.path.insert(0, str(ROOT / "strict-topk-overlap_amd"))
+    from strict_topk import kernels, paged
+    st = kernels.PartialState(torch.zeros((2, 3)), torch.zeros((2, 3)), torch.zeros((2, 3, 8)))
+    with pytest.raises(ValueError, match="include"):
+        kernels.merge_partials(st, include=torch.ones((2, 3), dtype=torch.bool))
+    k = torch.zeros((2, 3, 4, 8))
+    with pytest.raises(ValueError, match="tokens"):
+        paged.pack([(k, k)], tokens=[8])        # 3 blocks of 4: tokens must be in (8, 12]
+    with pytest.raises(ValueError, match="tokens"):
+        paged.pack([(k, k)], tokens=[13])
+    r, hkv, nb, b, d, pages = 2, 2, 5, 4, 64, 30
+    kv = paged.PagedKV(torch.zeros((pages, b, d), dtype=torch.bfloat16),
+                       torch.zeros((pages, b, d), dtype=torch.bfloat16),
+                       torch.zeros((pages, d)), torch.zeros((pages, d)),
+                       torch.zeros((r, hkv, nb), dtype=torch.int32),
+                       torch.full((r,), nb, dtype=torch.int32),
+                       torch.full((r,), nb * b, dtype=torch.int64))
+    q = torch.zeros((r, 4, d), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ntokens"):
+        paged.exact(q, kv, 2)

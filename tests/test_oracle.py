@@ -364,3 +364,41 @@ def test_paged_gather_and_select_pinned():
         bad = inv[h // g]
         order = sorted((j for j in range(14) if not bad[j]), key=lambda j: (-sc[h, j], j))[:6]
         assert got[h].tolist() == sorted(order)
+
+
+def test_token_count_mask_pinned_by_brute_force():
+    """attention / block_states with a token count (a partly filled last
+    block) equal a token-by-token softmax over exactly the tokens before the
+    count, in plain Python; values past the count (NaN here) are ignored;
+    with the count at N * B nothing changes."""
+    rng = np.random.default_rng(11)
+    hkv, g, n, b, d = 2, 2, 5, 4, 3
+    q = rng.standard_normal((hkv * g, d))
+    k = rng.standard_normal((hkv, n, b, d))
+    v = rng.standard_normal((hkv, n, b, d))
+    ids = np.array([[4, 0, 2], [1, 4, 3], [4, 2, 0], [3, 1, 4]])
+    full = O.attention(q, k, v, ids)
+    np.testing.assert_array_equal(O.attention(q, k, v, ids, tokens=n * b), full)
+    for tokens in (4 * b + 1, 4 * b + 3, 3 * b + 2):
+        kp, vp = k.copy(), v.copy()
+        tail = np.arange(n * b).reshape(n, b) >= tokens
+        kp[:, tail] = np.nan
+        vp[:, tail] = np.nan
+        got = O.attention(q, kp, vp, ids, tokens=tokens)
+        st = O.block_states(q, kp, vp, ids, tokens=tokens)
+        for h in range(hkv * g):
+            toks = [(blk, t) for blk in ids[h] for t in range(b) if blk * b + t < tokens]
+            logits = [float(np.dot(k[h // g, blk, t], q[h])) / math.sqrt(d) for blk, t in toks]
+            mx = max(logits)
+            w = [math.exp(x - mx) for x in logits]
+            want = sum(wi * v[h // g, blk, t] for wi, (blk, t) in zip(w, toks)) / sum(w)
+            np.testing.assert_allclose(got[h], want, rtol=1e-12, atol=1e-12)
+            for j, blk in enumerate(ids[h]):
+                live = [t for t in range(b) if blk * b + t < tokens]
+                if not live:
+                    assert st.m[h, j] == -np.inf and st.l[h, j] == 0 and not st.u[h, j].any()
+                    continue
+                s = [float(np.dot(k[h // g, blk, t], q[h])) / math.sqrt(d) for t in live]
+                mm = max(s)
+                assert st.m[h, j] == pytest.approx(mm, abs=1e-12)
+                assert st.l[h, j] == pytest.approx(sum(math.exp(x - mm) for x in s), rel=1e-12)
