@@ -255,6 +255,25 @@ int stk_speculative_step(const void* q, const void* k, const void* v, int dtype,
                          int32_t* selected, float* m, float* l, float* u, float* out,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of stk_speculative_step.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, results and shape support as stk_speculative_step, without the
+ * workspace: the score keys live in a fixed array of device memory inside the
+ * library, one per GPU (4 MiB, held until the process ends), so Hq * N may
+ * not exceed stk_step_noalloc_max_keys() (524288); larger shapes return
+ * STK_EINVAL.  The call allocates nothing, not even on its first use on a
+ * device (it then only looks up the array's address).  Calls on one GPU share
+ * the array: calls that overlap in time on one GPU (on concurrent streams)
+ * race and must be ordered by the caller. */
+size_t stk_step_noalloc_max_keys(void);
+
+int stk_speculative_step_noalloc(const void* q, const void* k, const void* v, int dtype, int hq,
+                                 int hkv, int n, int b, int d, const float* lo, const float* hi,
+                                 int topk, const void* predicted, int pred_dtype, int sp,
+                                 int union_mode, int32_t* selected, float* m, float* l, float* u,
+                                 float* out, void* stream);
+
 /* The two launches of stk_speculative_step separately.  stk_step_front
  * (select || speculate) writes the prediction state and the score keys into
  * `workspace`; stk_step_tail (top-K + repair) reads them from the same

@@ -17,6 +17,8 @@
 //                  blocks' tiles).
 // The arithmetic is that of stk_select_blocks, stk_block_partials and
 // stk_gqa_repair; results are identical up to FP32 reduction order.
+#include <mutex>
+
 #include "step_launch.hpp"
 
 namespace stk {
@@ -132,6 +134,75 @@ STK_API int stk_speculative_step(const void* q, const void* k, const void* v, in
   return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, topk, predicted, pred_dtype, sp,
                    union_mode, selected, m, l, u, out, workspace, workspace_bytes, stream, true,
                    true);
+}
+
+// ---- the allocation-free variant of stk_speculative_step
+//
+// Its score keys live in `scratch`, one array per GPU, sized for
+// hq * n <= kNoAllocMaxKeys (4 MiB).  In host code `scratch` names a host-side
+// stand-in, never the device copy: the device address comes from
+// hipGetSymbolAddress, once per device with that device current, and only
+// that address is passed to kernels.  Every call on one GPU shares the array
+// and the last call's keys stay in it; the front writes every key the tail
+// reads (keys [h, 0, n) of each head), so nothing needs clearing.  Calls that
+// overlap on one GPU (two streams at once) race on it.
+constexpr size_t kNoAllocMaxKeys = (size_t)1 << 19;
+static __device__ __align__(256) uint64_t scratch[kNoAllocMaxKeys];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kMaxDevices];
+
+// The device address of `scratch` on the device that runs `stream`.
+static int scratch_address(hipStream_t stream, void** out) {
+  hipDevice_t dev = 0;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) {
+    stk_set_error("hipStreamGetDevice failed: %s", hipGetErrorString(e));
+    return STK_EHIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    stk_set_error("device ordinal %d out of range", (int)dev);
+    return STK_EINVAL;
+  }
+  std::lock_guard<std::mutex> guard(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t restore = cur != dev ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess || restore != hipSuccess || !p) {
+      stk_set_error("scratch address on device %d: %s", (int)dev,
+                    hipGetErrorString(e != hipSuccess ? e : restore));
+      return STK_EHIP;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return STK_OK;
+}
+
+STK_API size_t stk_step_noalloc_max_keys(void) { return kNoAllocMaxKeys; }
+
+STK_API int stk_speculative_step_noalloc(const void* q, const void* k, const void* v, int dtype,
+                                         int hq, int hkv, int n, int b, int d, const float* lo,
+                                         const float* hi, int topk, const void* predicted,
+                                         int pred_dtype, int sp, int union_mode,
+                                         int32_t* selected, float* m, float* l, float* u,
+                                         float* out, void* stream) {
+  STK_REQUIRE(stk_check_kv(dtype, hq, hkv, n, b, d));
+  STK_REQUIRE(q && k && v && lo && hi && predicted && selected && m && l && u && out,
+              "null pointer");
+  STK_REQUIRE((size_t)hq * (size_t)n <= kNoAllocMaxKeys,
+              "the allocation-free step holds at most 524288 score keys (Hq * N)");
+  void* ws = nullptr;
+  const int rc = scratch_address((hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, topk, predicted, pred_dtype, sp,
+                   union_mode, selected, m, l, u, out, ws, kNoAllocMaxKeys * sizeof(uint64_t),
+                   stream, true, true);
 }
 
 STK_API int stk_step_front(const void* q, const void* k, const void* v, int dtype, int hq,

@@ -59,6 +59,9 @@ _SIGS = {
     "stk_step_supported": (I, [I, I, I, I, I, I, I, I, I]),
     "stk_speculative_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I,
                                  P, P, P, P, P, P, Z, P]),
+    "stk_step_noalloc_max_keys": (Z, []),
+    "stk_speculative_step_noalloc": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I,
+                                         P, P, P, P, P, P]),
     "stk_step_front": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, P, P, P, P, Z, P]),
     "stk_step_tail": (I, [P, P, P, I, I, I, I, I, I, I, P, I, I, I, P, P, P, P, P, P, Z, P]),
     "stk_indexer_workspace_bytes": (Z, [I]),

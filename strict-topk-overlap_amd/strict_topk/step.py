@@ -82,6 +82,34 @@ def speculative_step(q, k, v, lo, hi, predicted, topk, union=False):
     return StepResult(selected, state, out)
 
 
+def speculative_step_noalloc(q, k, v, lo, hi, predicted, topk, union=False, into=None):
+    """``speculative_step`` for callers that cannot allocate device memory
+    (graph capture, serving loops): the library keeps the step's scratch in a
+    fixed per-GPU array, so the call allocates nothing.  ``into``: an
+    optional ``StepResult`` whose tensors receive the results (else they are
+    allocated here, before the call).  Only shapes the fused kernels support
+    with Hq * N <= 524288 are accepted (ValueError otherwise).  Calls that
+    overlap in time on one GPU share the array and must not run
+    concurrently."""
+    gqa._shape(q, k, v, predicted)
+    topk = int(topk)
+    hq, d = q.shape
+    hkv, n, b, _ = k.shape
+    sp = predicted.shape[1]
+    if not supported(q, k, lo, topk, predicted):
+        raise ValueError("shape not supported by the fused step")
+    dev = q.device
+    if into is None:
+        into = StepResult(torch.empty((hq, topk), device=dev, dtype=torch.int32),
+                          _allocate_state(hq, sp, d, dev),
+                          torch.empty((hq, d), device=dev, dtype=torch.float32))
+    _lib.call("stk_speculative_step_noalloc", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi), topk,
+              _lib.ptr(predicted), _lib.id_code(predicted), sp, 1 if union else 0,
+              _lib.ptr(into.selected), _lib.ptr(into.state.m), _lib.ptr(into.state.l),
+              _lib.ptr(into.state.u), _lib.ptr(into.output), _lib.stream(dev))
+    return into
+
+
 @dataclass
 class SignedStepResult:
     selected: torch.Tensor     # int32 [Hq, topk], ascending block IDs
