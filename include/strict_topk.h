@@ -19,6 +19,12 @@
  *   - `stream` is a hipStream_t.  Every call only enqueues work on it: no
  *     allocation, no host synchronisation, no copy to the host, so calls can
  *     be captured into a HIP graph and issued on concurrent streams.
+ *   - Bounds lo/hi (and lo/hi pages) are float32, or, where an entry point
+ *     takes `bounds_dtype`, optionally stored in the keys' own 16-bit type
+ *     (bounds_dtype = dtype): the min / max of 16-bit keys are 16-bit values,
+ *     so that storage is exact, scores and selections are the same bits, and
+ *     the scorer reads half the bytes.  bounds_dtype = STK_F32 is the
+ *     reference's layout.
  *   - Scratch memory beyond inputs and outputs is the caller's `workspace`
  *     of at least the size the matching *_workspace_bytes() returns.
  *   - ID values are not validated on the device; an ID outside [0, N)
@@ -50,8 +56,9 @@ int stk_abi_version(void);
 /* strict_topk/selector.py:23-38 block_scores (and gqa.py:15-26 scoring):
  * scores[h,n] = sum_d q_d * (q_d >= 0 ? hi : lo)[h/G, n, d], evaluated in
  * float64 in a fixed order, stored as float32. */
-int stk_block_scores(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
-                     int hkv, int n, int d, float* scores, void* stream);
+int stk_block_scores(const void* q, int q_dtype, const void* lo, const void* hi,
+                     int bounds_dtype, int hq, int hkv, int n, int d, float* scores,
+                     void* stream);
 
 size_t stk_select_workspace_bytes(int hq, int hkv, int n, int d, int topk);
 
@@ -59,9 +66,9 @@ size_t stk_select_workspace_bytes(int hq, int hkv, int n, int d, int topk);
  * select_blocks (score + torch.topk(sorted=False)): ids[h, 0..topk) are the
  * topk highest-scoring blocks, ties toward the lower block index, in
  * ascending block order.  `scores` may be NULL. */
-int stk_select_blocks(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
-                      int hkv, int n, int d, int topk, float* scores, int32_t* ids,
-                      void* workspace, size_t workspace_bytes, void* stream);
+int stk_select_blocks(const void* q, int q_dtype, const void* lo, const void* hi,
+                      int bounds_dtype, int hq, int hkv, int n, int d, int topk, float* scores,
+                      int32_t* ids, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------- states and merge */
 
@@ -221,16 +228,17 @@ int stk_indexer_select(const void* iq, const void* ik, int dtype, int h, int n, 
  * per-dim minimum / maximum of k[Hkv, N, B, D] over the B tokens, as the
  * reference harness builds them with k.amin(dim=2).float() / k.amax(dim=2)
  * (benchmarks/critical_path.py:186, benchmarks/run_benchmark.py:43).  NaN
- * keys give NaN bounds, as torch does.  k: fp32 / fp16 / bf16. */
-int stk_block_bounds(const void* k, int dtype, int hkv, int n, int b, int d, float* lo,
-                     float* hi, void* stream);
+ * keys give NaN bounds, as torch does.  k: fp32 / fp16 / bf16; bounds_dtype:
+ * STK_F32, or the 16-bit dtype of k (exact, half the bytes). */
+int stk_block_bounds(const void* k, int dtype, int hkv, int n, int b, int d, void* lo, void* hi,
+                     int bounds_dtype, void* stream);
 
 /* Decode append: the token k_new[Hkv, D] lands at position `pos` of block
  * `block`; pos 0 starts the block's bounds over, otherwise they widen.  The
  * reference has no counterpart (its harness rebuilds lo/hi outside timing);
  * this is the per-token update a decode loop needs. */
 int stk_bounds_append(const void* k_new, int dtype, int hkv, int n, int d, int block, int pos,
-                      float* lo, float* hi, void* stream);
+                      void* lo, void* hi, int bounds_dtype, void* stream);
 
 /* ------------------------------------------------------- fused decode step */
 
@@ -250,10 +258,10 @@ int stk_step_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk
  * prediction state m,l[Hq,sp], u[Hq,sp,D] (as stk_block_partials) and
  * out[Hq,D].  bf16/fp16 only, int32 predicted IDs, D in {64, 128, 256}. */
 int stk_speculative_step(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
-                         int n, int b, int d, const float* lo, const float* hi, int topk,
-                         const void* predicted, int pred_dtype, int sp, int union_mode,
-                         int32_t* selected, float* m, float* l, float* u, float* out,
-                         void* workspace, size_t workspace_bytes, void* stream);
+                         int n, int b, int d, const void* lo, const void* hi, int bounds_dtype,
+                         int topk, const void* predicted, int pred_dtype, int sp,
+                         int union_mode, int32_t* selected, float* m, float* l, float* u,
+                         float* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Allocation-free variant of stk_speculative_step.  It has no counterpart in
  * the reference: it is for callers that cannot allocate (code under HIP graph
@@ -269,17 +277,17 @@ int stk_speculative_step(const void* q, const void* k, const void* v, int dtype,
 size_t stk_step_noalloc_max_keys(void);
 
 int stk_speculative_step_noalloc(const void* q, const void* k, const void* v, int dtype, int hq,
-                                 int hkv, int n, int b, int d, const float* lo, const float* hi,
-                                 int topk, const void* predicted, int pred_dtype, int sp,
-                                 int union_mode, int32_t* selected, float* m, float* l, float* u,
-                                 float* out, void* stream);
+                                 int hkv, int n, int b, int d, const void* lo, const void* hi,
+                                 int bounds_dtype, int topk, const void* predicted,
+                                 int pred_dtype, int sp, int union_mode, int32_t* selected,
+                                 float* m, float* l, float* u, float* out, void* stream);
 
 /* The two launches of stk_speculative_step separately.  stk_step_front
  * (select || speculate) writes the prediction state and the score keys into
  * `workspace`; stk_step_tail (top-K + repair) reads them from the same
  * workspace and writes `selected` and `out`. */
 int stk_step_front(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
-                   int b, int d, const float* lo, const float* hi, int topk,
+                   int b, int d, const void* lo, const void* hi, int bounds_dtype, int topk,
                    const void* predicted, int pred_dtype, int sp, float* m, float* l, float* u,
                    void* workspace, size_t workspace_bytes, void* stream);
 
@@ -304,7 +312,8 @@ int stk_step_tail(const void* q, const void* k, const void* v, int dtype, int hq
  * Supported shapes are those of stk_step_supported; the workspace is
  * stk_step_workspace_bytes. */
 int stk_signed_step(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
-                    int n, int b, int d, const float* lo, const float* hi, int topk,
+                    int n, int b, int d, const void* lo, const void* hi, int bounds_dtype,
+                    int topk,
                     const void* predicted, int pred_dtype, int sp, int hybrid,
                     float mass_threshold, float min_remaining, float cancellation_tol,
                     float max_extra_mass, int32_t* selected, float* m, float* l, float* u,
@@ -318,7 +327,8 @@ int stk_signed_step(const void* q, const void* k, const void* v, int dtype, int 
  * request per FlashInfer call) with a native wire format shared by a whole
  * batch of R requests:
  *   k_pages, v_pages [pages, B, D]   one page = one KV head's block of B tokens
- *   lo_pages, hi_pages [pages, D]    FP32 per-dim key min / max of the page
+ *   lo_pages, hi_pages [pages, D]    per-dim key min / max of the page, FP32
+ *                                    or the pages' 16-bit type (bounds_dtype)
  *                                    (stk_block_bounds on the pool as
  *                                    hkv = 1, n = pages)
  *   block_table [R, Hkv, nb] int32   page of logical block j of (request r,
@@ -354,14 +364,16 @@ size_t stk_paged_workspace_bytes(int requests, int hq, int nb);
  * the paged form of stk_bounds_append plus the K/V write. */
 int stk_paged_append(const void* k_new, const void* v_new, int dtype, int requests, int hkv,
                      int nb, int b, int d, int pages, void* k_pages, void* v_pages,
-                     float* lo_pages, float* hi_pages, const int32_t* block_table,
+                     void* lo_pages, void* hi_pages, int bounds_dtype,
+                     const int32_t* block_table,
                      int32_t* nblocks, int32_t* ntokens, const int32_t* positions,
                      void* stream);
 
 /* stk_speculative_step over a paged batch (union_mode: repair_union). */
 int stk_paged_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
                    int requests, int hq, int hkv, int nb, int b, int d, int pages,
-                   const float* lo_pages, const float* hi_pages, const int32_t* block_table,
+                   const void* lo_pages, const void* hi_pages, int bounds_dtype,
+                   const int32_t* block_table,
                    const int32_t* nblocks, const int32_t* ntokens, int topk,
                    const int32_t* predicted, int sp, int union_mode, int32_t* selected, float* m,
                    float* l, float* u, float* out, void* workspace, size_t workspace_bytes,
@@ -370,7 +382,7 @@ int stk_paged_step(const void* q, const void* k_pages, const void* v_pages, int 
 /* stk_signed_step over a paged batch. */
 int stk_paged_signed_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
                           int requests, int hq, int hkv, int nb, int b, int d, int pages,
-                          const float* lo_pages, const float* hi_pages,
+                          const void* lo_pages, const void* hi_pages, int bounds_dtype,
                           const int32_t* block_table, const int32_t* nblocks,
                           const int32_t* ntokens, int topk, const int32_t* predicted, int sp,
                           int hybrid, float mass_threshold,

@@ -64,6 +64,11 @@ int stk_launch_states_skip(const void* q, const void* k, const void* v, int dtyp
 int stk_launch_merge(const float* m, const float* l, const float* u, const uint8_t* inc, int h,
                      int s, int d, float* out, hipStream_t st);
 
-int stk_launch_score(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
+// lo / hi element type: STK_F32, or the keys' own 16-bit type (lb = 1).
+inline bool stk_bounds_ok(int dtype, int bounds_dtype) {
+  return bounds_dtype == 0 || (bounds_dtype == dtype && dtype != 0);
+}
+
+int stk_launch_score(const void* q, int q_dtype, const void* lo, const void* hi, int lb, int hq,
                      int hkv, int n, int d, float* scores, uint64_t* keys, hipStream_t st);
 int stk_launch_topk(const uint64_t* keys, int rows, int n, int k, int32_t* ids, hipStream_t st);

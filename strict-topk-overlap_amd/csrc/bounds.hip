@@ -11,7 +11,9 @@
 // k_bounds_cols (16-bit keys, 16-byte aligned rows): one thread per (block,
 // 16-byte column); k_bounds (unaligned lo/hi): one workgroup per block, token
 // groups folded through LDS; k_bounds_any: every other case.  HBM-bound:
-// B * D * e bytes read and 8 * D bytes written per block.
+// B * D * e bytes read and 8 * D bytes written per block (4 * D with lb:
+// the bounds stored in the keys' own 16-bit type, exact since they are
+// values of that type).
 #include "common.hpp"
 #include "api.hpp"
 
@@ -21,12 +23,44 @@ struct BoundsArgs {
   const void* k; int dtype;
   int rows;          // hkv * n blocks
   int b, d;
-  float* lo; float* hi;
+  void* lo; void* hi;
+  int lb;            // 1: lo / hi in T (16-bit), else FP32
 };
 
 // NaN-propagating min / max (torch.amin / amax semantics)
 __device__ __forceinline__ float nmin(float m, float v) { return (v < m || v != v) ? v : m; }
 __device__ __forceinline__ float nmax(float m, float v) { return (v > m || v != v) ? v : m; }
+
+// FP32 -> T bits for a value that is exactly a T value (a bound is one of
+// the keys), NaN payload kept.
+template <typename T> __device__ __forceinline__ uint16_t bits16(float v);
+template <> __device__ __forceinline__ uint16_t bits16<bf16s>(float v) {
+  return (uint16_t)(__float_as_uint(v) >> 16);
+}
+template <> __device__ __forceinline__ uint16_t bits16<f16s>(float v) {
+  const _Float16 h = (_Float16)v;
+  uint16_t r;
+  __builtin_memcpy(&r, &h, 2);
+  return r;
+}
+template <> __device__ __forceinline__ uint16_t bits16<float>(float) { return 0; }
+
+// Bound element i of p, stored as FP32 or (lb) as T.
+template <typename T>
+__device__ __forceinline__ float get_bound(const void* p, size_t i, bool lb) {
+  if constexpr (sizeof(T) == 2)
+    if (lb) return cvt(T{static_cast<const uint16_t*>(p)[i]});
+  return static_cast<const float*>(p)[i];
+}
+template <typename T>
+__device__ __forceinline__ void put_bound(void* p, size_t i, float v, bool lb) {
+  if constexpr (sizeof(T) == 2)
+    if (lb) {
+      static_cast<uint16_t*>(p)[i] = bits16<T>(v);
+      return;
+    }
+  static_cast<float*>(p)[i] = v;
+}
 
 template <typename T>
 __device__ __forceinline__ void unpack8(const uint4& x, float (&f)[8]) {
@@ -79,8 +113,8 @@ __global__ __launch_bounds__(256) void k_bounds(BoundsArgs a) {
       l = nmin(l, s_lo[e * 256 + gg * cpr + cc]);
       h = nmax(h, s_hi[e * 256 + gg * cpr + cc]);
     }
-    a.lo[(size_t)row * a.d + x] = l;
-    a.hi[(size_t)row * a.d + x] = h;
+    put_bound<T>(a.lo, (size_t)row * a.d + x, l, a.lb);
+    put_bound<T>(a.hi, (size_t)row * a.d + x, h, a.lb);
   }
 }
 
@@ -129,8 +163,22 @@ __global__ __launch_bounds__(STK_BOUNDS_WG) void k_bounds_cols(BoundsArgs a) {
       }
     }
   }
-  float4* ol = reinterpret_cast<float4*>(a.lo + (size_t)row * a.d + 8 * c);
-  float4* oh = reinterpret_cast<float4*>(a.hi + (size_t)row * a.d + 8 * c);
+  const size_t o = (size_t)row * a.d + 8 * c;
+  if (a.lb) {
+    uint32_t wl[4], wh[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wl[i] = bits16<T>(lo[2 * i]) | ((uint32_t)bits16<T>(lo[2 * i + 1]) << 16);
+      wh[i] = bits16<T>(hi[2 * i]) | ((uint32_t)bits16<T>(hi[2 * i + 1]) << 16);
+    }
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.lo) + o) =
+        make_uint4(wl[0], wl[1], wl[2], wl[3]);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.hi) + o) =
+        make_uint4(wh[0], wh[1], wh[2], wh[3]);
+    return;
+  }
+  float4* ol = reinterpret_cast<float4*>(static_cast<float*>(a.lo) + o);
+  float4* oh = reinterpret_cast<float4*>(static_cast<float*>(a.hi) + o);
   ol[0] = make_float4(lo[0], lo[1], lo[2], lo[3]);
   ol[1] = make_float4(lo[4], lo[5], lo[6], lo[7]);
   oh[0] = make_float4(hi[0], hi[1], hi[2], hi[3]);
@@ -149,15 +197,15 @@ __global__ __launch_bounds__(256) void k_bounds_any(BoundsArgs a) {
       l = nmin(l, v);
       h = nmax(h, v);
     }
-    a.lo[(size_t)row * a.d + x] = l;
-    a.hi[(size_t)row * a.d + x] = h;
+    put_bound<T>(a.lo, (size_t)row * a.d + x, l, a.lb);
+    put_bound<T>(a.hi, (size_t)row * a.d + x, h, a.lb);
   }
 }
 
 struct AppendArgs {
   const void* k; int dtype;   // new token's keys [hkv, d]
   int hkv, n, d, block, pos;
-  float* lo; float* hi;
+  void* lo; void* hi; int lb;
 };
 
 // One appended token: block `block` of every KV head starts over at pos 0,
@@ -169,8 +217,8 @@ __global__ __launch_bounds__(256) void k_bounds_append(AppendArgs a) {
   const int kv = x / a.d, dim = x % a.d;
   const float v = cvt(reinterpret_cast<const T*>(a.k)[x]);
   const size_t o = ((size_t)kv * a.n + a.block) * a.d + dim;
-  a.lo[o] = a.pos == 0 ? v : nmin(a.lo[o], v);
-  a.hi[o] = a.pos == 0 ? v : nmax(a.hi[o], v);
+  put_bound<T>(a.lo, o, a.pos == 0 ? v : nmin(get_bound<T>(a.lo, o, a.lb), v), a.lb);
+  put_bound<T>(a.hi, o, a.pos == 0 ? v : nmax(get_bound<T>(a.hi, o, a.lb), v), a.lb);
 }
 
 // One decode token per request into a paged pool (the paged wire format of
@@ -186,7 +234,8 @@ struct PagedAppendArgs {
   const void* k_new; const void* v_new;   // [R, Hkv, D]
   int requests, hkv, nb, b, d, pages;
   void* k_pages; void* v_pages;           // [P, B, D]
-  float* lo; float* hi;                   // [P, D]
+  void* lo; void* hi;                     // [P, D], FP32 or (lb) T
+  int lb;
   const int32_t* table;                   // [R, Hkv, nb]
   int32_t* nblocks;                       // [R]
   int32_t* ntokens;                       // [R] or null
@@ -222,8 +271,8 @@ __global__ __launch_bounds__(256) void k_paged_append(PagedAppendArgs a) {
   reinterpret_cast<T*>(a.v_pages)[o] = reinterpret_cast<const T*>(a.v_new)[x];
   const float f = cvt(kv);
   const size_t ob = (size_t)page * a.d + dim;
-  a.lo[ob] = off == 0 ? f : nmin(a.lo[ob], f);
-  a.hi[ob] = off == 0 ? f : nmax(a.hi[ob], f);
+  put_bound<T>(a.lo, ob, off == 0 ? f : nmin(get_bound<T>(a.lo, ob, a.lb), f), a.lb);
+  put_bound<T>(a.hi, ob, off == 0 ? f : nmax(get_bound<T>(a.hi, ob, a.lb), f), a.lb);
 }
 
 }  // namespace stk
@@ -232,14 +281,15 @@ using namespace stk;
 
 extern "C" {
 
-STK_API int stk_block_bounds(const void* k, int dtype, int hkv, int n, int b, int d, float* lo,
-                             float* hi, void* stream) {
+STK_API int stk_block_bounds(const void* k, int dtype, int hkv, int n, int b, int d, void* lo,
+                             void* hi, int bounds_dtype, void* stream) {
   STK_REQUIRE(k && lo && hi, "null pointer");
   STK_REQUIRE(dtype == DT_F32 || dtype == DT_F16 || dtype == DT_BF16, "unsupported dtype");
+  STK_REQUIRE(stk_bounds_ok(dtype, bounds_dtype), "lo and hi must be FP32 or K's 16-bit type");
   STK_REQUIRE(hkv > 0 && n >= 0 && b > 0 && d > 0, "bad shape");
   if (n == 0) return STK_OK;
   STK_REQUIRE((int64_t)hkv * n <= 0x7fffffff, "too many blocks");
-  BoundsArgs a{k, dtype, hkv * n, b, d, lo, hi};
+  BoundsArgs a{k, dtype, hkv * n, b, d, lo, hi, bounds_dtype != 0};
   hipStream_t st = (hipStream_t)stream;
   const bool vec = dtype != DT_F32 && d % 8 == 0 && d <= 2048 &&
                    (reinterpret_cast<uintptr_t>(k) & 15) == 0;
@@ -267,12 +317,13 @@ STK_API int stk_block_bounds(const void* k, int dtype, int hkv, int n, int b, in
 }
 
 STK_API int stk_bounds_append(const void* k_new, int dtype, int hkv, int n, int d, int block,
-                              int pos, float* lo, float* hi, void* stream) {
+                              int pos, void* lo, void* hi, int bounds_dtype, void* stream) {
   STK_REQUIRE(k_new && lo && hi, "null pointer");
   STK_REQUIRE(dtype == DT_F32 || dtype == DT_F16 || dtype == DT_BF16, "unsupported dtype");
+  STK_REQUIRE(stk_bounds_ok(dtype, bounds_dtype), "lo and hi must be FP32 or K's 16-bit type");
   STK_REQUIRE(hkv > 0 && n > 0 && d > 0, "bad shape");
   STK_REQUIRE(block >= 0 && block < n && pos >= 0, "block or position out of range");
-  AppendArgs a{k_new, dtype, hkv, n, d, block, pos, lo, hi};
+  AppendArgs a{k_new, dtype, hkv, n, d, block, pos, lo, hi, bounds_dtype != 0};
   const int grid = (hkv * d + 255) / 256;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DT_BF16)
@@ -286,7 +337,7 @@ STK_API int stk_bounds_append(const void* k_new, int dtype, int hkv, int n, int 
 
 STK_API int stk_paged_append(const void* k_new, const void* v_new, int dtype, int requests,
                              int hkv, int nb, int b, int d, int pages, void* k_pages,
-                             void* v_pages, float* lo_pages, float* hi_pages,
+                             void* v_pages, void* lo_pages, void* hi_pages, int bounds_dtype,
                              const int32_t* block_table, int32_t* nblocks, int32_t* ntokens,
                              const int32_t* positions, void* stream) {
   STK_REQUIRE(k_new && v_new && k_pages && v_pages && lo_pages && hi_pages && block_table &&
@@ -294,10 +345,12 @@ STK_API int stk_paged_append(const void* k_new, const void* v_new, int dtype, in
               "null pointer");
   STK_REQUIRE(dtype == DT_F32 || dtype == DT_F16 || dtype == DT_BF16, "unsupported dtype");
   STK_REQUIRE(requests > 0 && hkv > 0 && nb > 0 && b > 0 && d > 0 && pages > 0, "bad shape");
+  STK_REQUIRE(stk_bounds_ok(dtype, bounds_dtype),
+              "lo and hi pages must be FP32 or the pages' 16-bit type");
   STK_REQUIRE((int64_t)nb * b <= 0x7fffffff && (int64_t)requests * hkv * d <= 0x7fffffff,
               "shape too large");
-  PagedAppendArgs a{k_new, v_new, requests, hkv, nb, b, d, pages, k_pages, v_pages,
-                    lo_pages, hi_pages, block_table, nblocks, ntokens, positions};
+  PagedAppendArgs a{k_new, v_new, requests, hkv, nb, b, d, pages, k_pages, v_pages, lo_pages,
+                    hi_pages, bounds_dtype != 0, block_table, nblocks, ntokens, positions};
   const int64_t n = (int64_t)requests * hkv * d;
   const dim3 grid((unsigned)((n + 255) / 256));
   hipStream_t st = (hipStream_t)stream;

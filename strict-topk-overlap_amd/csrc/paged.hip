@@ -56,7 +56,8 @@ STK_API size_t stk_paged_workspace_bytes(int requests, int hq, int nb) {
 
 static int paged_common(const void* q, const void* k_pages, const void* v_pages, int dtype,
                         int requests, int hq, int hkv, int nb, int b, int d, int pages,
-                        const float* lo_pages, const float* hi_pages, const int32_t* table,
+                        const void* lo_pages, const void* hi_pages, int bounds_dtype,
+                        const int32_t* table,
                         const int32_t* nblocks, const int32_t* ntokens, int topk,
                         const int32_t* predicted, int sp, float* m, float* l, float* u,
                         void* workspace, size_t workspace_bytes, FrontArgs* f, PagedPlan* plan,
@@ -65,6 +66,8 @@ static int paged_common(const void* q, const void* k_pages, const void* v_pages,
   STK_REQUIRE(q && k_pages && v_pages && lo_pages && hi_pages && table && nblocks,
               "null pointer");
   STK_REQUIRE(sp == 0 || (predicted && m && l && u), "null pointer");
+  STK_REQUIRE(stk_bounds_ok(dtype, bounds_dtype),
+              "lo and hi pages must be FP32 or the pages' 16-bit type");
   STK_REQUIRE(workspace && workspace_bytes >= stk_paged_workspace_bytes(requests, hq, nb),
               "workspace too small");
   const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_pages) |
@@ -81,14 +84,14 @@ static int paged_common(const void* q, const void* k_pages, const void* v_pages,
   *dummy = static_cast<char*>(workspace) +
            stk_align((size_t)requests * hq * nb * sizeof(uint64_t));
   *f = make_front_args(q, k_pages, v_pages, dtype, plan->hq, plan->hkv, nb, b, d, lo_pages,
-                       hi_pages, predicted, sp, m, l, u, *keys, plan->s);
+                       hi_pages, bounds_dtype != 0, predicted, sp, m, l, u, *keys, plan->s);
   f->pg = Paging{table, nblocks, hkv, pages, ntokens};
   return STK_OK;
 }
 
 STK_API int stk_paged_step(const void* q, const void* k_pages, const void* v_pages, int dtype,
                            int requests, int hq, int hkv, int nb, int b, int d, int pages,
-                           const float* lo_pages, const float* hi_pages,
+                           const void* lo_pages, const void* hi_pages, int bounds_dtype,
                            const int32_t* block_table, const int32_t* nblocks,
                            const int32_t* ntokens, int topk, const int32_t* predicted, int sp,
                            int union_mode, int32_t* selected, float* m, float* l, float* u,
@@ -98,8 +101,8 @@ STK_API int stk_paged_step(const void* q, const void* k_pages, const void* v_pag
   uint64_t* keys = nullptr;
   const void* dummy = nullptr;
   int rc = paged_common(q, k_pages, v_pages, dtype, requests, hq, hkv, nb, b, d, pages, lo_pages,
-                        hi_pages, block_table, nblocks, ntokens, topk, predicted, sp, m, l, u,
-                        workspace, workspace_bytes, &f, &plan, &keys, &dummy);
+                        hi_pages, bounds_dtype, block_table, nblocks, ntokens, topk, predicted,
+                        sp, m, l, u, workspace, workspace_bytes, &f, &plan, &keys, &dummy);
   if (rc) return rc;
   STK_REQUIRE(selected && out, "null pointer");
   TailArgs t{};
@@ -121,8 +124,9 @@ STK_API int stk_paged_step(const void* q, const void* k_pages, const void* v_pag
 
 STK_API int stk_paged_signed_step(const void* q, const void* k_pages, const void* v_pages,
                                   int dtype, int requests, int hq, int hkv, int nb, int b, int d,
-                                  int pages, const float* lo_pages, const float* hi_pages,
-                                  const int32_t* block_table, const int32_t* nblocks,
+                                  int pages, const void* lo_pages, const void* hi_pages,
+                                  int bounds_dtype, const int32_t* block_table,
+                                  const int32_t* nblocks,
                                   const int32_t* ntokens, int topk, const int32_t* predicted,
                                   int sp, int hybrid, float mass_threshold, float min_remaining,
                                   float cancellation_tol, float max_extra_mass,
@@ -135,8 +139,8 @@ STK_API int stk_paged_signed_step(const void* q, const void* k_pages, const void
   uint64_t* keys = nullptr;
   const void* dummy = nullptr;
   int rc = paged_common(q, k_pages, v_pages, dtype, requests, hq, hkv, nb, b, d, pages, lo_pages,
-                        hi_pages, block_table, nblocks, ntokens, topk, predicted, sp, m, l, u,
-                        workspace, workspace_bytes, &f, &plan, &keys, &dummy);
+                        hi_pages, bounds_dtype, block_table, nblocks, ntokens, topk, predicted,
+                        sp, m, l, u, workspace, workspace_bytes, &f, &plan, &keys, &dummy);
   if (rc) return rc;
   STK_REQUIRE(selected && out && fallback && remaining && positive && total, "null pointer");
   STK_REQUIRE(!(max_extra_mass > 0.f) || (approx && extra),

@@ -2,7 +2,10 @@
 //
 // Reference: strict_topk/selector.py:8-20 (_score) and strict_topk/gqa.py:15-26
 // (_bound_score): score[h,n] = sum_d q_d * (q_d >= 0 ? hi : lo)[h/G, n, d].
-// Evaluated in FP64: products of a 16/32-bit q and an FP32 bound are exact;
+// Evaluated in FP64: products of a 16/32-bit q and an FP32 bound are exact
+// (the bounds may also be stored in the query's own 16-bit type, lb = 1:
+// the min / max of 16-bit keys are 16-bit values, so that storage is exact
+// and the scores are the same bits);
 // 16 logical lanes share a block, lane c summing dims 64*j + 4*c + t
 // (j ascending, t = 0..3) from +0.0, then an xor butterfly (8, 4, 2, 1)
 // combines the lanes.  A workgroup (4 waves) covers 16 * STEPS consecutive
@@ -42,7 +45,8 @@ __device__ __forceinline__ uint64_t score_key(double s) {
 
 struct ScoreArgs {
   const void* q; int qtype;
-  const float* lo; const float* hi;
+  const void* lo; const void* hi;
+  int lb;                // 1: lo / hi are 16-bit, the query's element type
   int hq, hkv, n, d;
   int chunks;            // workgroups per KV head
   float* scores;         // optional FP32 [hq, n]
@@ -139,37 +143,91 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
   // branch around a load: blocks past n read row 0 and are not stored
   float4 lv[STEPS][P], hv[STEPS][P];
   int dead = 0;   // PG: bit s set when this lane's block of step s has no page
+  size_t rows[STEPS];
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     const int nb = wave_base + 4 * s + sub;
     const bool valid = nb < nv;
-    size_t row;
     if constexpr (PG) {
       const int page = valid ? pgs[s] : -1;
       dead |= (page < 0) << s;
-      row = page >= 0 ? (size_t)page : 0;
+      rows[s] = page >= 0 ? (size_t)page : 0;
     } else {
-      row = (size_t)kv * a.n + (valid ? nb : 0);
+      rows[s] = (size_t)kv * a.n + (valid ? nb : 0);
     }
-    const float* lrow = a.lo + row * a.d;
-    const float* hrow = a.hi + row * a.d;
+  }
+  bool b16 = false;
+  if constexpr (sizeof(Q) == 2) b16 = a.lb != 0;
+  if constexpr (sizeof(Q) == 2) if (b16) {
+    // 16-bit bounds: a lane's four dims are 8 bytes; the raw words are kept
+    // in .x / .y and widened below, once every load is in flight
+    const uint16_t* lb16 = static_cast<const uint16_t*>(a.lo);
+    const uint16_t* hb16 = static_cast<const uint16_t*>(a.hi);
 #pragma unroll
-    for (int j = 0; j < P; ++j) {
-      const int d0 = 64 * j + 4 * c;
-      if constexpr (FULL) {
-        const int dd = 64 * j < a.d ? d0 : 0;   // passes past D: unused
-        lv[s][j] = *reinterpret_cast<const float4*>(lrow + dd);
-        hv[s][j] = *reinterpret_cast<const float4*>(hrow + dd);
-      } else {
-        float l4[4], h4[4];
+    for (int s = 0; s < STEPS; ++s) {
+      const uint16_t* lrow = lb16 + rows[s] * a.d;
+      const uint16_t* hrow = hb16 + rows[s] * a.d;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const bool ok = d0 + t < a.d;
-          l4[t] = ld_or(lrow, (int64_t)(d0 + t), ok, 0.f);
-          h4[t] = ld_or(hrow, (int64_t)(d0 + t), ok, 0.f);
+      for (int j = 0; j < P; ++j) {
+        const int d0 = 64 * j + 4 * c;
+        uint2 l2, h2;
+        if constexpr (FULL) {
+          const int dd = 64 * j < a.d ? d0 : 0;   // passes past D: unused
+          l2 = *reinterpret_cast<const uint2*>(lrow + dd);
+          h2 = *reinterpret_cast<const uint2*>(hrow + dd);
+        } else {
+          uint32_t l4[4], h4[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const bool ok = d0 + t < a.d;
+            l4[t] = ld_or(lrow, (int64_t)(d0 + t), ok, (uint16_t)0);
+            h4[t] = ld_or(hrow, (int64_t)(d0 + t), ok, (uint16_t)0);
+          }
+          l2 = make_uint2(l4[0] | (l4[1] << 16), l4[2] | (l4[3] << 16));
+          h2 = make_uint2(h4[0] | (h4[1] << 16), h4[2] | (h4[3] << 16));
         }
-        lv[s][j] = make_float4(l4[0], l4[1], l4[2], l4[3]);
-        hv[s][j] = make_float4(h4[0], h4[1], h4[2], h4[3]);
+        lv[s][j] = make_float4(__uint_as_float(l2.x), __uint_as_float(l2.y), 0.f, 0.f);
+        hv[s][j] = make_float4(__uint_as_float(h2.x), __uint_as_float(h2.y), 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        float f[4];
+        Unpack<Q>::run(__float_as_uint(lv[s][j].x), f);
+        Unpack<Q>::run(__float_as_uint(lv[s][j].y), f + 2);
+        lv[s][j] = make_float4(f[0], f[1], f[2], f[3]);
+        Unpack<Q>::run(__float_as_uint(hv[s][j].x), f);
+        Unpack<Q>::run(__float_as_uint(hv[s][j].y), f + 2);
+        hv[s][j] = make_float4(f[0], f[1], f[2], f[3]);
+      }
+  }
+  if (!b16) {
+    const float* lb32 = static_cast<const float*>(a.lo);
+    const float* hb32 = static_cast<const float*>(a.hi);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const float* lrow = lb32 + rows[s] * a.d;
+      const float* hrow = hb32 + rows[s] * a.d;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        const int d0 = 64 * j + 4 * c;
+        if constexpr (FULL) {
+          const int dd = 64 * j < a.d ? d0 : 0;   // passes past D: unused
+          lv[s][j] = *reinterpret_cast<const float4*>(lrow + dd);
+          hv[s][j] = *reinterpret_cast<const float4*>(hrow + dd);
+        } else {
+          float l4[4], h4[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const bool ok = d0 + t < a.d;
+            l4[t] = ld_or(lrow, (int64_t)(d0 + t), ok, 0.f);
+            h4[t] = ld_or(hrow, (int64_t)(d0 + t), ok, 0.f);
+          }
+          lv[s][j] = make_float4(l4[0], l4[1], l4[2], l4[3]);
+          hv[s][j] = make_float4(h4[0], h4[1], h4[2], h4[3]);
+        }
       }
     }
   }

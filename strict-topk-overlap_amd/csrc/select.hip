@@ -206,10 +206,10 @@ static void launch_score_q(ScoreArgs& a, hipStream_t st) {
 #undef STK_SCORE
 }
 
-int stk_launch_score(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
+int stk_launch_score(const void* q, int q_dtype, const void* lo, const void* hi, int lb, int hq,
                      int hkv, int n, int d, float* scores, uint64_t* keys, hipStream_t st) {
   ScoreArgs a{};
-  a.q = q; a.qtype = q_dtype; a.lo = lo; a.hi = hi;
+  a.q = q; a.qtype = q_dtype; a.lo = lo; a.hi = hi; a.lb = lb;
   a.hq = hq; a.hkv = hkv; a.n = n; a.d = d;
   a.scores = scores; a.keys = keys;
   if (q_dtype == DT_BF16) launch_score_q<bf16s>(a, st);
@@ -245,11 +245,14 @@ int stk_launch_topk(const uint64_t* keys, int rows, int n, int k, int32_t* ids, 
 
 extern "C" {
 
-STK_API int stk_block_scores(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
-                             int hkv, int n, int d, float* scores, void* stream) {
+STK_API int stk_block_scores(const void* q, int q_dtype, const void* lo, const void* hi,
+                             int bounds_dtype, int hq, int hkv, int n, int d, float* scores,
+                             void* stream) {
   STK_REQUIRE(check_select(q_dtype, hq, hkv, n, d));
   STK_REQUIRE(q && lo && hi && scores, "null pointer");
-  return stk_launch_score(q, q_dtype, lo, hi, hq, hkv, n, d, scores, nullptr,
+  STK_REQUIRE(stk_bounds_ok(q_dtype, bounds_dtype),
+              "lo and hi must be FP32 or the query's 16-bit type");
+  return stk_launch_score(q, q_dtype, lo, hi, bounds_dtype != 0, hq, hkv, n, d, scores, nullptr,
                           (hipStream_t)stream);
 }
 
@@ -258,17 +261,21 @@ STK_API size_t stk_select_workspace_bytes(int hq, int hkv, int n, int d, int top
   return stk_align((size_t)hq * n * sizeof(uint64_t));
 }
 
-STK_API int stk_select_blocks(const void* q, int q_dtype, const float* lo, const float* hi, int hq,
-                              int hkv, int n, int d, int topk, float* scores, int32_t* ids,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+STK_API int stk_select_blocks(const void* q, int q_dtype, const void* lo, const void* hi,
+                              int bounds_dtype, int hq, int hkv, int n, int d, int topk,
+                              float* scores, int32_t* ids, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   STK_REQUIRE(check_select(q_dtype, hq, hkv, n, d));
   STK_REQUIRE(q && lo && hi && ids, "null pointer");
+  STK_REQUIRE(stk_bounds_ok(q_dtype, bounds_dtype),
+              "lo and hi must be FP32 or the query's 16-bit type");
   STK_REQUIRE(topk >= 1 && topk <= n, "selected index k out of range");
   STK_REQUIRE(workspace && workspace_bytes >= stk_select_workspace_bytes(hq, hkv, n, d, topk),
               "workspace too small");
   hipStream_t st = (hipStream_t)stream;
   uint64_t* keys = static_cast<uint64_t*>(workspace);
-  int rc = stk_launch_score(q, q_dtype, lo, hi, hq, hkv, n, d, scores, keys, st);
+  int rc = stk_launch_score(q, q_dtype, lo, hi, bounds_dtype != 0, hq, hkv, n, d, scores, keys,
+                            st);
   if (rc) return rc;
   return stk_launch_topk(keys, hq, n, topk, ids, st);
 }

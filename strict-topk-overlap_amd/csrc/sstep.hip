@@ -15,8 +15,8 @@ using namespace stk;
 extern "C" {
 
 STK_API int stk_signed_step(const void* q, const void* k, const void* v, int dtype, int hq,
-                            int hkv, int n, int b, int d, const float* lo, const float* hi,
-                            int topk, const void* predicted, int pred_dtype, int sp, int hybrid,
+                            int hkv, int n, int b, int d, const void* lo, const void* hi,
+                            int bounds_dtype, int topk, const void* predicted, int pred_dtype, int sp, int hybrid,
                             float mass_threshold, float min_remaining, float cancellation_tol,
                             float max_extra_mass, int32_t* selected, float* m, float* l, float* u,
                             float* out, uint8_t* fallback, float* remaining, uint8_t* approx,
@@ -26,6 +26,8 @@ STK_API int stk_signed_step(const void* q, const void* k, const void* v, int dty
   STK_REQUIRE(q && k && v && lo && hi && predicted && selected && m && l && u && out &&
                   fallback && remaining && positive && total,
               "null pointer");
+  STK_REQUIRE(stk_bounds_ok(dtype, bounds_dtype),
+              "lo and hi must be FP32 or the element type of Q/K/V");
   STK_REQUIRE(!(max_extra_mass > 0.f) || (approx && extra),
               "max_extra_mass > 0 needs the approx and extra outputs");
   STK_REQUIRE(max_extra_mass >= 0.f && max_extra_mass <= 1.f, "max_extra_mass must be in [0,1]");
@@ -40,8 +42,8 @@ STK_API int stk_signed_step(const void* q, const void* k, const void* v, int dty
   const char* why = plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, align, &s);
   STK_REQUIRE(why == nullptr, why ? why : "");
   uint64_t* keys = static_cast<uint64_t*>(workspace);
-  const FrontArgs f = make_front_args(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, predicted, sp, m,
-                                      l, u, keys, s);
+  const FrontArgs f = make_front_args(q, k, v, dtype, hq, hkv, n, b, d, lo, hi,
+                                      bounds_dtype != 0, predicted, sp, m, l, u, keys, s);
   STailArgs t{};
   t.kv = KV{q, k, v, hq, hkv, n, b, d};
   t.keys = keys; t.k = topk; t.ids = selected;

@@ -50,11 +50,11 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
 }
 
 FrontArgs make_front_args(const void* q, const void* k, const void* v, int dtype, int hq,
-                          int hkv, int n, int b, int d, const float* lo, const float* hi,
+                          int hkv, int n, int b, int d, const void* lo, const void* hi, int lb,
                           const void* predicted, int sp, float* m, float* l, float* u,
                           uint64_t* keys, const StepShape& s) {
   FrontArgs f{};
-  f.sc.q = q; f.sc.qtype = dtype; f.sc.lo = lo; f.sc.hi = hi;
+  f.sc.q = q; f.sc.qtype = dtype; f.sc.lo = lo; f.sc.hi = hi; f.sc.lb = lb;
   f.sc.hq = hq; f.sc.hkv = hkv; f.sc.n = n; f.sc.d = d;
   f.sc.scores = nullptr; f.sc.keys = keys;
   f.sc.chunks = (n + kScoreWaves * 4 * s.steps - 1) / (kScoreWaves * 4 * s.steps);
@@ -90,7 +90,8 @@ STK_API int stk_step_supported(int dtype, int hq, int hkv, int n, int b, int d, 
 }
 
 static int step_call(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
-                     int n, int b, int d, const float* lo, const float* hi, int topk,
+                     int n, int b, int d, const void* lo, const void* hi, int bounds_dtype,
+                     int topk,
                      const void* predicted, int pred_dtype, int sp, int union_mode,
                      int32_t* selected, float* m, float* l, float* u, float* out,
                      void* workspace, size_t workspace_bytes, void* stream, bool front,
@@ -98,6 +99,8 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
   STK_REQUIRE(stk_check_kv(dtype, hq, hkv, n, b, d));
   STK_REQUIRE(q && k && v && predicted && m && l && u, "null pointer");
   STK_REQUIRE(!front || (lo && hi), "null pointer");
+  STK_REQUIRE(!front || stk_bounds_ok(dtype, bounds_dtype),
+              "lo and hi must be FP32 or the element type of Q/K/V");
   STK_REQUIRE(!tail || (selected && out), "null pointer");
   STK_REQUIRE(workspace && workspace_bytes >= stk_step_workspace_bytes(hq, hkv, n, d, topk),
               "workspace too small");
@@ -109,8 +112,8 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
   const char* why = plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, align, &s);
   STK_REQUIRE(why == nullptr, why ? why : "");
   uint64_t* keys = static_cast<uint64_t*>(workspace);
-  const FrontArgs f = make_front_args(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, predicted, sp, m,
-                                      l, u, keys, s);
+  const FrontArgs f = make_front_args(q, k, v, dtype, hq, hkv, n, b, d, lo, hi,
+                                      bounds_dtype != 0, predicted, sp, m, l, u, keys, s);
   TailArgs t{};
   t.kv = KV{q, k, v, hq, hkv, n, b, d};
   t.keys = keys; t.k = topk; t.ids = selected;
@@ -126,14 +129,14 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
 }
 
 STK_API int stk_speculative_step(const void* q, const void* k, const void* v, int dtype, int hq,
-                                 int hkv, int n, int b, int d, const float* lo, const float* hi,
-                                 int topk, const void* predicted, int pred_dtype, int sp,
+                                 int hkv, int n, int b, int d, const void* lo, const void* hi,
+                                 int bounds_dtype, int topk, const void* predicted, int pred_dtype, int sp,
                                  int union_mode, int32_t* selected, float* m, float* l, float* u,
                                  float* out, void* workspace, size_t workspace_bytes,
                                  void* stream) {
-  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, topk, predicted, pred_dtype, sp,
-                   union_mode, selected, m, l, u, out, workspace, workspace_bytes, stream, true,
-                   true);
+  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, bounds_dtype, topk, predicted,
+                   pred_dtype, sp, union_mode, selected, m, l, u, out, workspace,
+                   workspace_bytes, stream, true, true);
 }
 
 // ---- the allocation-free variant of stk_speculative_step
@@ -187,8 +190,9 @@ static int scratch_address(hipStream_t stream, void** out) {
 STK_API size_t stk_step_noalloc_max_keys(void) { return kNoAllocMaxKeys; }
 
 STK_API int stk_speculative_step_noalloc(const void* q, const void* k, const void* v, int dtype,
-                                         int hq, int hkv, int n, int b, int d, const float* lo,
-                                         const float* hi, int topk, const void* predicted,
+                                         int hq, int hkv, int n, int b, int d, const void* lo,
+                                         const void* hi, int bounds_dtype, int topk,
+                                         const void* predicted,
                                          int pred_dtype, int sp, int union_mode,
                                          int32_t* selected, float* m, float* l, float* u,
                                          float* out, void* stream) {
@@ -200,18 +204,19 @@ STK_API int stk_speculative_step_noalloc(const void* q, const void* k, const voi
   void* ws = nullptr;
   const int rc = scratch_address((hipStream_t)stream, &ws);
   if (rc) return rc;
-  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, topk, predicted, pred_dtype, sp,
-                   union_mode, selected, m, l, u, out, ws, kNoAllocMaxKeys * sizeof(uint64_t),
-                   stream, true, true);
+  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, bounds_dtype, topk, predicted,
+                   pred_dtype, sp, union_mode, selected, m, l, u, out, ws,
+                   kNoAllocMaxKeys * sizeof(uint64_t), stream, true, true);
 }
 
 STK_API int stk_step_front(const void* q, const void* k, const void* v, int dtype, int hq,
-                           int hkv, int n, int b, int d, const float* lo, const float* hi,
-                           int topk, const void* predicted, int pred_dtype, int sp, float* m,
+                           int hkv, int n, int b, int d, const void* lo, const void* hi,
+                           int bounds_dtype, int topk, const void* predicted, int pred_dtype, int sp, float* m,
                            float* l, float* u, void* workspace, size_t workspace_bytes,
                            void* stream) {
-  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, topk, predicted, pred_dtype, sp, 0,
-                   nullptr, m, l, u, nullptr, workspace, workspace_bytes, stream, true, false);
+  return step_call(q, k, v, dtype, hq, hkv, n, b, d, lo, hi, bounds_dtype, topk, predicted,
+                   pred_dtype, sp, 0, nullptr, m, l, u, nullptr, workspace, workspace_bytes,
+                   stream, true, false);
 }
 
 STK_API int stk_step_tail(const void* q, const void* k, const void* v, int dtype, int hq,
@@ -219,7 +224,7 @@ STK_API int stk_step_tail(const void* q, const void* k, const void* v, int dtype
                           int pred_dtype, int sp, int union_mode, const float* m, const float* l,
                           const float* u, int32_t* selected, float* out, void* workspace,
                           size_t workspace_bytes, void* stream) {
-  return step_call(q, k, v, dtype, hq, hkv, n, b, d, nullptr, nullptr, topk, predicted,
+  return step_call(q, k, v, dtype, hq, hkv, n, b, d, nullptr, nullptr, 0, topk, predicted,
                    pred_dtype, sp, union_mode, selected, const_cast<float*>(m),
                    const_cast<float*>(l), const_cast<float*>(u), out, workspace,
                    workspace_bytes, stream, false, true);

@@ -28,9 +28,9 @@ const char* plan_step(int dtype, int hq, int hkv, int n, int b, int d, int topk,
                       int pred_dtype, uintptr_t align, StepShape* s);
 
 // Front arguments: keys[hq, n] into `keys`, states of predicted[hq, sp]
-// into m, l, u.
+// into m, l, u; lb: lo / hi are 16-bit (the element type of q, k, v).
 FrontArgs make_front_args(const void* q, const void* k, const void* v, int dtype, int hq,
-                          int hkv, int n, int b, int d, const float* lo, const float* hi,
+                          int hkv, int n, int b, int d, const void* lo, const void* hi, int lb,
                           const void* predicted, int sp, float* m, float* l, float* u,
                           uint64_t* keys, const StepShape& s);
 

@@ -108,7 +108,8 @@ def main():
         sq, sk, sv, slo, shi = step.sets[i % args.sets]
         rc = L.stk_step_front(sq.data_ptr(), sk.data_ptr(), sv.data_ptr(), _lib.dtype_code(sq),
                               c.hq, c.hkv, c.blocks, c.block, c.dim, slo.data_ptr(),
-                              shi.data_ptr(), c.topk, step.predicted.data_ptr(), 0, c.sp,
+                              shi.data_ptr(), _lib.bounds_code(slo, sq), c.topk,
+                              step.predicted.data_ptr(), 0, c.sp,
                               st.m.data_ptr(), st.l.data_ptr(), st.u.data_ptr(), ws.data_ptr(),
                               ws.numel(), _lib.stream(dev))
         if rc:

@@ -28,9 +28,9 @@ Z = ctypes.c_size_t
 _SIGS = {
     "stk_last_error": (ctypes.c_char_p, []),
     "stk_abi_version": (I, []),
-    "stk_block_scores": (I, [P, I, P, P, I, I, I, I, P, P]),
+    "stk_block_scores": (I, [P, I, P, P, I, I, I, I, I, P, P]),
     "stk_select_workspace_bytes": (Z, [I, I, I, I, I]),
-    "stk_select_blocks": (I, [P, I, P, P, I, I, I, I, I, P, P, P, Z, P]),
+    "stk_select_blocks": (I, [P, I, P, P, I, I, I, I, I, I, P, P, P, Z, P]),
     "stk_block_partials": (I, [P, P, P, I, I, I, I, I, I, P, I, I, P, I, P, P, P, P]),
     "stk_merge_partials": (I, [P, P, P, P, I, I, I, P, P]),
     "stk_exact_workspace_bytes": (Z, [I, I, I]),
@@ -57,25 +57,25 @@ _SIGS = {
     "stk_hier_repair": (I, [P, P, P, I, I, I, I, I, I, P, I, I, P, I, I, P, P, P, I, P, P, Z, P]),
     "stk_step_workspace_bytes": (Z, [I, I, I, I, I]),
     "stk_step_supported": (I, [I, I, I, I, I, I, I, I, I]),
-    "stk_speculative_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I,
+    "stk_speculative_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, I,
                                  P, P, P, P, P, P, Z, P]),
     "stk_step_noalloc_max_keys": (Z, []),
-    "stk_speculative_step_noalloc": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I,
+    "stk_speculative_step_noalloc": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, I,
                                          P, P, P, P, P, P]),
-    "stk_step_front": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, P, P, P, P, Z, P]),
+    "stk_step_front": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, P, P, P, P, Z, P]),
     "stk_step_tail": (I, [P, P, P, I, I, I, I, I, I, I, P, I, I, I, P, P, P, P, P, P, Z, P]),
     "stk_indexer_workspace_bytes": (Z, [I]),
     "stk_indexer_scores": (I, [P, P, I, I, I, I, P, P, Z, P]),
     "stk_indexer_select": (I, [P, P, I, I, I, I, I, I, P, P, P, Z, P]),
-    "stk_block_bounds": (I, [P, I, I, I, I, I, P, P, P]),
-    "stk_bounds_append": (I, [P, I, I, I, I, I, I, P, P, P]),
-    "stk_signed_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, P, I, I, I, F, F, F, F,
+    "stk_block_bounds": (I, [P, I, I, I, I, I, P, P, I, P]),
+    "stk_bounds_append": (I, [P, I, I, I, I, I, I, P, P, I, P]),
+    "stk_signed_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, I, F, F, F, F,
                             P, P, P, P, P, P, P, P, P, P, P, P, Z, P]),
     "stk_paged_workspace_bytes": (Z, [I, I, I]),
-    "stk_paged_append": (I, [P, P, I, I, I, I, I, I, I, P, P, P, P, P, P, P, P, P]),
-    "stk_paged_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, P, I, P, I, I,
+    "stk_paged_append": (I, [P, P, I, I, I, I, I, I, I, P, P, P, P, I, P, P, P, P, P]),
+    "stk_paged_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, I, P, P, P, I, P, I, I,
                            P, P, P, P, P, P, Z, P]),
-    "stk_paged_signed_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, P, I, P, I, I,
+    "stk_paged_signed_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, I, P, P, P, I, P, I, I,
                                   F, F, F, F, P, P, P, P, P, P, P, P, P, P, P, P, Z, P]),
 }
 
@@ -113,6 +113,17 @@ def dtype_code(t):
         return DTYPE[t.dtype]
     except KeyError:
         raise ValueError(f"unsupported element dtype {t.dtype}; expected float16, bfloat16 or float32")
+
+
+def bounds_code(bound, q):
+    """bounds_dtype of the C ABI: STK_F32 for float32 lo/hi, or the code of
+    the queries' 16-bit type when the bounds are stored in it (exact: the
+    min / max of 16-bit keys are 16-bit values)."""
+    if bound.dtype == torch.float32:
+        return 0
+    if bound.dtype == q.dtype and q.dtype in (torch.float16, torch.bfloat16):
+        return DTYPE[q.dtype]
+    raise ValueError("lo and hi must be FP32 or the element type of Q/K/V")
 
 
 def id_code(t):

@@ -3,7 +3,8 @@
 Wire format (one pool shared by a batch of requests of different lengths):
 
   k_pages, v_pages  [P, B, D]      one page = one KV head's block of B tokens
-  lo_pages, hi_pages [P, D] FP32   per-dim key min / max of the page
+  lo_pages, hi_pages [P, D]        per-dim key min / max of the page, FP32 or
+                                   (exact, half the bytes) the pages' dtype
   block_table       [R, Hkv, NB]   int32 page of logical block j of (request r,
                                    KV head h), valid for j < nblocks[r]
   nblocks           [R] int32      blocks per request, on the device
@@ -43,8 +44,8 @@ from .step import SignedStepResult, StepResult
 class PagedKV:
     k_pages: torch.Tensor       # [P, B, D]
     v_pages: torch.Tensor       # [P, B, D]
-    lo_pages: torch.Tensor      # [P, D] float32
-    hi_pages: torch.Tensor      # [P, D] float32
+    lo_pages: torch.Tensor      # [P, D] float32 or the pages' dtype
+    hi_pages: torch.Tensor      # [P, D] float32 or the pages' dtype
     block_table: torch.Tensor   # [R, Hkv, NB] int32
     nblocks: torch.Tensor       # [R] int32
     ntokens: torch.Tensor | None = None   # [R] int32; None: every block full
@@ -74,7 +75,7 @@ class PagedKV:
         return self.k_pages.shape[2]
 
 
-def pack(caches, width=None, order=None, spare=0, tokens=None):
+def pack(caches, width=None, order=None, spare=0, tokens=None, bounds_dtype=torch.float32):
     """Pack dense per-request caches [(k, v), ...] (k, v: [Hkv, N_r, B, D])
     into one pool, building lo/hi pages on the device (``bounds.block_bounds``
     on the pool).  ``order``: an optional permutation of the pages (pages are
@@ -82,7 +83,9 @@ def pack(caches, width=None, order=None, spare=0, tokens=None):
     zeroed pages at the end of the pool; ``width``: the table's row width
     (default: the longest request); ``tokens``: each request's token count
     ((N_r - 1) * B < tokens[r] <= N_r * B; default N_r * B), the bounds of a
-    partly filled last block taken over its tokens that hold data."""
+    partly filled last block taken over its tokens that hold data;
+    ``bounds_dtype``: float32, or the caches' 16-bit dtype (exact, half the
+    bytes for the scorer)."""
     from .bounds import block_bounds
     if not caches:
         raise ValueError("expected at least one request")
@@ -117,14 +120,14 @@ def pack(caches, width=None, order=None, spare=0, tokens=None):
         v_pages[idx] = v.reshape(hkv * n, b, d)
         table[r, :, :n] = idx.view(hkv, n).to(torch.int32).cpu()
         base += hkv * n
-    lo, hi = block_bounds(k_pages.unsqueeze(0))
+    lo, hi = block_bounds(k_pages.unsqueeze(0), bounds_dtype)
     lo, hi = lo[0], hi[0]
     for r, (n, t) in enumerate(zip(counts, tokens)):
         part = t - (n - 1) * b
         if part < b:
             pages = table[r, :, n - 1].to(dev).long()
-            lo[pages] = k_pages[pages, :part].amin(1).float()
-            hi[pages] = k_pages[pages, :part].amax(1).float()
+            lo[pages] = k_pages[pages, :part].amin(1).to(lo.dtype)
+            hi[pages] = k_pages[pages, :part].amax(1).to(hi.dtype)
     return PagedKV(k_pages, v_pages, lo, hi, table.to(dev),
                    torch.tensor(counts, dtype=torch.int32, device=dev),
                    torch.tensor(tokens, dtype=torch.int32, device=dev))
@@ -161,6 +164,7 @@ def append(kv, k_new, v_new, positions):
     _lib.call("stk_paged_append", _lib.ptr(k_new), _lib.ptr(v_new), _lib.dtype_code(k_new),
               kv.requests, kv.hkv, kv.width, kv.block, kv.dim, kv.pages, _lib.ptr(kv.k_pages),
               _lib.ptr(kv.v_pages), _lib.ptr(kv.lo_pages), _lib.ptr(kv.hi_pages),
+              _lib.bounds_code(kv.lo_pages, kv.k_pages),
               _lib.ptr(kv.block_table), _lib.ptr(kv.nblocks), _lib.ptr(kv.ntokens),
               _lib.ptr(positions), _lib.stream(k_new.device))
     return kv
@@ -180,8 +184,9 @@ def _check(q, kv, predicted, topk):
         raise ValueError("predicted IDs must be int32")
     if q.dtype != kv.k_pages.dtype:
         raise ValueError("Q and the pages must share a dtype")
-    if kv.lo_pages.dtype != torch.float32 or kv.hi_pages.dtype != torch.float32:
-        raise ValueError("lo and hi pages must be FP32")
+    if kv.hi_pages.dtype != kv.lo_pages.dtype or \
+            kv.lo_pages.dtype not in (torch.float32, kv.k_pages.dtype):
+        raise ValueError("lo and hi pages must be FP32 or the pages' dtype")
     if kv.block_table.dtype != torch.int32 or kv.nblocks.dtype != torch.int32:
         raise ValueError("block_table and nblocks must be int32")
     if kv.ntokens is not None and (kv.ntokens.dtype != torch.int32 or
@@ -216,7 +221,8 @@ def _common(q, kv, predicted, topk):
     ws = _lib.workspace(_lib.size("stk_paged_workspace_bytes", r, hq, kv.width), dev)
     head = (_lib.ptr(q), _lib.ptr(kv.k_pages), _lib.ptr(kv.v_pages), _lib.dtype_code(q), r, hq,
             kv.hkv, kv.width, kv.block, d, kv.pages, _lib.ptr(kv.lo_pages),
-            _lib.ptr(kv.hi_pages), _lib.ptr(kv.block_table), _lib.ptr(kv.nblocks),
+            _lib.ptr(kv.hi_pages), _lib.bounds_code(kv.lo_pages, q), _lib.ptr(kv.block_table),
+            _lib.ptr(kv.nblocks),
             _lib.ptr(kv.ntokens), topk, _lib.ptr(predicted), sp)
     st = (None, None, None) if state is None else (_lib.ptr(state.m), _lib.ptr(state.l),
                                                    _lib.ptr(state.u))

@@ -30,7 +30,7 @@ def block_scores(q, lo, hi):
     h, n, d = _check(q, lo, hi)
     scores = torch.empty((h, n), device=q.device, dtype=torch.float32)
     _lib.call("stk_block_scores", _lib.ptr(q), _lib.dtype_code(q), _lib.ptr(lo), _lib.ptr(hi),
-              h, h, n, d, _lib.ptr(scores), _lib.stream(q.device))
+              0, h, h, n, d, _lib.ptr(scores), _lib.stream(q.device))
     return scores
 
 
@@ -50,6 +50,6 @@ def select_ids(q, lo, hi, topk, hq, hkv, n, d):
     nbytes = _lib.size("stk_select_workspace_bytes", hq, hkv, n, d, topk)
     ws = _lib.workspace(nbytes, q.device)
     _lib.call("stk_select_blocks", _lib.ptr(q), _lib.dtype_code(q), _lib.ptr(lo), _lib.ptr(hi),
-              hq, hkv, n, d, topk, None, _lib.ptr(ids), _lib.ptr(ws), ws.numel(),
-              _lib.stream(q.device))
+              _lib.bounds_code(lo, q), hq, hkv, n, d, topk, None, _lib.ptr(ids), _lib.ptr(ws),
+              ws.numel(), _lib.stream(q.device))
     return ids

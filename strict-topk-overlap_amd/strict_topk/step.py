@@ -26,6 +26,7 @@ import torch
 
 from . import _lib, gqa, gqa_light
 from .kernels import PartialState, _allocate_state, _args
+from .selector import select_ids
 
 
 @dataclass
@@ -35,8 +36,47 @@ class StepResult:
     output: torch.Tensor       # float32 [Hq, D]
 
 
+def _check_bounds(q, k, lo, hi):
+    """lo / hi [Hkv, N, D], float32 or (lossless) the element type of Q/K/V."""
+    if lo.ndim != 3 or hi.shape != lo.shape or lo.shape[0] != k.shape[0] or \
+            lo.shape[1:] != (k.shape[1], k.shape[3]):
+        raise ValueError("expected LO/HI[Hkv,N,D] matching K")
+    if hi.dtype != lo.dtype or lo.dtype not in (torch.float32, q.dtype):
+        raise ValueError("lo and hi must be FP32 or the element type of Q/K/V")
+    if any(x.device != q.device or not x.is_contiguous() for x in (lo, hi)):
+        raise ValueError("Q/LO/HI must be contiguous and on the same CUDA device")
+
+
+def select_blocks(q, lo, hi, topk):
+    """``gqa.select_blocks`` that also takes bounds stored in the queries' own
+    16-bit type (the same IDs, from half the bound bytes)."""
+    if q.ndim != 2 or lo.ndim != 3 or hi.shape != lo.shape:
+        raise ValueError("expected Q[Hq,D] and LO/HI[Hkv,N,D]")
+    hkv, n, d = lo.shape
+    hq, qd = q.shape
+    if min(hq, hkv, n, d) <= 0 or qd != d or hq % hkv != 0:
+        raise ValueError("expected nonempty shapes, matching head dimensions and Hq divisible by Hkv")
+    if hi.dtype != lo.dtype or lo.dtype not in (torch.float32, q.dtype):
+        raise ValueError("lo and hi must be FP32 or the element type of Q/K/V")
+    if not q.is_cuda or any(x.device != q.device or not x.is_contiguous() for x in (q, lo, hi)):
+        raise ValueError("Q/LO/HI must be contiguous and on the same CUDA device")
+    return select_ids(q, lo, hi, topk, hq, hkv, n, d)
+
+
+def serial_step(q, k, v, lo, hi, topk):
+    """The same-work serial path: select_blocks, then the exact attention over
+    the selected blocks (``gqa.exact``); returns (selected, output)."""
+    sel = select_blocks(q, lo, hi, topk)
+    return sel, gqa.exact(q, k, v, sel)
+
+
 def supported(q, k, lo, topk, predicted):
+    """True when the fused kernels serve this shape: bf16/fp16, int32
+    predictions, D in {64, 128, 256}, B a multiple of 16, N <= 8192, K and SP
+    <= 256, SP * D <= 32768, and 16-byte aligned Q/K/V/LO."""
     hkv, n, b, d = k.shape
+    if any(t.data_ptr() % 16 for t in (q, k, lo)):
+        return False
     return bool(_lib.lib().stk_step_supported(_lib.dtype_code(q), q.shape[0], hkv, n, b, d,
                                               int(topk), predicted.shape[1],
                                               _lib.id_code(predicted)))
@@ -49,13 +89,7 @@ def speculative_step(q, k, v, lo, hi, predicted, topk, union=False):
     ValueError messages).  ``union`` selects ``repair_union`` semantics.
     """
     gqa._shape(q, k, v, predicted)
-    if lo.ndim != 3 or hi.shape != lo.shape or lo.shape[0] != k.shape[0] or \
-            lo.shape[1:] != (k.shape[1], k.shape[3]):
-        raise ValueError("expected LO/HI[Hkv,N,D] matching K")
-    if lo.dtype != torch.float32 or hi.dtype != torch.float32:
-        raise ValueError("lo and hi must be FP32")
-    if any(x.device != q.device or not x.is_contiguous() for x in (lo, hi)):
-        raise ValueError("Q/LO/HI must be contiguous and on the same CUDA device")
+    _check_bounds(q, k, lo, hi)
     topk = int(topk)
     hq, d = q.shape
     hkv, n, b, _ = k.shape
@@ -68,12 +102,13 @@ def speculative_step(q, k, v, lo, hi, predicted, topk, union=False):
         state = _allocate_state(hq, sp, d, dev)
         out = torch.empty((hq, d), device=dev, dtype=torch.float32)
         ws = _lib.workspace(_lib.size("stk_step_workspace_bytes", hq, hkv, n, d, topk), dev)
-        _lib.call("stk_speculative_step", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi), topk,
+        _lib.call("stk_speculative_step", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi),
+                  _lib.bounds_code(lo, q), topk,
                   _lib.ptr(predicted), _lib.id_code(predicted), sp, 1 if union else 0,
                   _lib.ptr(selected), _lib.ptr(state.m), _lib.ptr(state.l), _lib.ptr(state.u),
                   _lib.ptr(out), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
         return StepResult(selected, state, out)
-    selected = gqa.select_blocks(q, lo, hi, topk)
+    selected = select_blocks(q, lo, hi, topk)
     state = gqa.partials(q, k, v, predicted)
     if union:
         out = gqa.repair_union(q, k, v, selected, predicted, state)
@@ -92,6 +127,7 @@ def speculative_step_noalloc(q, k, v, lo, hi, predicted, topk, union=False, into
     overlap in time on one GPU share the array and must not run
     concurrently."""
     gqa._shape(q, k, v, predicted)
+    _check_bounds(q, k, lo, hi)
     topk = int(topk)
     hq, d = q.shape
     hkv, n, b, _ = k.shape
@@ -103,7 +139,8 @@ def speculative_step_noalloc(q, k, v, lo, hi, predicted, topk, union=False, into
         into = StepResult(torch.empty((hq, topk), device=dev, dtype=torch.int32),
                           _allocate_state(hq, sp, d, dev),
                           torch.empty((hq, d), device=dev, dtype=torch.float32))
-    _lib.call("stk_speculative_step_noalloc", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi), topk,
+    _lib.call("stk_speculative_step_noalloc", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi),
+              _lib.bounds_code(lo, q), topk,
               _lib.ptr(predicted), _lib.id_code(predicted), sp, 1 if union else 0,
               _lib.ptr(into.selected), _lib.ptr(into.state.m), _lib.ptr(into.state.l),
               _lib.ptr(into.state.u), _lib.ptr(into.output), _lib.stream(dev))
@@ -136,13 +173,7 @@ def speculative_signed_step(q, k, v, lo, hi, predicted, topk, mode="hybrid", mas
     if not 0 <= max_extra_mass <= 1:
         raise ValueError("max_extra_mass must be in [0,1]")
     gqa._shape(q, k, v, predicted)
-    if lo.ndim != 3 or hi.shape != lo.shape or lo.shape[0] != k.shape[0] or \
-            lo.shape[1:] != (k.shape[1], k.shape[3]):
-        raise ValueError("expected LO/HI[Hkv,N,D] matching K")
-    if lo.dtype != torch.float32 or hi.dtype != torch.float32:
-        raise ValueError("lo and hi must be FP32")
-    if any(x.device != q.device or not x.is_contiguous() for x in (lo, hi)):
-        raise ValueError("Q/LO/HI must be contiguous and on the same CUDA device")
+    _check_bounds(q, k, lo, hi)
     topk = int(topk)
     hq, d = q.shape
     hkv, n, b, _ = k.shape
@@ -161,7 +192,8 @@ def speculative_signed_step(q, k, v, lo, hi, predicted, topk, mode="hybrid", mas
         positive = torch.empty((hq,), device=dev, dtype=torch.int32)
         total = torch.empty_like(positive)
         ws = _lib.workspace(_lib.size("stk_step_workspace_bytes", hq, hkv, n, d, topk), dev)
-        _lib.call("stk_signed_step", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi), topk,
+        _lib.call("stk_signed_step", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi),
+                  _lib.bounds_code(lo, q), topk,
                   _lib.ptr(predicted), _lib.id_code(predicted), sp, 1 if mode == "hybrid" else 0,
                   float(mass_threshold), float(min_remaining), float(cancellation_tol),
                   float(max_extra_mass), _lib.ptr(selected), _lib.ptr(state.m),
@@ -170,7 +202,7 @@ def speculative_signed_step(q, k, v, lo, hi, predicted, topk, mode="hybrid", mas
                   _lib.ptr(total), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
         res = SignedRepairResult(out, fallback, remaining, approx, extra, positive, total)
         return SignedStepResult(selected, state, res)
-    selected = gqa.select_blocks(q, lo, hi, topk)
+    selected = select_blocks(q, lo, hi, topk)
     pred = kernels.speculate(q, k, v, predicted, mode, mass_threshold, keep_mass=True)
     res = signed_fused.repair_signed_fused(q, k, v, selected, predicted, pred, min_remaining,
                                            cancellation_tol, max_extra_mass)

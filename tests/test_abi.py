@@ -57,7 +57,7 @@ def test_host_only_queries(lib):
     assert L.stk_step_supported(2, 32, 8, 2048, 32, 96, 64, 64, 0) == 0    # D = 96
     assert lib.size("stk_select_workspace_bytes", 32, 8, 2048, 128, 64) >= 32 * 2048 * 8
     # argument errors are reported without touching a device
-    rc = L.stk_block_scores(None, 2, None, None, 4, 3, 10, 8, None, None)
+    rc = L.stk_block_scores(None, 2, None, None, 0, 4, 3, 10, 8, None, None)
     assert rc == -1 and b"divisible" in L.stk_last_error()
 
 
@@ -68,5 +68,5 @@ def test_noalloc_step_rejects_oversized_key_rows(lib):
     assert L.stk_step_noalloc_max_keys() == 1 << 19
     fake = ctypes.c_void_p(256)
     rc = L.stk_speculative_step_noalloc(fake, fake, fake, 2, 128, 8, 8192, 32, 128, fake, fake,
-                                        64, fake, 0, 64, 0, fake, fake, fake, fake, fake, None)
+                                        0, 64, fake, 0, 64, 0, fake, fake, fake, fake, fake, None)
     assert rc == -1 and b"524288" in L.stk_last_error()

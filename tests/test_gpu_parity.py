@@ -1115,3 +1115,75 @@ def test_masks_and_bounds_reject_host_tensors():
     with pytest.raises(ValueError, match="lo and hi"):
         bounds.append(lo.transpose(0, 1).contiguous().transpose(0, 1), hi,
                       k[:, 0, 0].contiguous(), 0, 0)
+
+
+@pytest.mark.parametrize("hq,hkv,n,b,d,topk,dtype", [
+    (32, 8, 2048, 32, 128, 64, torch.bfloat16),    # c3
+    (8, 4, 300, 16, 64, 20, torch.float16),
+    (8, 4, 300, 32, 256, 40, torch.bfloat16),
+])
+def test_16bit_bounds_give_the_same_results(hq, hkv, n, b, d, topk, dtype):
+    """Bounds kept in K's own 16-bit type are exact (min / max of 16-bit keys),
+    so every entry point that takes them returns exactly what it returns with
+    FP32 bounds: the builder, the append, the selection extension, the saved,
+    signed and allocation-free steps, and a paged batch."""
+    from stk_harness.configs import make_qkv, perturb
+    from strict_topk import bounds, gqa, paged, step
+    q, k, v, lo, hi = make_qkv(hq, hkv, d, b, n, dtype, True, 4040 + n)
+    ids = O.select_blocks(C.f64(q), lo.numpy(), hi.numpy(), topk)
+    p = perturb(torch.from_numpy(ids), n, topk, 0.75, 3)
+    qd, kd, vd, pd = dev(q, k, v, p)
+    lo32, hi32 = bounds.block_bounds(kd)
+    lo16, hi16 = bounds.block_bounds(kd, dtype=dtype)
+    assert lo16.dtype == dtype and torch.equal(lo16.float(), lo32) and torch.equal(hi16.float(), hi32)
+    assert torch.equal(lo32.cpu(), lo) and torch.equal(hi32.cpu(), hi)
+    sel32 = gqa.select_blocks(qd, lo32, hi32, topk)
+    assert torch.equal(step.select_blocks(qd, lo16, hi16, topk), sel32)
+    assert sel32.cpu().numpy().tolist() == ids.tolist()
+    r32 = step.speculative_step(qd, kd, vd, lo32, hi32, pd, topk)
+    r16 = step.speculative_step(qd, kd, vd, lo16, hi16, pd, topk)
+    for a, b_ in ((r32.selected, r16.selected), (r32.state.u, r16.state.u), (r32.output, r16.output)):
+        assert torch.equal(a, b_)
+    s32 = step.speculative_signed_step(qd, kd, vd, lo32, hi32, pd, topk, "hybrid", 0.2,
+                                       max_extra_mass=0.01)
+    s16 = step.speculative_signed_step(qd, kd, vd, lo16, hi16, pd, topk, "hybrid", 0.2,
+                                       max_extra_mass=0.01)
+    assert torch.equal(s32.selected, s16.selected)
+    for f in ("output", "fallback", "remaining", "total_jobs", "extra_mass_bound"):
+        assert torch.equal(getattr(s32.result, f), getattr(s16.result, f)), f
+    na = step.speculative_step_noalloc(qd, kd, vd, lo16, hi16, pd, topk)
+    assert torch.equal(na.selected, r32.selected) and torch.equal(na.output, r32.output)
+    ser = step.serial_step(qd, kd, vd, lo16, hi16, topk)
+    assert torch.equal(ser[0], sel32)
+    check(ser[1], O.attention(*np_(q, k, v), ids), "serial step, 16-bit bounds")
+    # a paged pool with 16-bit bounds
+    kv32 = paged.pack([(kd, vd)])
+    kv16 = paged.pack([(kd, vd)], bounds_dtype=dtype)
+    assert torch.equal(kv16.lo_pages.float(), kv32.lo_pages)
+    a32 = paged.speculative_step(qd[None], kv32, pd[None], topk)
+    a16 = paged.speculative_step(qd[None], kv16, pd[None], topk)
+    assert torch.equal(a32.selected, a16.selected) and torch.equal(a32.output, a16.output)
+    # append into 16-bit bounds equals append into FP32 bounds
+    kn = kd[:, 5, 3].contiguous()
+    bounds.append(lo32, hi32, kn, 5, 0)
+    bounds.append(lo16, hi16, kn, 5, 0)
+    bounds.append(lo32, hi32, kd[:, 5, 7].contiguous(), 5, 1)
+    bounds.append(lo16, hi16, kd[:, 5, 7].contiguous(), 5, 1)
+    assert torch.equal(lo16.float(), lo32) and torch.equal(hi16.float(), hi32)
+
+
+def test_16bit_bounds_select_unaligned_dims():
+    """The selection extension with 16-bit bounds on a head dimension that is
+    not a multiple of 64 (element-wise bound loads)."""
+    from strict_topk import gqa, step
+    gen = torch.Generator().manual_seed(12)
+    q = torch.randn((6, 48), generator=gen).half()
+    keys = torch.randn((3, 40, 8, 48), generator=gen).half()
+    lo, hi = keys.amin(2), keys.amax(2)
+    ref = O.select_blocks(*np_(q, lo.float(), hi.float()), 9)
+    qd, lod, hid = dev(q, lo, hi)
+    got = step.select_blocks(qd, lod, hid, 9)
+    assert got.cpu().numpy().tolist() == ref.tolist()
+    assert torch.equal(got, gqa.select_blocks(qd, lod.float(), hid.float(), 9))
+    with pytest.raises(ValueError, match="FP32"):
+        gqa.select_blocks(qd, lod, hid, 9)   # the reference contract stays FP32

@@ -39,7 +39,8 @@ def _noalloc(q, k, v, lo, hi, p, topk, union):
     sel = torch.full((hq, topk), -7, device=DEV, dtype=torch.int32)
     st = _allocate_state(hq, sp, d, q.device)
     out = torch.full((hq, d), float("nan"), device=DEV)
-    _lib.call("stk_speculative_step_noalloc", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi), topk,
+    _lib.call("stk_speculative_step_noalloc", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi),
+              _lib.bounds_code(lo, q), topk,
               _lib.ptr(p), _lib.id_code(p), sp, 1 if union else 0, _lib.ptr(sel),
               _lib.ptr(st.m), _lib.ptr(st.l), _lib.ptr(st.u), _lib.ptr(out),
               _lib.stream(q.device))
