@@ -70,6 +70,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=2400)
     ap.add_argument("--warmup", type=int, default=240)
     ap.add_argument("--config", default="c3", choices=("c2", "c3"))
+    ap.add_argument("--bounds", default="keys", choices=("keys", "fp32"),
+                    help="lo/hi of the fused step and the serial path: in K's own 16-bit "
+                         "type (exact, half the bytes) or FP32 (the reference's layout)")
     ap.add_argument("--overlap", type=float, default=0.9)
     ap.add_argument("--seed", type=int, default=20261103)
     ap.add_argument("--graph-steps", type=int, default=12,
@@ -161,6 +164,11 @@ def cpu_leg(args, step, c3_outs, cases):
     cpu = {"value": round(us, 1), "unit": "us/step", "cores": threads, "kind": "port",
            "sample": f"{steps} serial decode steps of {cfg.name} (torch fp32 CPU: "
                      "where/sum bound score, topk, gather-softmax attention)"}
+    log("bench: FP64 oracle cost (~5 s)")
+    o_us, o_steps = cpu_path.time_oracle(q, k, v, lo, hi, cfg.topk, budget_s=5.0)
+    cpu["fp64_oracle"] = {"value": round(o_us, 1), "unit": "us/step", "steps": o_steps,
+                          "sample": f"{o_steps} serial decode steps of {cfg.name} through the "
+                                    "FP64 numpy oracle (bound scores, top-K, attention)"}
     return parity, cpu
 
 
@@ -183,7 +191,8 @@ def main():
     M = divisor_at_most(args.steps, args.graph_steps)
     log(f"bench: {args.config} inputs, {M} device copies (seed {args.seed}, "
         f"overlap {args.overlap})")
-    step = decode.gqa_step(args.config, args.overlap, args.seed, dev, sets=M)
+    step = decode.gqa_step(args.config, args.overlap, args.seed, dev, sets=M,
+                           bounds=args.bounds)
     cfg = step.cfg
 
     def seq(fn, hot):
@@ -195,10 +204,14 @@ def main():
         for hot in (False, True):
             key = name + ("_hot" if hot else "")
             graphs[key], outs[key] = timing.capture(seq(fn, hot))
+    if args.bounds == "keys":
+        # the same two paths on the reference's FP32 bounds
+        for name, fn in (("fused_fp32_bounds", step.fused32), ("serial_fp32_bounds", step.serial32)):
+            graphs[name], outs[name] = timing.capture(seq(fn, False))
 
     # ---- the timed region: exactly --steps fused decode steps (cold)
     g = graphs["fused"]
-    warm = max(1, args.warmup // M)
+    warm = max(1, -(-args.warmup // M))   # whole replays, at least the requested steps
     reps = args.steps // M
     log(f"bench: {warm * M} warm-up + {reps * M} timed steps ({M} per graph replay)")
     for _ in range(warm):
@@ -322,16 +335,18 @@ def main():
     line = {
         "metric": "us/decode step full path (select+spec+repair) vs serial; HBM GB/s % of peak",
         "value": round(full_us, 3), "unit": "us/step", "n_gpus": 1, "steps": reps * M,
-        "warmup": warm * M, "ms_per_step": round(ms_per_step, 6), "higher_is_better": False,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "warmup_steps_run": warm * M,
         "data": "synthetic (seeded generators, hot blocks +1.5 along the group-mean query)",
         "config": {"workload": f"{cfg.name}: Hq={cfg.hq} Hkv={cfg.hkv} D={cfg.dim} "
                                f"B={cfg.block} N={cfg.blocks} K={cfg.topk} "
                                f"overlap={args.overlap}, fused select||speculate + "
                                "top-K/repair, inputs rotated over "
-                               f"{M} HBM copies",
+                               f"{M} HBM copies, lo/hi "
+                               f"{'in K dtype' if args.bounds == 'keys' else 'FP32'}",
                    "context": cfg.context, "topk": cfg.topk, "overlap": args.overlap,
-                   "seed": args.seed, "steps_per_graph": M},
+                   "seed": args.seed, "steps_per_graph": M, "bounds": args.bounds},
         "serial_us": per_step["serial"],
         "speedup_vs_serial": round(per_step["serial"] / per_step["fused"], 4),
         "paired_us_per_step": per_step,

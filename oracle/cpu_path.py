@@ -70,3 +70,24 @@ def time_serial(q, k, v, lo, hi, topk, budget_s=10.0, max_steps=2000):
         return el * 1e6 / steps, steps, threads
     finally:
         torch.set_num_threads(old)
+
+
+def time_oracle(q, k, v, lo, hi, topk, budget_s=5.0, max_steps=50):
+    """Time the FP64 oracle's serial step (bound scores in the fixed order,
+    top-K, FP64 attention over the selected blocks), the reference's own
+    FP64 torch path restated in numpy.  Returns (microseconds per step,
+    steps)."""
+    from . import stk_oracle as O
+    qn = q.double().numpy()
+    kn, vn = k.double().numpy(), v.double().numpy()
+    lon, hin = lo.double().numpy(), hi.double().numpy()
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        ids = O.select_blocks(qn, lon, hin, topk)
+        O.attention(qn, kn, vn, ids)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= max_steps:
+            break
+    return el * 1e6 / steps, steps

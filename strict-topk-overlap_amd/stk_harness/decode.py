@@ -10,7 +10,8 @@ once per decode step, from the actual IDs of the run):
   tile      = 2 * B * D * e            K and V of one (KV head, block), e = element bytes
   U_x       = unique (KV head, block) pairs read by pass x
   kv_bytes  = (U_spec + U_miss) * tile              (saved repair reads no wrong blocks)
-  meta      = 2 * Hkv * N * D * 4                   lo and hi, read once
+  meta      = 2 * Hkv * N * D * eb                  lo and hi, read once (eb = 4 for
+                                                    FP32 bounds, 2 for bounds in K's type)
   states    = Hq * SP * (D + 2) * 4                 speculative state write
             + Hq * hits * (D + 2) * 4               state read of the hits
   small     = Q + output + ID rows
@@ -73,7 +74,7 @@ class Bytes:
         return self.meta + self.serial_kv + self.small
 
 
-def byte_model(cfg, selected, predicted, elem_bytes):
+def byte_model(cfg, selected, predicted, elem_bytes, bound_bytes=4):
     g = cfg.hq // cfg.hkv
     tile = 2 * cfg.block * cfg.dim * elem_bytes
     sel = np.asarray(selected, dtype=np.int64)
@@ -90,7 +91,7 @@ def byte_model(cfg, selected, predicted, elem_bytes):
     return Bytes(
         kv_spec=unique_pairs(pred, g) * tile,
         kv_miss=u_miss * tile,
-        meta=2 * cfg.hkv * cfg.blocks * cfg.dim * 4,
+        meta=2 * cfg.hkv * cfg.blocks * cfg.dim * bound_bytes,
         states=cfg.hq * pred.shape[1] * st + hits * st,
         small=small,
         serial_kv=unique_pairs(sel, g) * tile,
@@ -104,15 +105,23 @@ class GqaStep:
     different addresses; step i of a captured sequence uses copy i % sets, so
     that a sequence larger than the caches (MI355X: 4 MB L2 per XCD, 256 MB
     Infinity Cache) reads its operands from HBM as a real decode loop does.
+    ``bounds``: "keys" keeps lo/hi in K's own 16-bit type (exact, half the
+    bytes) for the fused step and the serial path; "fp32" is the reference's
+    layout.  The drop-in composition (gqa.select_blocks) always reads the
+    FP32 copies (``sets32``), its contract.
     """
 
-    def __init__(self, cfg, overlap, seed, device, repair="auto", sets=1):
+    def __init__(self, cfg, overlap, seed, device, repair="auto", sets=1, bounds="keys"):
         self.cfg, self.overlap, self.seed = cfg, overlap, seed
         q, k, v, lo, hi = make_qkv(cfg.hq, cfg.hkv, cfg.dim, cfg.block, cfg.blocks, cfg.dtype,
                                    cfg.hot, seed)
         self.host = (q, k, v, lo, hi)
+        self.bounds = bounds
+        bdt = cfg.dtype if bounds == "keys" else torch.float32
         first = tuple(t.to(device) for t in (q, k, v, lo, hi))
-        self.sets = [first] + [tuple(t.clone() for t in first) for _ in range(sets - 1)]
+        self.sets32 = [first] + [tuple(t.clone() for t in first) for _ in range(sets - 1)]
+        self.sets = [(q_, k_, v_, lo_.to(bdt), hi_.to(bdt)) for q_, k_, v_, lo_, hi_ in
+                     self.sets32]
         self.q, self.k, self.v, self.lo, self.hi = first
         self.selected = gqa.select_blocks(self.q, self.lo, self.hi, cfg.topk)
         self.predicted = perturb(self.selected.cpu(), cfg.blocks, cfg.sp, overlap, seed).to(device)
@@ -124,7 +133,8 @@ class GqaStep:
 
     # -- phases on input copy i
     def select(self, i=0):
-        q, k, v, lo, hi = self.sets[i % len(self.sets)]
+        """The drop-in selection (FP32 bounds, the reference contract)."""
+        q, k, v, lo, hi = self.sets32[i % len(self.sets32)]
         return gqa.select_blocks(q, lo, hi, self.cfg.topk)
 
     def speculate(self, i=0):
@@ -145,18 +155,31 @@ class GqaStep:
         return overlap_run(lambda: self.select(i), lambda: self.speculate(i),
                            lambda a, st: self.finish(a, st, i), self.ss, self.ps)
 
-    def fused(self, i=0):
+    def fused(self, i=0, sets=None):
         """The same step in two launches on one stream (strict_topk.step)."""
-        q, k, v, lo, hi = self.sets[i % len(self.sets)]
+        sets = self.sets if sets is None else sets
+        q, k, v, lo, hi = sets[i % len(sets)]
         return step_mod.speculative_step(q, k, v, lo, hi, self.predicted, self.cfg.topk).output
 
-    def serial(self, i=0):
-        q, k, v, lo, hi = self.sets[i % len(self.sets)]
-        return gqa.exact(q, k, v, self.select(i))
+    def serial(self, i=0, sets=None):
+        """The same-work serial path: selection, then attention over it."""
+        sets = self.sets if sets is None else sets
+        q, k, v, lo, hi = sets[i % len(sets)]
+        return step_mod.serial_step(q, k, v, lo, hi, self.cfg.topk)[1]
+
+    def fused32(self, i=0):
+        return self.fused(i, self.sets32)
+
+    def serial32(self, i=0):
+        return self.serial(i, self.sets32)
+
+    def bound_bytes(self):
+        return self.sets[0][3].element_size()
 
     def bytes(self):
         e = torch.tensor([], dtype=self.cfg.dtype).element_size()
-        return byte_model(self.cfg, self.selected.cpu().numpy(), self.predicted.cpu().numpy(), e)
+        return byte_model(self.cfg, self.selected.cpu().numpy(), self.predicted.cpu().numpy(), e,
+                          self.bound_bytes())
 
     def front_bytes(self):
         """Algorithmic bytes of the select || speculate launch (k_front)."""
@@ -167,5 +190,6 @@ class GqaStep:
                 + c.hq * c.dim * e + c.hq * c.sp * 4)
 
 
-def gqa_step(name="c3", overlap=0.9, seed=20261103, device="cuda", repair="auto", sets=1):
-    return GqaStep(CONFIGS[name], overlap, seed, device, repair, sets)
+def gqa_step(name="c3", overlap=0.9, seed=20261103, device="cuda", repair="auto", sets=1,
+             bounds="keys"):
+    return GqaStep(CONFIGS[name], overlap, seed, device, repair, sets, bounds)
