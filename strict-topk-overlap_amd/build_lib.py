@@ -21,8 +21,9 @@ CSRC = ROOT / "csrc"
 OUT = ROOT / "strict_topk" / "libstrict_topk_hip.so"
 BUILD = ROOT / "_build"
 ARCH = "gfx950"
-SOURCES = ["api.cpp", "states.hip", "select.hip", "repair.hip", "signed.hip", "hier.hip", "sstep.hip", "bounds.hip", "indexer.hip", "paged.hip",
-           "step.hip"]
+SOURCES = ["api.cpp", "states.hip", "select.hip", "repair.hip", "signed.hip", "hier.hip", "sstep.hip",
+           "bounds.hip", "indexer.hip", "paged.hip", "step.hip", "tail_dense.hip", "front_pg.hip",
+           "tail_pg.hip", "stail_pg.hip"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
@@ -39,8 +40,19 @@ def hipcc():
     raise RuntimeError("hipcc not found")
 
 
+def _up_to_date(src: str, obj: Path) -> bool:
+    """STK_INCREMENTAL=1 (development only): an object newer than its source
+    and every header is kept."""
+    if not os.environ.get("STK_INCREMENTAL") or not obj.exists():
+        return False
+    deps = [CSRC / src, *CSRC.glob("*.hpp"), ROOT.parent / "include" / "strict_topk.h"]
+    return obj.stat().st_mtime > max(d.stat().st_mtime for d in deps)
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
+    if _up_to_date(src, obj):
+        return obj
     lang = ["-x", "hip"] if src.endswith(".hip") else []
     cmd = [hipcc(), *FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -117,9 +117,9 @@ STK_API int stk_paged_step(const void* q, const void* k_pages, const void* v_pag
   t.uni = union_mode ? 1 : 0; t.out = out;
   t.pg = f.pg;
   hipStream_t st = (hipStream_t)stream;
-  rc = launch::front<true>(dtype, f, plan.s, st);
+  rc = launch_front_pg(dtype, f, plan.s, st);
   if (rc) return rc;
-  return launch::tail<true>(dtype, t, plan.s, st);
+  return launch_tail_pg(dtype, t, plan.s, st);
 }
 
 STK_API int stk_paged_signed_step(const void* q, const void* k_pages, const void* v_pages,
@@ -164,9 +164,9 @@ STK_API int stk_paged_signed_step(const void* q, const void* k_pages, const void
   t.pos = positive; t.total = total;
   t.pg = f.pg;
   hipStream_t st = (hipStream_t)stream;
-  rc = launch::front<true>(dtype, f, plan.s, st);
+  rc = launch_front_pg(dtype, f, plan.s, st);
   if (rc) return rc;
-  return launch::stail<true>(dtype, t, plan.s, st);
+  return launch_stail_pg(dtype, t, plan.s, st);
 }
 
 }  // extern "C"

@@ -125,7 +125,7 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
     if (rc) return rc;
   }
   if (!tail) return STK_OK;
-  return launch::tail<false>(dtype, t, s, st);
+  return launch_tail(dtype, t, s, st);
 }
 
 STK_API int stk_speculative_step(const void* q, const void* k, const void* v, int dtype, int hq,

@@ -132,4 +132,13 @@ int stail(int dtype, const STailArgs& t, const StepShape& s, hipStream_t st) {
 }
 
 }  // namespace launch
+
+// Each instantiation set lives in one translation unit of its own (the
+// kernels are large and compile in parallel): launch_front (step.hip),
+// launch_tail (tail_dense.hip), launch_stail (sstep.hip) and their paged
+// counterparts (front_pg.hip, tail_pg.hip, stail_pg.hip).
+int launch_tail(int dtype, const TailArgs& t, const StepShape& s, hipStream_t st);
+int launch_front_pg(int dtype, const FrontArgs& f, const StepShape& s, hipStream_t st);
+int launch_tail_pg(int dtype, const TailArgs& t, const StepShape& s, hipStream_t st);
+int launch_stail_pg(int dtype, const STailArgs& t, const StepShape& s, hipStream_t st);
 }  // namespace stk

@@ -17,7 +17,7 @@
 // the merge.
 #pragma once
 
-#include "topk.hpp"
+#include "topk_bins.hpp"
 #include "tile2.hpp"
 
 namespace stk {
@@ -56,12 +56,12 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   __shared__ int map[kTailMapN];
   __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
   __shared__ float s_pm[kTailMaxK], s_pl[kTailMaxK];
-  __shared__ TopkLds tl;
+  __shared__ TopkBinsLds tb;
+  __shared__ int s_scan[kTailWaves];
   // the hits' partial sums, one row per wave (relative to the wave's max)
   __shared__ float s_hmax[kTailWaves], s_hl[kTailWaves];
   __shared__ __align__(16) float s_hu[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_wu[kTailWaves][D];
-  __shared__ int spg[PG ? kTailMaxK : 1];   // PG: pages of the selected blocks
   __shared__ int mtk[PG ? kTailMaxK : 1];   // PG: tokens of each listed miss
   const int h = blockIdx.x;
   const int nrow = a.kv.n, sp = a.sp;
@@ -100,7 +100,8 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
     const int64_t row = (int64_t)h * sp + (r < sp ? r : 0);
     uu[j] = *reinterpret_cast<const float4*>(a.pu + row * D + 4 * c4);
   }
-  // ---- membership map: max predicted slot + 1 per block ID
+  // ---- membership map (max predicted slot + 1 per block ID), cleared here
+  // and filled between the top-K's first two barriers
   for (int i = tid; i < n; i += kTailThreads) map[i] = 0;
   // every slot entry is written (empty past sp): the row sums below read
   // entries past sp with zero weight, and LDS holds whatever an earlier
@@ -110,38 +111,58 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
     s_pm[tid] = pmv;
     s_pl[tid] = plv;
   }
-  __syncthreads();
-  if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
-  // ---- exact top-K (its first barrier orders the map writes above)
-  if (!PG || kk > 0)
-    topk_select_keys<KPT>(key, n, kk, tl, [&](int pos, int idx, int i) {
-      sel[pos] = idx;
-      if constexpr (PG) spg[pos] = pgk[i];
-      atomicOr(&map[idx], kSelFlag);
-    });
-  __syncthreads();
-  // ---- misses (selected, not predicted) in ascending block order, listed
-  // by every wave for itself: wave w keeps misses w, w + 8, ... (its own
-  // entries of the list, read back only by it) and the count
-  // (PG: a miss on an invalid page or with no tokens has the empty state and
-  // is not listed; the list holds the misses' pages instead of their IDs, and
-  // their token counts beside them)
-  int nm = 0;
-  for (int p0 = 0; p0 < kk; p0 += STK_WAVE) {
-    const int p = p0 + lane_id();
-    const bool in = p < kk;
-    const int id = in ? sel[p] : 0;
-    const int mp = PG ? (in ? spg[p] : -1) : id;
-    const int mt = PG ? pg_block_tokens(rtok, id, a.kv.b) : 0;
-    const bool ms = in && (map[id] & ~kSelFlag) == 0 && (!PG || (mp >= 0 && mt > 0));
-    const uint64_t bal = __ballot(ms);
-    const int x = nm + (int)__popcll(bal & lanemask_lt());
-    if (ms && x % kTailWaves == w) {
-      miss[x] = mp;
-      if constexpr (PG) mtk[x] = mt;
-    }
-    nm += (int)__popcll(bal);
+  auto fill_map = [&] {
+    if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
+  };
+  // ---- exact top-K: a bit per selected key of this thread
+  uint32_t flags = 0;
+  if (!PG || kk > 0) {
+    flags = topk_bins_flags<KPT>(key, n, kk, tb, fill_map);
+  } else {
+    __syncthreads();
+    fill_map();
   }
+  // ---- ranks: selected IDs in ascending block order, and the misses
+  // (selected, not predicted) among them in the same order, from one scan
+  // of packed counts (PG: a miss on an invalid page or with no tokens has
+  // the empty state and is not listed; the list holds the misses' pages
+  // instead of their IDs, and their token counts beside them)
+  uint32_t mflags = 0;
+  int mtok[PG ? KPT : 1];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int idx = tid * KPT + i;
+    const bool on = (flags >> i) & 1u;
+    const int mv = map[on ? idx : 0];
+    bool ms = on && mv == 0;
+    if constexpr (PG) {
+      mtok[i] = pg_block_tokens(rtok, idx, a.kv.b);
+      ms = ms && pgk[i] >= 0 && mtok[i] > 0;
+    }
+    mflags |= (uint32_t)ms << i;
+  }
+  int total;
+  const int pre = block_excl_scan1(__popc(flags) | (__popc(mflags) << 16), s_scan, &total);
+  int pos = pre & 0xffff, mpos = pre >> 16;
+  const int nm = total >> 16;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int idx = tid * KPT + i;
+    if ((flags >> i) & 1u) {
+      sel[pos++] = idx;
+      map[idx] |= kSelFlag;   // this thread's block: no other writer
+    }
+    if ((mflags >> i) & 1u) {
+      if constexpr (PG) {
+        miss[mpos] = pgk[i];
+        mtk[mpos] = mtok[i];
+      } else {
+        miss[mpos] = idx;
+      }
+      ++mpos;
+    }
+  }
+  __syncthreads();
   // ---- round trip 2: wave w streams misses w, w + 8, ...; the first
   // tile's loads are issued before the hits' arithmetic
   const int kvh = PG ? kvp : h / G;
@@ -164,17 +185,28 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   // saved mode takes slot p when P[p] is selected and p is the highest slot
   // holding that block; union mode takes every slot.  Each wave sums its
   // rows relative to its own maximum (no barrier); the merge rescales.
+  // (every LDS read is issued unconditionally, from clamped indices, so the
+  // rows' reads go out together instead of one dependent round trip each)
   bool used[RPT];
-  float um[RPT];
-  float hm = -INFINITY;
+  float um[RPT], ul[RPT];
+  int pv[RPT];
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int r = rg + RG * j;   // < 16 * RG <= 512
     const int rr = r < kTailMaxK ? r : 0;
-    const int pv = pids[rr];
-    const int mv = pv >= 0 && pv < n ? map[pv] : 0;
-    used[j] = r < sp && (a.uni || ((mv & kSelFlag) && (mv & ~kSelFlag) == r + 1));
+    pv[j] = pids[rr];
     um[j] = s_pm[rr];
+    ul[j] = s_pl[rr];
+  }
+  float hm = -INFINITY;
+  const int nlast = n > 0 ? n - 1 : 0;
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int r = rg + RG * j;
+    const bool inr = (pv[j] >= 0) & (pv[j] < n);
+    const int mv = map[pv[j] < 0 ? 0 : (pv[j] > nlast ? nlast : pv[j])];
+    const bool hit = ((mv & kSelFlag) != 0) & ((mv & ~kSelFlag) == r + 1);
+    used[j] = (r < sp) & inr & ((a.uni != 0) | hit);
     hm = used[j] ? fmaxf(hm, um[j]) : hm;
   }
   hm = wave_max_u(hm);
@@ -186,7 +218,7 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
     const float wt = used[j] ? wexp(um[j], hm) : 0.f;
     // rows past sp were loaded from row 0 (or a stand-in buffer): zero them
     const float4 ur = r < sp ? uu[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-    hl += wt * s_pl[r < kTailMaxK ? r : 0];
+    hl += wt * ul[j];
     hu.x += wt * ur.x; hu.y += wt * ur.y; hu.z += wt * ur.z; hu.w += wt * ur.w;
   }
   // fold the row groups of this wave (lanes with the same columns)

@@ -1,0 +1,182 @@
+// Exact top-K of one row of order-preserving 64-bit keys by value bins, for
+// a whole workgroup of full waves (the tails of the fused steps).
+//
+// Contract: the k largest (key, -index) pairs, so ties go to the lower index
+// (the contract of topk.hpp).  Result: a bit mask per thread, bit i set when
+// the thread's key i is selected; the caller ranks the selected indices.
+//
+// Method, built for latency (a tail is one workgroup per head, and every
+// step of the selection is on its critical path):
+//   A  the row's range: per-wave max / min of the keys' high 32 bits (DPP),
+//      one barrier;
+//   B  a 1024-bin histogram, linear in the score value over that range
+//      (bin = (s - lo) * 1024 / (hi - lo) in FP32, clamped), one LDS atomic
+//      per key on mostly distinct addresses, one barrier;
+//   C  every wave reads the whole histogram and finds the threshold bin t
+//      (keys above it, keys in it) with two DPP scans, so no barrier;
+//   D  if bin t is taken whole, done; otherwise its keys (a few) are listed
+//      in LDS and every wave ranks them by (key, -index) from registers,
+//      one barrier.
+// The bin map is monotone non-decreasing in the key (every rounding step is
+// monotone, NaN keys, whose key is 0, go to bin 0), so the selection is the
+// exact one whatever the ranges and roundings are.  Rows whose range is
+// empty or not finite, or whose threshold bin holds more than 64 keys, take
+// the radix select of topk.hpp instead (the decision is the same in every
+// wave).
+#pragma once
+
+#include "topk.hpp"
+
+namespace stk {
+
+constexpr int kBins = 1024;
+constexpr int kBinCands = 64;
+
+struct TopkBinsLds {
+  __align__(16) int hist[kBins];
+  uint32_t red[2][16];     // per-wave max / min of the keys' high words
+  int ncand;
+  uint64_t ck[kBinCands];
+  int ci[kBinCands];
+  TopkLds radix;           // the fallback's scratch
+};
+
+// The double a key stands for, as FP32 (monotone; NaN for key 0).
+__device__ __forceinline__ float key_value(uint64_t key) {
+  const uint64_t b = (key >> 63) ? (key & 0x7fffffffffffffffull) : ~key;
+  return (float)__longlong_as_double((long long)b);
+}
+
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_ext_u32(uint32_t v) {
+  const int id = MAX ? 0 : -1;
+  auto f = [&](uint32_t x, int y) {
+    return MAX ? (x > (uint32_t)y ? x : (uint32_t)y) : (x < (uint32_t)y ? x : (uint32_t)y);
+  };
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0xB1, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x4E, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x141, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x140, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x142, 0xa, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x143, 0xc, 0xf, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Phase A's LDS words must be free when it starts (a barrier since their
+// last use).  `between` runs after barrier A and before barrier B, for the
+// caller's own LDS writes that must follow a clear done before A.
+template <int KPT, typename BETWEEN>
+__device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], int n, int k,
+                                                    TopkBinsLds& L, BETWEEN between) {
+  const int nwaves = blockDim.x / STK_WAVE;
+  const int base = threadIdx.x * KPT;
+  const int lane = lane_id();
+  // ---- A: range of the finite-or-infinite, non-NaN keys (key 0 is NaN)
+  uint32_t hmax = 0u, hmin = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const bool ok = base + i < n && key[i] != 0ull;
+    const uint32_t hw = (uint32_t)(key[i] >> 32);
+    hmax = ok && hw > hmax ? hw : hmax;
+    hmin = ok && hw < hmin ? hw : hmin;
+  }
+  hmax = wave_ext_u32<true>(hmax);
+  hmin = wave_ext_u32<false>(hmin);
+  if (lane == 0) {
+    L.red[0][wave_id()] = hmax;
+    L.red[1][wave_id()] = hmin;
+  }
+  for (int i = threadIdx.x; i < kBins; i += blockDim.x) L.hist[i] = 0;
+  if (threadIdx.x == 0) L.ncand = 0;
+  __syncthreads();
+  between();
+  hmax = 0u;
+  hmin = 0xffffffffu;
+  for (int w = 0; w < nwaves; ++w) {
+    hmax = L.red[0][w] > hmax ? L.red[0][w] : hmax;
+    hmin = L.red[1][w] < hmin ? L.red[1][w] : hmin;
+  }
+  const float lo = key_value((uint64_t)hmin << 32);
+  const float hi = key_value(((uint64_t)hmax << 32) | 0xffffffffull);
+  const float range = hi - lo;
+  const bool binned = hmin <= hmax && range > 0.f && range <= 3.0e38f;
+  uint32_t flags = 0;
+  if (binned) {
+    // ---- B: histogram
+    const float inv = (float)kBins / range;
+    int bin[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const float x = (key_value(key[i]) - lo) * inv;   // NaN for key 0
+      bin[i] = x >= (float)(kBins - 1) ? kBins - 1 : (x > 0.f ? (int)x : 0);
+      if (base + i < n) atomicAdd(&L.hist[bin[i]], 1);
+    }
+    __syncthreads();
+    // ---- C: threshold bin, every wave alike.  Lane l sums bins
+    // [kBins - 16 (l + 1), kBins - 16 l), lane 0 the top ones.
+    const int4* h4 = reinterpret_cast<const int4*>(L.hist + kBins - 16 * (lane + 1));
+    const int4 b0 = h4[0], b1 = h4[1], b2 = h4[2], b3 = h4[3];
+    const int s = b0.x + b0.y + b0.z + b0.w + b1.x + b1.y + b1.z + b1.w + b2.x + b2.y + b2.z +
+                  b2.w + b3.x + b3.y + b3.z + b3.w;
+    const int cum = wave_incl_scan_dpp(s);
+    const int L16 = __ffsll((long long)__ballot(cum >= k)) - 1;
+    const int above16 = __builtin_amdgcn_readlane(cum - s, L16);
+    // the 16 bins of lane L16, top first, on lanes 0..15
+    const int v = lane < 16 ? L.hist[kBins - 16 * L16 - 1 - lane] : 0;
+    int c = v;
+    c += __builtin_amdgcn_update_dpp(0, c, 0x111, 0xf, 0xf, true);
+    c += __builtin_amdgcn_update_dpp(0, c, 0x112, 0xf, 0xf, true);
+    c += __builtin_amdgcn_update_dpp(0, c, 0x114, 0xf, 0xf, true);
+    c += __builtin_amdgcn_update_dpp(0, c, 0x118, 0xf, 0xf, true);
+    const int J = __ffsll((long long)(__ballot(lane < 16 && above16 + c >= k))) - 1;
+    const int t = kBins - 16 * L16 - 1 - J;
+    const int cnt = __builtin_amdgcn_readlane(v, J);
+    const int need = k - (above16 + __builtin_amdgcn_readlane(c, J) - cnt);
+    if (cnt == need) {
+#pragma unroll
+      for (int i = 0; i < KPT; ++i)
+        flags |= (uint32_t)(base + i < n && bin[i] >= t) << i;
+      return flags;
+    }
+    if (cnt <= kBinCands) {
+      // ---- D: rank the threshold bin's keys
+#pragma unroll
+      for (int i = 0; i < KPT; ++i)
+        if (base + i < n && bin[i] == t) {
+          const int x = atomicAdd(&L.ncand, 1);
+          L.ck[x] = key[i];
+          L.ci[x] = base + i;
+        }
+      __syncthreads();
+      const uint64_t kc = lane < cnt ? L.ck[lane] : 0ull;
+      const int ic = lane < cnt ? L.ci[lane] : 0x7fffffff;
+      int rank = 0;
+      for (int j = 0; j < cnt; ++j) {
+        const uint32_t jh = (uint32_t)__builtin_amdgcn_readlane((int)(kc >> 32), j);
+        const uint32_t jl = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kc, j);
+        const int ij = __builtin_amdgcn_readlane(ic, j);
+        const uint64_t kj = ((uint64_t)jh << 32) | jl;
+        rank += (kj > kc) || (kj == kc && ij < ic);
+      }
+      const int star = __ffsll((long long)__ballot(lane < cnt && rank == need - 1)) - 1;
+      const uint64_t ks = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(kc >> 32), star)
+                           << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kc, star);
+      const int is = __builtin_amdgcn_readlane(ic, star);
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const bool sel = bin[i] > t ||
+                         (bin[i] == t && (key[i] > ks || (key[i] == ks && base + i <= is)));
+        flags |= (uint32_t)(base + i < n && sel) << i;
+      }
+      return flags;
+    }
+  } else {
+    __syncthreads();   // as barrier B: the caller's writes in `between` are ordered
+  }
+  // ---- fallback: the radix select
+  topk_select_keys<KPT>(key, n, k, L.radix, [&](int, int, int i) { flags |= 1u << i; });
+  return flags;
+}
+
+}  // namespace stk
