@@ -10,11 +10,17 @@
 //   1. the head's keys, its predicted row, its query row and every predicted
 //      state (m, l, u) are requested together at entry;
 //   2. the missed blocks' K/V tiles, once the top-K is known.
-// In between: top-K (two barriers per radix pass), membership through an
-// LDS map over block IDs (max predicted slot + 1, plus a selected flag),
-// each wave's own misses (their tile loads go out at once), and the hits'
-// LSE partial sums from registers, per wave, with no further barrier before
-// the merge.
+// In between: top-K by value bins (topk_bins.hpp), membership through an
+// LDS map over block IDs (max predicted slot + 1, plus a selected flag), one
+// packed scan that ranks the selected IDs and lists the misses (wave w
+// takes misses w, w + 8, ...; their tile loads go out at once), and the
+// hits' LSE partial sums from registers, per wave, with no further barrier
+// before the merge.
+//
+// Cost model: a wave64 VALU instruction occupies a SIMD for 4 cycles and the
+// 8 waves share 4 SIMDs, so every instruction on the path costs about 8
+// cycles; the phases are kept short in instructions, LDS reads are issued
+// together from clamped indices rather than under branches.
 #pragma once
 
 #include "topk_bins.hpp"

@@ -20,9 +20,10 @@
 // inputs allow):
 //   1. keys, predicted row, query row and every predicted state (m, l, u);
 //      the u rows stay in registers (RPT rows of four columns per thread);
-//   2. top-K; then every wave lists its own misses and issues their tile
-//      loads at once (wave w takes misses w, w + 8, ..., two tiles in
-//      flight), and wave 0 does the per-slot work (grouping, membership,
+//   2. top-K (value bins, topk_bins.hpp) and one packed scan that ranks the
+//      selected IDs and lists the misses; every wave issues the tile loads
+//      of its misses at once (wave w takes misses w, w + 8, ..., two tiles
+//      in flight), and wave 0 does the per-slot work (grouping, membership,
 //      keep / low / wrong sets, the extra-mass test) while they travel;
 //   3. the partial sums of the registered u rows: the kept states, the low
 //      aggregate with its envelope, and the wrong low blocks' corrections.
@@ -40,7 +41,7 @@
 
 #include <type_traits>
 
-#include "topk.hpp"
+#include "topk_bins.hpp"
 #include "tile2.hpp"
 #include "tail.hpp"
 
@@ -76,7 +77,8 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   __shared__ int map[kTailMapN];
   __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
   __shared__ float s_pm[kTailMaxK], s_pl[kTailMaxK];
-  __shared__ TopkLds tl;
+  __shared__ TopkBinsLds tb;
+  __shared__ int s_scan[kTailWaves];
   __shared__ int s_nw, s_lowhit, s_skip, s_bad;
   __shared__ float s_lowm, s_ll, s_mk, s_mu, s_extra;
   __shared__ uint64_t s_keep[SW], s_low[SW], s_wrong[SW], s_used[SW];
@@ -90,7 +92,6 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   __shared__ __align__(16) float s_su[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves];
   __shared__ float s_wu[kTailWaves][D];
-  __shared__ int spg[PG ? kTailMaxK : 1];   // PG: pages of the selected blocks
   __shared__ int mtk[PG ? kTailMaxK : 1];   // PG: tokens of each listed miss
   const int h = blockIdx.x;
   const int nrow = a.kv.n, sp = a.sp;
@@ -128,7 +129,8 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     const int64_t row = (int64_t)h * sp + (r < sp ? r : 0);
     uu[j] = *reinterpret_cast<const float4*>(a.pu + row * D + 4 * c4);
   }
-  // ---- membership map: max predicted slot + 1 per block ID
+  // ---- membership map (max predicted slot + 1 per block ID), cleared here
+  // and filled between the top-K's first two barriers
   for (int i = tid; i < n; i += kTailThreads) map[i] = 0;
   // every slot entry is written (empty past sp): the row sums below read
   // entries past sp with zero weight, and LDS holds whatever an earlier
@@ -139,15 +141,57 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     s_pl[tid] = plv;
   }
   if (tid == 0) s_bad = 0;
-  __syncthreads();
-  if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
-  // ---- exact top-K (its first barrier orders the map writes above)
-  if (!PG || kk > 0)
-    topk_select_keys<KPT>(key, n, kk, tl, [&](int pos, int idx, int i) {
-      sel[pos] = idx;
-      if constexpr (PG) spg[pos] = pgk[i];
-      atomicOr(&map[idx], kSelFlag);
-    });
+  auto fill_map = [&] {
+    if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
+  };
+  // ---- exact top-K: a bit per selected key of this thread
+  uint32_t flags = 0;
+  if (!PG || kk > 0) {
+    flags = topk_bins_flags<KPT>(key, n, kk, tb, fill_map);
+  } else {
+    __syncthreads();
+    fill_map();
+  }
+  // ---- ranks: selected IDs in ascending block order, and the misses
+  // (selected, not predicted) among them in the same order, from one scan
+  // of packed counts (PG: a miss on an invalid page or with no tokens has
+  // the empty state and is not listed; the list holds the misses' pages
+  // instead of their IDs, and their token counts beside them)
+  uint32_t mflags = 0;
+  int mtok[PG ? KPT : 1];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int idx = tid * KPT + i;
+    const bool on = (flags >> i) & 1u;
+    const int mv = map[on ? idx : 0];
+    bool ms = on && mv == 0;
+    if constexpr (PG) {
+      mtok[i] = pg_block_tokens(rtok, idx, a.kv.b);
+      ms = ms && pgk[i] >= 0 && mtok[i] > 0;
+    }
+    mflags |= (uint32_t)ms << i;
+  }
+  int total;
+  const int pre = block_excl_scan1(__popc(flags) | (__popc(mflags) << 16), s_scan, &total);
+  int spos = pre & 0xffff, mpos = pre >> 16;
+  const int nm = total >> 16;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int idx = tid * KPT + i;
+    if ((flags >> i) & 1u) {
+      sel[spos++] = idx;
+      map[idx] |= kSelFlag;   // this thread's block: no other writer
+    }
+    if ((mflags >> i) & 1u) {
+      if constexpr (PG) {
+        miss[mpos] = pgk[i];
+        mtk[mpos] = mtok[i];
+      } else {
+        miss[mpos] = idx;
+      }
+      ++mpos;
+    }
+  }
   __syncthreads();
   // ---- per-slot work (wave 0), lane l holding slots l, l + 64, ...; SWN
   // slot words, one when SP <= 64 (a single wave runs this part alone, so
@@ -264,29 +308,6 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
     for (int c = SWN; c < SW; ++c)
       if (lane_id() == 0) s_keep[c] = s_low[c] = s_wrong[c] = s_used[c] = 0ull;
   };
-  // ---- misses (selected, not predicted) in ascending block order, listed
-  // by every wave for itself: wave w keeps misses w, w + 8, ... (its own
-  // entries of the list, read back only by it) and the count, so its tile
-  // loads go out before the per-slot work and the barrier below
-  // (PG: a miss on an invalid page or with no tokens has the empty state and
-  // is not listed; the list holds the misses' pages instead of their IDs, and
-  // their token counts beside them)
-  int nm = 0;
-  for (int p0 = 0; p0 < kk; p0 += STK_WAVE) {
-    const int p = p0 + lane_id();
-    const bool in = p < kk;
-    const int id = in ? sel[p] : 0;
-    const int mp = PG ? (in ? spg[p] : -1) : id;
-    const int mt = PG ? pg_block_tokens(rtok, id, a.kv.b) : 0;
-    const bool ms = in && (map[id] & ~kSelFlag) == 0 && (!PG || (mp >= 0 && mt > 0));
-    const uint64_t bal = __ballot(ms);
-    const int x = nm + (int)__popcll(bal & lanemask_lt());
-    if (ms && x % kTailWaves == w) {
-      miss[x] = mp;
-      if constexpr (PG) mtk[x] = mt;
-    }
-    nm += (int)__popcll(bal);
-  }
   // ---- round trip 2: wave w streams misses w, w + 8, ..., two tiles in
   // flight when they fit
   const int kvh = PG ? kvp : h / G;
