@@ -392,6 +392,42 @@ int stk_paged_signed_step(const void* q, const void* k_pages, const void* v_page
                           int32_t* positive, int32_t* total, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/* ---- Host-backed cache (docs/hisparse_integration.md:11-27: a pinned host
+ * KV pool, a device working set per request, swap-in of the selected blocks
+ * that are not resident, speculation on the resident predicted blocks
+ * P n R only).  Layout, all device memory unless said otherwise:
+ *   host_k, host_v [host_pages, B, D]  pinned host memory the GPU reads in
+ *                                      place (hipHostMalloc)
+ *   lo_pages, hi_pages [host_pages, D] every block's bounds (bounds_dtype)
+ *   host_table [R, Hkv, nb] int32      host page of logical block j
+ *   k_slots, v_slots [R * Hkv * C, B, D]  device slots; group r * Hkv + kvh
+ *                                      owns slots [g * C, g * C + C)
+ *   table [R, Hkv, nb] int32           device slot of block j, or -1
+ *   slot_block [R * Hkv * C] int32     block a slot holds, or -1
+ *   slot_stamp [R * Hkv * C] int32     step of a slot's last use
+ *   clock [1] int32                    step counter (advanced by each step)
+ *   nblocks, ntokens [R]               as in the paged format
+ * One step (four launches): scores of every block || prediction states of
+ * the resident predicted blocks (a non-resident one has the empty state);
+ * the top-K; swap-in per (request, KV head): selected blocks without a slot
+ * take the least recently used slots not needed this step (free ones first)
+ * and are copied from the host pool, *h2d_bytes grows by the bytes copied;
+ * then the strict repair from the slots.  Outputs as stk_paged_step, over
+ * the request's selected set A.  Needs G * topk <= C <= 1024, nb <= 8192,
+ * bf16 / fp16.  The reference has no such kernels (it describes the design
+ * for SGLang's HiSparse); this is its native form here. */
+size_t stk_cache_workspace_bytes(int requests, int hq, int nb);
+
+int stk_cache_step(const void* q, int dtype, int requests, int hq, int hkv, int nb, int b, int d,
+                   void* k_slots, void* v_slots, int slots_per_group, const void* host_k,
+                   const void* host_v, int host_pages, const void* lo_pages,
+                   const void* hi_pages, int bounds_dtype, const int32_t* host_table,
+                   int32_t* table, int32_t* slot_block, int32_t* slot_stamp, int32_t* clock,
+                   const int32_t* nblocks, const int32_t* ntokens, int topk,
+                   const int32_t* predicted, int sp, int32_t* selected, float* m, float* l,
+                   float* u, float* out, unsigned long long* h2d_bytes, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

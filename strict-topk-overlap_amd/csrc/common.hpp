@@ -107,13 +107,31 @@ __device__ __forceinline__ X ld_or(const X* p, int64_t i, bool ok, X other) {
 // ntok[r], so a request's last block may be partly filled (the tokens past
 // the count are never weighted, whatever the page holds there); without it
 // every block holds B tokens.
+//
+// btable (optional) gives the scorer its own table into the lo/hi pages, of
+// bpages rows: with a host-backed cache, K/V pages are resident for only
+// some blocks (table holds -1 for the others, whose blocks then have the
+// empty state), while every block's bounds stay on the device and every
+// block is scored.  Without btable the scorer uses table.
 struct Paging {
   const int32_t* table;
   const int32_t* nblk;
   int hkv_req;
   int pages;
   const int32_t* ntok;
+  const int32_t* btable;
+  int bpages;
 };
+
+// Bounds row of block j of KV row kv when ok, else -1 (the load always
+// issued, as in pg_page).
+__device__ __forceinline__ int pg_bounds_row(const Paging& pg, int kv, int n, int64_t j,
+                                             bool ok) {
+  const int32_t* t = pg.btable ? pg.btable : pg.table;
+  const int lim = pg.btable ? pg.bpages : pg.pages;
+  const int p = ld_or(t, (int64_t)kv * n + j, ok, -1);
+  return (p >= 0 && p < lim) ? p : -1;
+}
 
 // Valid blocks of KV row kv, clamped to [0, n].
 __device__ __forceinline__ int pg_blocks(const Paging& pg, int kv, int n) {

@@ -85,7 +85,7 @@ static int paged_common(const void* q, const void* k_pages, const void* v_pages,
            stk_align((size_t)requests * hq * nb * sizeof(uint64_t));
   *f = make_front_args(q, k_pages, v_pages, dtype, plan->hq, plan->hkv, nb, b, d, lo_pages,
                        hi_pages, bounds_dtype != 0, predicted, sp, m, l, u, *keys, plan->s);
-  f->pg = Paging{table, nblocks, hkv, pages, ntokens};
+  f->pg = Paging{table, nblocks, hkv, pages, ntokens, nullptr, 0};
   return STK_OK;
 }
 

@@ -134,7 +134,7 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       const int nb = wave_base + 4 * s + sub;
-      pgs[s] = pg_page(pg, kv, a.n, nb, nb < a.n);
+      pgs[s] = pg_bounds_row(pg, kv, a.n, nb, nb < a.n);
     }
   }
   const int nv = PG ? pg_blocks(pg, kv, a.n) : a.n;   // blocks of this row

@@ -117,8 +117,11 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
     s_pm[tid] = pmv;
     s_pl[tid] = plv;
   }
+  // a predicted slot counts only with a state: a slot whose state is empty
+  // (its block had no resident page when the front ran, as with a host-backed
+  // cache) is recomputed like a miss when its block is selected
   auto fill_map = [&] {
-    if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
+    if (tid < sp && pid >= 0 && pid < n && pmv != -INFINITY) atomicMax(&map[pid], tid + 1);
   };
   // ---- exact top-K: a bit per selected key of this thread
   uint32_t flags = 0;
