@@ -81,7 +81,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU leg (CPU baseline and oracle parity)")
     ap.add_argument("--no-suite", action="store_true", help="time c3 only")
-    ap.add_argument("--suite", default="c1,c2,c4,c5,c3sweep",
+    ap.add_argument("--suite", default="c1,c2,c4,c5,c3sweep,cache",
                     help="comma-separated configs timed beside c3")
     return ap.parse_args()
 

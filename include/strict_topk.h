@@ -407,16 +407,18 @@ int stk_paged_signed_step(const void* q, const void* k_pages, const void* v_page
  *   slot_stamp [R * Hkv * C] int32     step of a slot's last use
  *   clock [1] int32                    step counter (advanced by each step)
  *   nblocks, ntokens [R]               as in the paged format
- * One step (four launches): scores of every block || prediction states of
+ * One step (five launches): scores of every block || prediction states of
  * the resident predicted blocks (a non-resident one has the empty state);
  * the top-K; swap-in per (request, KV head): selected blocks without a slot
  * take the least recently used slots not needed this step (free ones first)
- * and are copied from the host pool, *h2d_bytes grows by the bytes copied;
+ * and are copied from the host pool by a copy kernel, *h2d_bytes grows by the
+ * bytes copied;
  * then the strict repair from the slots.  Outputs as stk_paged_step, over
- * the request's selected set A.  Needs G * topk <= C <= 1024, nb <= 8192,
+ * the request's selected set A; sp = 0 (predicted, m, l, u may be null) is
+ * the serial path: select, swap-in, then the exact attention over A.  Needs G * topk <= C <= 1024, nb <= 8192,
  * bf16 / fp16.  The reference has no such kernels (it describes the design
  * for SGLang's HiSparse); this is its native form here. */
-size_t stk_cache_workspace_bytes(int requests, int hq, int nb);
+size_t stk_cache_workspace_bytes(int requests, int hq, int hkv, int nb);
 
 int stk_cache_step(const void* q, int dtype, int requests, int hq, int hkv, int nb, int b, int d,
                    void* k_slots, void* v_slots, int slots_per_group, const void* host_k,

@@ -21,7 +21,7 @@
 //   slot_stamp [R * Hkv * C]           step of the slot's last use (LRU)
 //   clock [1]                          step counter, advanced once a step
 //
-// One step is four launches on one stream:
+// One step is five launches on one stream:
 //   k_front (paged)  bound scores of every block (bounds table = host_table)
 //                    || prediction states of the resident predicted blocks
 //                    (P n R: a predicted block without a slot gets the empty
@@ -31,8 +31,12 @@
 //   k_swap_in        per group: the union of its heads' selected blocks;
 //                    resident ones are stamped, missing ones take the least
 //                    recently used slots not needed this step (free slots
-//                    first) and are copied from the host pool into them;
+//                    first), the table is updated and the copies listed;
 //                    H2D bytes are counted;
+//   k_swap_copy      the listed host pages into their slots, 16 workgroups
+//                    per group with several 16-byte loads in flight per
+//                    thread (host reads cross PCIe: their latency needs many
+//                    bytes in flight);
 //   k_tail (paged)   the repair: a predicted block with a state that is
 //                    selected is a hit, every other selected block (A \ P
 //                    and A n (P \ R)) is computed from its slot.
@@ -46,6 +50,7 @@ namespace {
 constexpr int kSwapThreads = 256;
 constexpr int kMaxSlots = 1024;     // slots per group
 constexpr int kMaxNeed = 1024;      // distinct selected blocks per group
+constexpr int kSlotsPerThread = kMaxSlots / kSwapThreads;
 
 struct SelArgs {
   const uint64_t* keys;   // [R * Hq, NB]
@@ -76,6 +81,9 @@ __global__ __launch_bounds__(kTailThreads) void k_cache_select(SelArgs a) {
   if (h == 0 && tid == 0) atomicAdd(a.clock, 1);
 }
 
+constexpr int kCopyWGs = 16;        // copy workgroups per group
+constexpr int kCopyUnroll = 4;      // 16-byte loads in flight per thread
+
 struct SwapArgs {
   const int32_t* ids;     // [R * Hq, K]
   int g, k, nb, hkv_req, c;   // heads per group, K, NB, KV heads per request, slots per group
@@ -90,6 +98,9 @@ struct SwapArgs {
   int32_t* slot_stamp;
   const int32_t* clock;
   unsigned long long* h2d;
+  int32_t* nlist;         // [R * Hkv] pages to copy per group
+  int32_t* src;           // [R * Hkv, kMaxNeed] host pages
+  int32_t* dst;           // [R * Hkv, kMaxNeed] device slots
 };
 
 // One workgroup per group (request, KV head).
@@ -97,13 +108,14 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
   __shared__ uint32_t need[kTailMapN / 32];
   __shared__ int loads[kMaxNeed];
   __shared__ int vict[kMaxNeed];
-  __shared__ long long skey[kMaxSlots];
+  __shared__ TopkLds tl;
   __shared__ int nload;
   const int grp = blockIdx.x, tid = threadIdx.x;
   const int r = grp / a.hkv_req;
   const int n = a.nblk[r] < a.nb ? (a.nblk[r] < 0 ? 0 : a.nblk[r]) : a.nb;
   const int words = (a.nb + 31) / 32;
   for (int w = tid; w < words; w += kSwapThreads) need[w] = 0u;
+  for (int x = tid; x < kMaxNeed; x += kSwapThreads) vict[x] = -1;
   if (tid == 0) nload = 0;
   __syncthreads();
   // the union of the group's selected blocks
@@ -131,52 +143,92 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
       }
     }
   }
-  // victims: slots whose block is not needed this step, free slots first,
-  // then least recently used (ties to the lower slot)
-  for (int s = tid; s < a.c; s += kSwapThreads) {
-    const int blk = a.slot_block[s0 + s];
-    const bool busy = blk >= 0 && blk < a.nb && ((need[blk >> 5] >> (blk & 31)) & 1u);
-    const long long stamp = blk < 0 ? -1ll : (long long)a.slot_stamp[s0 + s];
-    skey[s] = busy ? 0x7fffffffffffffffll : ((stamp + 1) << 20) | s;
-  }
   __syncthreads();
   const int nl = nload < kMaxNeed ? nload : kMaxNeed;
-  for (int s = tid; s < a.c; s += kSwapThreads) {
-    const long long mine = skey[s];
-    if (mine == 0x7fffffffffffffffll) continue;
-    int rank = 0;
-    for (int x = 0; x < a.c; ++x) rank += skey[x] < mine;
-    if (rank < nl) {
-      const int j = loads[rank];
-      const int old = a.slot_block[s0 + s];
-      if (old >= 0 && old < a.nb) trow[old] = -1;
-      a.slot_block[s0 + s] = j;
-      a.slot_stamp[s0 + s] = now;
-      trow[j] = (int)(s0 + s);
-      vict[rank] = (int)(s0 + s);
+  if (tid == 0) a.nlist[grp] = nl;
+  if (nl == 0) return;   // the whole selection is resident
+  // victims: the nl slots whose block is not needed this step, free slots
+  // first, then least recently used (ties to the lower slot): the largest
+  // keys ~(stamp + 1, slot) by the radix select, a needed slot keyed 0
+  uint64_t vkey[kSlotsPerThread];
+#pragma unroll
+  for (int i = 0; i < kSlotsPerThread; ++i) {
+    const int s = tid * kSlotsPerThread + i;
+    const int blk = s < a.c ? a.slot_block[s0 + s] : -1;
+    const bool busy = blk >= 0 && blk < a.nb && ((need[blk >> 5] >> (blk & 31)) & 1u);
+    const uint64_t stamp = blk < 0 ? 0ull : (uint64_t)(uint32_t)(a.slot_stamp[s0 + s] + 1);
+    vkey[i] = busy ? 0ull : ~((stamp << 20) | (uint64_t)s);
+  }
+  topk_select_keys<kSlotsPerThread>(vkey, a.c, nl, tl, [&](int pos, int s, int i) {
+    if (vkey[i] == 0ull) return;   // a needed slot (C >= G * K rules this out)
+    const int j = loads[pos];
+    const int old = a.slot_block[s0 + s];
+    if (old >= 0 && old < a.nb) trow[old] = -1;
+    a.slot_block[s0 + s] = j;
+    a.slot_stamp[s0 + s] = now;
+    trow[j] = (int)(s0 + s);
+    vict[pos] = (int)(s0 + s);
+  });
+  __syncthreads();
+  // the copy list: host page and device slot of each missing block (a block
+  // left without a slot, which C >= G * K rules out, is copied nowhere)
+  const int32_t* hrow = a.host_table + (size_t)grp * a.nb;
+  for (int x = tid; x < nl; x += kSwapThreads) {
+    const int hp = hrow[loads[x]];
+    const bool ok = hp >= 0 && hp < a.host_pages && vict[x] >= 0;
+    a.src[(size_t)grp * kMaxNeed + x] = ok ? hp : -1;
+    a.dst[(size_t)grp * kMaxNeed + x] = ok ? vict[x] : -1;
+  }
+  const int chunks = a.b * a.d * a.esize / 16;   // 16-byte chunks per page
+  if (tid == 0) atomicAdd(a.h2d, (unsigned long long)nl * 2ull * chunks * 16ull);
+}
+
+// The listed pages: workgroup (group, part) copies pages part, part + 16,
+// ... of its group's list, K then V, every thread keeping kCopyUnroll
+// 16-byte host loads in flight before its stores.
+__global__ __launch_bounds__(kSwapThreads) void k_swap_copy(SwapArgs a) {
+  const int grp = blockIdx.x / kCopyWGs, part = blockIdx.x % kCopyWGs;
+  const int nl = a.nlist[grp];
+  const int chunks = a.b * a.d * a.esize / 16;
+  const uint4* hk = reinterpret_cast<const uint4*>(a.host_k);
+  const uint4* hv = reinterpret_cast<const uint4*>(a.host_v);
+  uint4* dk = reinterpret_cast<uint4*>(a.k_slots);
+  uint4* dv = reinterpret_cast<uint4*>(a.v_slots);
+  for (int x = part; x < nl; x += kCopyWGs) {
+    const int hp = a.src[(size_t)grp * kMaxNeed + x], sl = a.dst[(size_t)grp * kMaxNeed + x];
+    if (hp < 0 || sl < 0) continue;
+    const size_t so = (size_t)hp * chunks, dof = (size_t)sl * chunks;
+    for (int c0 = threadIdx.x; c0 < 2 * chunks; c0 += kSwapThreads * kCopyUnroll) {
+      uint4 buf[kCopyUnroll];
+#pragma unroll
+      for (int u = 0; u < kCopyUnroll; ++u) {
+        const int c = c0 + u * kSwapThreads;
+        const int cc = c < 2 * chunks ? c : 0;
+        buf[u] = cc < chunks ? hk[so + cc] : hv[so + cc - chunks];
+      }
+#pragma unroll
+      for (int u = 0; u < kCopyUnroll; ++u) {
+        const int c = c0 + u * kSwapThreads;
+        if (c < chunks) dk[dof + c] = buf[u];
+        else if (c < 2 * chunks) dv[dof + c - chunks] = buf[u];
+      }
     }
   }
-  __syncthreads();
-  // copy the missing blocks' K and V pages from the host pool
-  const int chunks = a.b * a.d * a.esize / 16;   // 16-byte chunks per page
-  const int32_t* hrow = a.host_table + (size_t)grp * a.nb;
-  for (int x = tid; x < nl * chunks; x += kSwapThreads) {
-    const int q = x / chunks, c = x % chunks;
-    const int hp = hrow[loads[q]];
-    if (hp < 0 || hp >= a.host_pages) continue;
-    const size_t src = (size_t)hp * chunks + c, dst = (size_t)vict[q] * chunks + c;
-    reinterpret_cast<uint4*>(a.k_slots)[dst] = reinterpret_cast<const uint4*>(a.host_k)[src];
-    reinterpret_cast<uint4*>(a.v_slots)[dst] = reinterpret_cast<const uint4*>(a.host_v)[src];
-  }
-  if (tid == 0 && nl > 0) atomicAdd(a.h2d, (unsigned long long)nl * 2ull * chunks * 16ull);
 }
 
 }  // namespace
 
 extern "C" {
 
-STK_API size_t stk_cache_workspace_bytes(int requests, int hq, int nb) {
-  return stk_paged_workspace_bytes(requests, hq, nb);
+// The paged step's workspace, then the copy lists (count, host pages and
+// slots of every group).
+static size_t cache_lists_bytes(int requests, int hkv) {
+  return stk_align((size_t)requests * hkv * (1 + 2 * kMaxNeed) * sizeof(int32_t));
+}
+
+STK_API size_t stk_cache_workspace_bytes(int requests, int hq, int hkv, int nb) {
+  if (requests <= 0 || hq <= 0 || hkv <= 0 || nb <= 0) return 0;
+  return stk_align(stk_paged_workspace_bytes(requests, hq, nb)) + cache_lists_bytes(requests, hkv);
 }
 
 STK_API int stk_cache_step(const void* q, int dtype, int requests, int hq, int hkv, int nb, int b,
@@ -200,15 +252,15 @@ STK_API int stk_cache_step(const void* q, int dtype, int requests, int hq, int h
   STK_REQUIRE(stk_bounds_ok(dtype, bounds_dtype),
               "lo and hi pages must be FP32 or the pages' 16-bit type");
   STK_REQUIRE(topk >= 1 && topk <= kTailMaxK, "topk must be in [1, 256]");
-  STK_REQUIRE(sp >= 1 && sp <= kTailMaxK && predicted && m && l && u,
-              "the predicted width must be in [1, 256]");
+  STK_REQUIRE(sp >= 0 && sp <= kTailMaxK, "the predicted width must be in [0, 256]");
+  STK_REQUIRE(sp == 0 || (predicted && m && l && u), "null pointer");
   STK_REQUIRE(nb <= kTailMapN, "at most 8192 blocks per request");
   const int G = hq / hkv;
   STK_REQUIRE(slots_per_group >= G * topk && slots_per_group <= kMaxSlots,
               "slots per (request, KV head) must be in [G * topk, 1024]");
   STK_REQUIRE((b * d * 2) % 16 == 0, "a page must be a whole number of 16-byte chunks");
   STK_REQUIRE((int64_t)requests * hkv * slots_per_group <= 0x7fffffff, "too many slots");
-  STK_REQUIRE(workspace_bytes >= stk_paged_workspace_bytes(requests, hq, nb),
+  STK_REQUIRE(workspace_bytes >= stk_cache_workspace_bytes(requests, hq, hkv, nb),
               "workspace too small");
   const int R = requests;
   const int hqa = R * hq, hkva = R * hkv;
@@ -219,8 +271,8 @@ STK_API int stk_cache_step(const void* q, int dtype, int requests, int hq, int h
                           reinterpret_cast<uintptr_t>(lo_pages) |
                           reinterpret_cast<uintptr_t>(hi_pages) | reinterpret_cast<uintptr_t>(u);
   StepShape s{};
-  const char* why = plan_step(dtype, hqa, hkva, nb, b, d, topk < nb ? topk : nb, sp, IT_I32,
-                              align, &s);
+  const char* why = plan_step(dtype, hqa, hkva, nb, b, d, topk < nb ? topk : nb,
+                              sp > 0 ? sp : 1, IT_I32, align, &s);
   STK_REQUIRE(why == nullptr, why ? why : "");
   uint64_t* keys = static_cast<uint64_t*>(workspace);
   const int pages = R * hkv * slots_per_group;
@@ -237,17 +289,28 @@ STK_API int stk_cache_step(const void* q, int dtype, int requests, int hq, int h
   else hipLaunchKernelGGL(k_cache_select<16>, tgrid, tblock, 0, st, sa);
   rc = stk_check_launch("k_cache_select");
   if (rc) return rc;
+  int32_t* lists = reinterpret_cast<int32_t*>(
+      static_cast<char*>(workspace) + stk_align(stk_paged_workspace_bytes(requests, hq, nb)));
   SwapArgs w{selected, G, topk, nb, hkv, slots_per_group, b, d, 2, nblocks, host_k, host_v,
              host_table, host_pages, k_slots, v_slots, table, slot_block, slot_stamp, clock,
-             h2d_bytes};
+             h2d_bytes, lists, lists + hkva, lists + hkva + (size_t)hkva * kMaxNeed};
   hipLaunchKernelGGL(k_swap_in, dim3(hkva), dim3(kSwapThreads), 0, st, w);
   rc = stk_check_launch("k_swap_in");
   if (rc) return rc;
+  hipLaunchKernelGGL(k_swap_copy, dim3(hkva * kCopyWGs), dim3(kSwapThreads), 0, st, w);
+  rc = stk_check_launch("k_swap_copy");
+  if (rc) return rc;
+  // with no predicted rows (the serial path) the tail's always-issued loads
+  // of slot 0 read a stand-in past the keys (their values are discarded)
+  const void* dummy = static_cast<char*>(workspace) +
+                      stk_align((size_t)requests * hq * nb * sizeof(uint64_t));
   TailArgs t{};
   t.kv = KV{q, k_slots, v_slots, hqa, hkva, nb, b, d};
   t.keys = keys; t.k = topk; t.ids = selected;
-  t.p = predicted; t.sp = sp;
-  t.pm = m; t.pl = l; t.pu = u;
+  t.p = sp ? predicted : static_cast<const int32_t*>(dummy); t.sp = sp;
+  t.pm = sp ? m : static_cast<const float*>(dummy);
+  t.pl = sp ? l : static_cast<const float*>(dummy);
+  t.pu = sp ? u : static_cast<const float*>(dummy);
   t.uni = 0; t.out = out;
   t.pg = f.pg;
   return launch_tail_pg(dtype, t, s, st);

@@ -68,6 +68,7 @@ class Case:
     # goes back to the driver at the next capture, and replaying the graph
     # then reads unmapped memory.  Released together with the graphs.
     keep: object = None
+    after: object = None             # measurements taken after the timing (dict)
 
     def release(self):
         self.graphs = {}
@@ -78,7 +79,9 @@ class Case:
                                warm_ms=50.0)
         per = {k: v / self.steps_per_graph for k, v in med.items()}
         full = per[self.primary]
+        extra = self.after() if self.after else {}
         return {
+            **extra,
             "strategy": self.strategy, "primary": self.primary,
             "us_per_step": {k: round(v, 3) for k, v in per.items()},
             "speedup_vs_serial": round(per[self.baseline] / full, 4),
@@ -412,4 +415,82 @@ def case_c3sweep(dev, seed=20261103):
     return case
 
 
-CASES = {"c1": case_c1, "c2": case_c2, "c4": case_c4, "c5": case_c5, "c3sweep": case_c3sweep}
+# ------------------------------------------------------------------ host cache
+def case_cache(dev, seed=20261103):
+    """c3's shape with its KV in pinned host memory (strict_topk.hostcache):
+    C = 2 * G * K device slots per KV head (a quarter of the context
+    resident), a decode sequence of 12 correlated queries (q_i = q_0 + 0.5 *
+    noise_i) whose prediction is the previous step's selection.  The cache
+    step (select || speculate on the resident predicted blocks, swap-in of
+    the selected blocks, repair) against the cache's serial path (select,
+    swap-in, exact attention), each on a cache of its own that evolves over
+    the replays; H2D bytes per step counted by the swap-in kernel."""
+    from strict_topk import hostcache
+    c = CONFIGS["c3"]
+    g = c.group
+    q, k, v, lo, hi = make_qkv(c.hq, c.hkv, c.dim, c.block, c.blocks, c.dtype, c.hot, seed)
+    m = 12
+    gen = torch.Generator().manual_seed(seed + 12)
+    qs = [(q.float() + 0.5 * torch.randn(q.shape, generator=gen)).to(c.dtype) for _ in range(m)]
+    qd = [x.to(dev)[None].contiguous() for x in qs]
+    lod, hid = lo.to(dev), hi.to(dev)
+    sels = [step_mod.select_blocks(x[0], lod, hid, c.topk) for x in qd]
+    preds = [sels[(i - 1) % m][None].contiguous() for i in range(m)]
+    slots = 2 * g * c.topk
+    spec = hostcache.build([(k, v)], slots, device=dev, bounds_dtype=c.dtype)
+    ser = hostcache.build([(k, v)], slots, device=dev, bounds_dtype=c.dtype)
+
+    def full(i):
+        return hostcache.speculative_step(qd[i], spec, preds[i], c.topk).output
+
+    def serial(i):
+        return hostcache.exact(qd[i], ser, c.topk)[1]
+
+    graphs, outs = {}, {}
+    for name, fn in (("cache_step", full), ("cache_serial", serial)):
+        graphs[name], outs[name] = timing.capture(_seq(fn, m))
+    tile = 2 * c.block * c.dim * 2
+    sa = torch.stack(sels).cpu().numpy()
+    u_a = sum(unique_pairs(x, g) for x in sa) / m
+    meta = 2 * c.hkv * c.blocks * c.dim * 2
+
+    def after():
+        out = {}
+        for name, cache in (("cache_step", spec), ("cache_serial", ser)):
+            g_ = graphs[name]
+            for _ in range(3):
+                g_.replay()
+            torch.cuda.synchronize()
+            b0 = int(cache.h2d_bytes.item())
+            reps = 10
+            for _ in range(reps):
+                g_.replay()
+            torch.cuda.synchronize()
+            out[f"h2d_bytes_per_step_{name}"] = (int(cache.h2d_bytes.item()) - b0) // (reps * m)
+        out["resident_fraction"] = round(slots / c.blocks, 4)
+        return out
+
+    case = Case("cache", "host-backed cache (pinned host pool, swap-in, P n R speculation): "
+                "hostcache.speculative_step against hostcache.exact", graphs, m,
+                int(meta + u_a * tile), int(u_a * tile), int(meta + u_a * tile),
+                primary="cache_step", baseline="cache_serial",
+                notes=f"c3 shape, {slots} device slots per KV head of {c.blocks} blocks, 12 "
+                      "correlated queries, prediction = previous step's selection; bytes: the "
+                      "device-side algorithmic bytes (H2D reported separately)")
+    case.after = after
+    case.keep = (qd, lod, hid, sels, preds, spec, ser)
+    for i in (0, m - 1):
+        sel = sels[i].cpu()
+        need = torch.unique(sel.flatten().long())
+        remap = torch.full((c.blocks,), -1, dtype=torch.int64)
+        remap[need] = torch.arange(len(need))
+        sel_r = remap[sel.long()].to(torch.int32)
+        for name in ("cache_step", "cache_serial"):
+            case.check.append((f"{name}[{i}]", "attention",
+                               (qs[i], k[:, need], v[:, need], sel_r,
+                                outs[name][i][0].cpu())))
+    return case
+
+
+CASES = {"c1": case_c1, "c2": case_c2, "c4": case_c4, "c5": case_c5, "c3sweep": case_c3sweep,
+         "cache": case_cache}

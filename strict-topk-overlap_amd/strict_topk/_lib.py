@@ -77,7 +77,7 @@ _SIGS = {
                            P, P, P, P, P, P, Z, P]),
     "stk_paged_signed_step": (I, [P, P, P, I, I, I, I, I, I, I, I, P, P, I, P, P, P, I, P, I, I,
                                   F, F, F, F, P, P, P, P, P, P, P, P, P, P, P, P, Z, P]),
-    "stk_cache_workspace_bytes": (Z, [I, I, I]),
+    "stk_cache_workspace_bytes": (Z, [I, I, I, I]),
     "stk_cache_step": (I, [P, I, I, I, I, I, I, I, P, P, I, P, P, I, P, P, I, P, P, P, P, P,
                            P, P, I, P, I, P, P, P, P, P, P, P, Z, P]),
 }

@@ -7,8 +7,8 @@ top-K, swap-in finds the resident hits, updates the LRU, copies the missing
 blocks in and hands attention a device slot table; speculation reads only
 the resident predicted blocks (P n R) and the repair recomputes the rest of
 the selected set A from the slots.  Here that is one call,
-``speculative_step(q, cache, predicted, topk)``, four launches on the
-current stream (``stk_cache_step``):
+``speculative_step(q, cache, predicted, topk)``, five launches on the
+current stream (``stk_cache_step``; the swap-in is two of them):
 
   scores of every block (their bounds stay on the device) || prediction
   states of P n R;  top-K;  swap-in (LRU over each (request, KV head)'s C
@@ -136,6 +136,14 @@ def build(caches, slots_per_group, device=None, bounds_dtype=torch.float32, toke
         torch.tensor(tokens, dtype=torch.int32, device=device), c)
 
 
+def exact(q, cache, topk):
+    """The serial path over the cache: select, swap-in, then the exact
+    attention over the selected blocks (no prediction).  Returns (selected,
+    out), laid out [R, Hq, ...]."""
+    res = _step(q, cache, None, topk)
+    return res.selected, res.output
+
+
 def speculative_step(q, cache, predicted, topk):
     """One decode step over the batch: select(q) || partials over the resident
     predicted blocks, then swap-in of the selected blocks that are not
@@ -143,6 +151,10 @@ def speculative_step(q, cache, predicted, topk):
     int32; returns ``StepResult`` laid out [R, Hq, ...] (the prediction
     state of a non-resident predicted block is the empty state).  The output
     is the exact attention over each request's selected blocks."""
+    return _step(q, cache, predicted, topk)
+
+
+def _step(q, cache, predicted, topk):
     if not isinstance(cache, HostCache):
         raise TypeError("cache must be a HostCache")
     if q.ndim != 3 or q.shape[0] != cache.requests or q.shape[2] != cache.dim:
@@ -150,28 +162,34 @@ def speculative_step(q, cache, predicted, topk):
     r, hq, d = q.shape
     if hq % cache.hkv:
         raise ValueError("Hq must be divisible by Hkv")
-    if predicted.ndim != 3 or predicted.shape[:2] != (r, hq) or predicted.dtype != torch.int32:
+    if predicted is not None and (predicted.ndim != 3 or predicted.shape[:2] != (r, hq) or
+                                  predicted.dtype != torch.int32):
         raise ValueError("expected int32 P[R,Hq,SP]")
     if q.dtype != cache.k_slots.dtype:
         raise ValueError("Q and the cache must share a dtype")
     topk = int(topk)
-    sp = predicted.shape[2]
-    if not 1 <= topk <= 256 or not 1 <= sp <= 256:
-        raise ValueError("topk and the predicted width must be in [1, 256]")
+    sp = 0 if predicted is None else predicted.shape[2]
+    if not 1 <= topk <= 256 or not 0 <= sp <= 256:
+        raise ValueError("topk must be in [1, 256] and the predicted width in [0, 256]")
     dev = q.device
-    ts = [q, predicted, cache.k_slots, cache.v_slots, cache.lo_pages, cache.hi_pages,
+    ts = [q, cache.k_slots, cache.v_slots, cache.lo_pages, cache.hi_pages,
           cache.host_table, cache.table, cache.slot_block, cache.slot_stamp, cache.clock,
           cache.h2d_bytes, cache.nblocks, cache.ntokens]
+    if predicted is not None:
+        ts.append(predicted)
     if not q.is_cuda or any(t.device != dev or not t.is_contiguous() for t in ts):
         raise ValueError("all device tensors must be contiguous and on Q's CUDA device")
     if not (cache.host_k.is_pinned() and cache.host_v.is_pinned()):
         raise ValueError("the host pool must be pinned memory")
     selected = torch.empty((r, hq, topk), device=dev, dtype=torch.int32)
-    m = torch.empty((r, hq, sp), device=dev, dtype=torch.float32)
-    state = PartialState(m, torch.empty_like(m),
-                         torch.empty((r, hq, sp, d), device=dev, dtype=torch.float32))
+    state = None
+    if sp:
+        m = torch.empty((r, hq, sp), device=dev, dtype=torch.float32)
+        state = PartialState(m, torch.empty_like(m),
+                             torch.empty((r, hq, sp, d), device=dev, dtype=torch.float32))
     out = torch.empty((r, hq, d), device=dev, dtype=torch.float32)
-    ws = _lib.workspace(_lib.size("stk_cache_workspace_bytes", r, hq, cache.width), dev)
+    ws = _lib.workspace(_lib.size("stk_cache_workspace_bytes", r, hq, cache.hkv, cache.width),
+                        dev)
     _lib.call("stk_cache_step", _lib.ptr(q), _lib.dtype_code(q), r, hq, cache.hkv, cache.width,
               cache.block, d, _lib.ptr(cache.k_slots), _lib.ptr(cache.v_slots),
               cache.slots_per_group, _lib.ptr(cache.host_k), _lib.ptr(cache.host_v),
@@ -179,7 +197,8 @@ def speculative_step(q, cache, predicted, topk):
               _lib.bounds_code(cache.lo_pages, q), _lib.ptr(cache.host_table),
               _lib.ptr(cache.table), _lib.ptr(cache.slot_block), _lib.ptr(cache.slot_stamp),
               _lib.ptr(cache.clock), _lib.ptr(cache.nblocks), _lib.ptr(cache.ntokens), topk,
-              _lib.ptr(predicted), sp, _lib.ptr(selected), _lib.ptr(state.m), _lib.ptr(state.l),
-              _lib.ptr(state.u), _lib.ptr(out), _lib.ptr(cache.h2d_bytes), _lib.ptr(ws),
+              _lib.ptr(predicted), sp, _lib.ptr(selected),
+              *((None, None, None) if state is None else
+                (_lib.ptr(state.m), _lib.ptr(state.l), _lib.ptr(state.u))), _lib.ptr(out), _lib.ptr(cache.h2d_bytes), _lib.ptr(ws),
               ws.numel(), _lib.stream(dev))
     return StepResult(selected, state, out)

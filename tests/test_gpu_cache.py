@@ -119,3 +119,25 @@ def test_host_cache_steps():
             assert new == 0
         h2d_prev = h2d
     assert int(cache.clock.item()) == len(queries)
+
+
+def test_host_cache_serial_path():
+    """hostcache.exact: select, swap-in, then the exact attention (no
+    prediction), over a request whose last block is partly filled."""
+    from stk_harness.configs import make_qkv
+    from strict_topk import hostcache
+    hq, hkv, b, d, topk, n = 8, 4, 16, 64, 12, 90
+    q, k, v, lo, hi = make_qkv(hq, hkv, d, b, n, torch.float16, True, 31)
+    tokens = (n - 1) * b + 5
+    live = torch.arange(n * b).view(n, b) < tokens
+    lo = torch.where(live[None, :, :, None], k.float(), float("inf")).amin(2)
+    hi = torch.where(live[None, :, :, None], k.float(), float("-inf")).amax(2)
+    cache = hostcache.build([(k, v)], 2 * topk, device=DEV, tokens=[tokens])
+    sel, out = hostcache.exact(q[None].to(DEV), cache, topk)
+    torch.cuda.synchronize()
+    qn, kn, vn = C.f64(q), C.f64(k), C.f64(v)
+    ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), topk)
+    assert sel[0].cpu().numpy().tolist() == ids.tolist()
+    m = C.error_metrics(C.f64(out[0]), O.attention(qn, kn, vn, ids, tokens=tokens))
+    assert m["passed"], m
+    assert int(cache.h2d_bytes.item()) > 0
