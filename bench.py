@@ -103,6 +103,22 @@ def traffic_record(workload):
     return json.loads(path.read_text()).get(workload)
 
 
+def path_traffic(config):
+    """The committed counter record of a config's paths (profiles/traffic.json,
+    written by stk_harness/profile_traffic.py): HBM bytes per decode step of
+    the speculative and the serial path, and their ratio to the algorithmic
+    bytes.  None when no run covers the config."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text()).get(config)
+    if not rec:
+        return None
+    return {name: {"traffic": p["traffic_per_step"],
+                   "traffic_over_algorithmic": p["traffic_over_algorithmic"]}
+            for name, p in rec["paths"].items()}
+
+
 def cpu_leg(args, step, c3_outs, cases):
     """The CPU side: the FP64 oracle as the checker of every GPU output, and
     the torch-CPU port of the serial path timed as the baseline."""
@@ -296,7 +312,9 @@ def main():
     timing.warm([g_a], ms=20.0)
     a_us = min(timing.interval_us(g_a, 20) for _ in range(3)) / M
     b_bytes = kk.numel() * kk.element_size() + 2 * lohi[-1][0].numel() * 4
+    tr_meta = path_traffic("metadata")
     metadata = {"kernel": "k_bounds (lo/hi from K)", "bytes_per_launch": b_bytes,
+                "traffic": tr_meta["block_bounds"] if tr_meta else None,
                 "us_per_launch": round(b_us, 3),
                 "achieved_GBps": round(b_bytes / (b_us * 1e-6) / 1e9, 1),
                 "frac": round(b_bytes / (b_us * 1e-6) / decode.HBM_PEAK, 4),
@@ -309,6 +327,7 @@ def main():
             "frac": round(by.full / (full_us * 1e-6) / decode.HBM_PEAK, 4),
             "kv_frac": round(by.kv_full / (full_us * 1e-6) / decode.HBM_PEAK, 4),
             "serial_bytes": by.serial,
+            "traffic": path_traffic("c3"),
             "serial_frac": round(by.serial / (per_step["serial"] * 1e-6) / decode.HBM_PEAK, 4)}
     del graphs, g, g_front
 
@@ -321,6 +340,9 @@ def main():
             log(f"bench: config {name}")
             case = make(dev, args.seed)
             configs[name] = case.measure(seed=args.seed)
+            tr = path_traffic(name)
+            if tr:
+                configs[name]["traffic"] = tr
             case.release()   # the graphs, then the device inputs they read
             cases.append(case)
             torch.cuda.synchronize()
