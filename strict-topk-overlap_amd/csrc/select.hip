@@ -18,13 +18,12 @@
 //               heads of that head (lo/hi read once per KV head); every lane
 //               issues all its 16-byte loads before any arithmetic.  Writes
 //               an order-preserving 64-bit key per (query head, block).
-//   k_topk   -- one 256-thread workgroup per query head: MSB-first radix
-//               select over the row's keys held in registers (8-bit digits
-//               from the highest bit where the row's keys differ, stopping
-//               as soon as the threshold digit's bin is taken whole), then a
-//               block-wide scan writes the selected IDs in index order.
+//   k_topk   -- one 256-thread workgroup per query head: the value-bin
+//               selection of topk_bins.hpp over the row's keys held in
+//               registers (radix select as its fallback), then a block-wide
+//               scan writes the selected IDs in index order.
 #include "score.hpp"
-#include "topk.hpp"
+#include "topk_bins.hpp"
 #include "api.hpp"
 
 namespace stk {
@@ -43,24 +42,38 @@ struct TopkArgs {
   int32_t* ids;
 };
 
-// One workgroup per row (TopkArgs.keys[row, 0..n)), see topk.hpp.
+// One row's selection by value bins (topk_bins.hpp): KPT keys per thread,
+// the selected indices ranked by one scan and written in ascending order.
+template <int KPT>
+__device__ __forceinline__ void topk_row(const TopkArgs& a, TopkBinsLds& tb, int* s_scan) {
+  const uint64_t* rk = a.keys + (size_t)blockIdx.x * a.n;
+  int32_t* out = a.ids + (size_t)blockIdx.x * a.k;
+  uint64_t key[KPT];
+  topk_load<KPT>(rk, a.n, key);
+  const uint32_t flags = topk_bins_flags<KPT>(key, a.n, a.k, tb, [] {});
+  int total;
+  int pos = block_excl_scan1(__popc(flags), s_scan, &total);
+#pragma unroll
+  for (int i = 0; i < KPT; ++i)
+    if ((flags >> i) & 1u) out[pos++] = threadIdx.x * KPT + i;
+}
+
+// One workgroup per row (TopkArgs.keys[row, 0..n)).
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void k_topk(TopkArgs a) {
-  __shared__ TopkLds s;
-  int32_t* out = a.ids + (size_t)blockIdx.x * a.k;
-  topk_select<KPT>(a.keys + (size_t)blockIdx.x * a.n, a.n, a.k, s,
-                   [&](int pos, int idx) { out[pos] = idx; });
+  __shared__ TopkBinsLds tb;
+  __shared__ int s_scan[kTopkThreads / STK_WAVE];
+  topk_row<KPT>(a, tb, s_scan);
 }
 
 // The same selection with 1024 threads (KPT keys each), for shapes with few
 // rows, where one workgroup per row leaves most of the chip idle and a
-// row's passes are the latency.
+// row's phases are the latency.
 template <int KPT>
 __global__ __launch_bounds__(kTopkWide) void k_topk_wide(TopkArgs a) {
-  __shared__ TopkLds s;
-  int32_t* out = a.ids + (size_t)blockIdx.x * a.k;
-  topk_select<KPT>(a.keys + (size_t)blockIdx.x * a.n, a.n, a.k, s,
-                   [&](int pos, int idx) { out[pos] = idx; });
+  __shared__ TopkBinsLds tb;
+  __shared__ int s_scan[kTopkWide / STK_WAVE];
+  topk_row<KPT>(a, tb, s_scan);
 }
 
 // Rows longer than 8192 keys: the same selection with keys re-read from
