@@ -138,7 +138,7 @@ using namespace stk;
 static StkCheck check_indexer(int dtype, int h, int n, int d) {
   if (dtype != DT_F32 && dtype != DT_F16 && dtype != DT_BF16) return {false, "unsupported dtype"};
   if (h <= 0 || n <= 0 || d <= 0) return {false, "bad indexer shape"};
-  if (h * d > kIdxMaxQ) return {false, "indexer heads * dim must be <= 4096"};
+  if ((int64_t)h * d > kIdxMaxQ) return {false, "indexer heads * dim must be <= 4096"};
   return {true, ""};
 }
 

@@ -151,12 +151,3 @@ class Request:
     overlap: float
     blocks: int
     extra: dict = field(default_factory=dict)
-
-
-def c5_plan(seed):
-    """Per-request block counts and overlaps for c5 (seeded)."""
-    gen = _gen(seed + 31337)
-    n = torch.randint(C5["min_blocks"], C5["max_blocks"] + 1, (C5["requests"],), generator=gen)
-    ov = torch.rand((C5["requests"],), generator=gen, dtype=torch.float64)
-    ov = C5["min_overlap"] + (C5["max_overlap"] - C5["min_overlap"]) * ov
-    return [int(x) for x in n], [float(x) for x in ov]

@@ -402,3 +402,24 @@ def test_token_count_mask_pinned_by_brute_force():
                 mm = max(s)
                 assert st.m[h, j] == pytest.approx(mm, abs=1e-12)
                 assert st.l[h, j] == pytest.approx(sum(math.exp(x - mm) for x in s), rel=1e-12)
+
+
+@pytest.mark.parametrize("b,d", [(16, 128), (8, 96), (3, 40)])
+def test_touch_kv_pinned_against_torch(b, d):
+    """touch_kv (reference strict_topk/kernels.py:250-260,553-560): the sum
+    of K + V over each 1024-element tile of a predicted block's flattened
+    [B, D] rows, the last tile short.  Pinned by a gather + padded view in
+    torch (an independent reduction), and by the invariant that a block's
+    tiles add up to its whole sum."""
+    gen = torch.Generator().manual_seed(b * 1000 + d)
+    h, n, s = 3, 9, 4
+    k = torch.randn((h, n, b, d), generator=gen, dtype=torch.float64)
+    v = torch.randn((h, n, b, d), generator=gen, dtype=torch.float64)
+    p = torch.stack([torch.randperm(n, generator=gen)[:s] for _ in range(h)])
+    got = O.touch_kv(k.numpy(), v.numpy(), p.numpy())
+    nt = -(-b * d // 1024)
+    kv = (k + v)[torch.arange(h)[:, None], p].reshape(h, s, b * d)
+    ref = torch.nn.functional.pad(kv, (0, nt * 1024 - b * d)).view(h, s, nt, 1024).sum(-1)
+    assert got.shape == (h, s, nt)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(got.sum(-1), kv.sum(-1).numpy(), rtol=1e-12, atol=1e-12)
