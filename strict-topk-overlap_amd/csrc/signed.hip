@@ -13,6 +13,7 @@
 // does not depend on the data.
 #include "head.hpp"
 #include "api.hpp"
+#include "srepair.hpp"
 
 namespace stk {
 
@@ -329,6 +330,17 @@ STK_API int stk_repair_signed(const void* q, const void* k, const void* v, int d
               "workspace too small");
   hipStream_t st = (hipStream_t)stream;
   int cap = mode == MODE_SAVED ? sa : sa + sp;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(pu);
+  if (fused && mode != MODE_COMPACT && sc == sp && srepair_covers(dtype, b, d, sa, sp, align)) {
+    // one launch: schedule, corrections and guarded merge (srepair.hip)
+    SRepairArgs r{{q, k, v, hq, hkv, n, b, d}, selected, sel_dtype, sa, predicted, pred_dtype, sp,
+                  mode == MODE_HYBRID ? 1 : 0, pm, pl, pu, high, low_m, low_l, low_u, low_abs,
+                  mass_m, mass_l, min_remaining, cancellation_tol, max_extra_mass, queue,
+                  queue_dtype, cap, positive_jobs, total_jobs, out, fallback, remaining,
+                  approximate, extra_mass_bound};
+    return launch_srepair(dtype, r, st);
+  }
   Carve w(workspace);
   uint8_t* keep = w.take<uint8_t>((size_t)hq * sc);
   uint8_t* low_hit = w.take<uint8_t>((size_t)hq);
