@@ -57,6 +57,16 @@ int stk_launch_states(const void* q, const void* k, const void* v, int dtype, in
                       int n, int b, int d, const void* ids, int itype, int s,
                       const uint8_t* active, int active_kind, const void* pred, int ptype, int sp,
                       int32_t* slot, float* m, float* l, float* u, bool with_v, hipStream_t st);
+// Hierarchical exact / repair in one launch: one merged state per pack of
+// 32 / B positions ([hq, packs] into m, l, u); with slot_in, hits take the
+// prediction's states (pm, pl, pu [hq, psp]).  Covers bf16 / fp16 (and FP32)
+// packed shapes (B = 4 or 8) with an even number of query heads per KV head.
+bool stk_states_comb_covers(int dtype, int hq, int hkv, int b, int d, uintptr_t align);
+int stk_launch_states_comb(const void* q, const void* k, const void* v, int dtype, int hq,
+                           int hkv, int n, int b, int d, const void* ids, int itype, int s,
+                           const int32_t* slot_in, int slot_shared, const float* pm,
+                           const float* pl, const float* pu, int psp, float* m, float* l,
+                           float* u, hipStream_t st);
 int stk_launch_states_skip(const void* q, const void* k, const void* v, int dtype, int hq,
                            int hkv, int n, int b, int d, const void* ids, int itype, int s,
                            const int32_t* slot_in, int slot_shared, float* m, float* l, float* u,

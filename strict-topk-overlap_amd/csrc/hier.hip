@@ -243,6 +243,18 @@ STK_API int stk_hier_exact(const void* q, const void* k, const void* v, int dtyp
   float* m = w.take<float>((size_t)hq * sa);
   float* l = w.take<float>((size_t)hq * sa);
   float* u = w.take<float>((size_t)hq * sa * d);
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(v);
+  if (stk_states_comb_covers(dtype, hq, hkv, b, d, align)) {
+    // small blocks: one merged state per pack of 32 / B positions, no
+    // per-block states (the reference's two-level reduction, merged in
+    // registers), then one LSE merge over the packs
+    const int packs = (sa + 32 / b - 1) / (32 / b);
+    int rc = stk_launch_states_comb(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa,
+                                    nullptr, 0, nullptr, nullptr, nullptr, 0, m, l, u, st);
+    if (rc) return rc;
+    return stk_launch_merge(m, l, u, nullptr, hq, packs, d, out, st);
+  }
   int rc = stk_launch_states(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa, nullptr, 0,
                              nullptr, 0, 0, nullptr, m, l, u, true, st);
   if (rc) return rc;
@@ -276,6 +288,17 @@ STK_API int stk_hier_repair(const void* q, const void* k, const void* v, int dty
   hipLaunchKernelGGL(k_match_ids, dim3(rows, (sa + 255) / 256), dim3(256), 0, st, ma);
   int rc = stk_check_launch("k_match_ids");
   if (rc) return rc;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(v);
+  if (stk_states_comb_covers(dtype, hq, hkv, b, d, align)) {
+    // the misses computed and the hits' prediction states merged per pack in
+    // one launch, then one LSE merge over the packs
+    const int packs = (sa + 32 / b - 1) / (32 / b);
+    rc = stk_launch_states_comb(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa, slot,
+                                shared ? 1 : 0, pm, pl, pu, sp, m, l, u, st);
+    if (rc) return rc;
+    return stk_launch_merge(m, l, u, nullptr, hq, packs, d, out, st);
+  }
   rc = stk_launch_states_skip(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa, slot,
                               shared ? 1 : 0, m, l, u, st);
   if (rc) return rc;

@@ -85,6 +85,13 @@ __global__ __launch_bounds__(256, NCH <= 4 ? 4 : 2) void k_states_pack_grp(State
                                                    : blockIdx.x);
 }
 
+// The same with one merged state per pack (hierarchical exact and repair).
+template <typename T, int NCH, int BB, typename I, int HG>
+__global__ __launch_bounds__(256) void k_states_pack_comb(StatesArgs a) {
+  states_pack_grp_wg<T, NCH, BB, I, HG, true>(a, a.remap ? xcd_remap(blockIdx.x, gridDim.x)
+                                                         : blockIdx.x);
+}
+
 // LSE merge arguments (kernels.py:74-91, merge_partials :437-442).
 struct MergeArgs {
   const float* m; const float* l; const float* u; const uint8_t* inc;
@@ -800,6 +807,50 @@ int stk_launch_states_skip(const void* q, const void* k, const void* v, int dtyp
   a.m = m; a.l = l; a.u = u;
   a.slot_in = slot_in; a.slot_shared = slot_shared;
   return launch_states(a, dtype, true, false, st);
+}
+
+bool stk_states_comb_covers(int dtype, int hq, int hkv, int b, int d, uintptr_t align) {
+  const int G = hq / hkv;
+  return pack_nch(dtype, d, b, align) != 0 && G % 2 == 0;
+}
+
+int stk_launch_states_comb(const void* q, const void* k, const void* v, int dtype, int hq,
+                           int hkv, int n, int b, int d, const void* ids, int itype, int s,
+                           const int32_t* slot_in, int slot_shared, const float* pm,
+                           const float* pl, const float* pu, int psp, float* m, float* l,
+                           float* u, hipStream_t st) {
+  StatesArgs a{};
+  a.q = q; a.k = k; a.v = v; a.ids = ids; a.itype = itype;
+  a.hq = hq; a.hkv = hkv; a.n = n; a.b = b; a.d = d; a.s = s;
+  a.m = m; a.l = l; a.u = u;
+  a.slot_in = slot_in; a.slot_shared = slot_shared;
+  a.combine = 1; a.pm = pm; a.pl = pl; a.pu = pu; a.psp = psp;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(v);
+  const int pnch = pack_nch(dtype, d, b, align);
+  const int G = hq / hkv;
+  if (!pnch || G % 2 != 0 || s <= 0) return STK_EINVAL;
+  if (slot_in && (!pm || !pl || !pu || psp <= 0)) return STK_EINVAL;
+  const int hg = G % 4 == 0 ? 4 : 2;
+  const int64_t items = (int64_t)hkv * ((s + 32 / b - 1) / (32 / b)) * (G / hg);
+  const int grid = (int)((items + 3) / 4);
+  a.remap = grid >= 8 ? 1 : 0;
+  const bool i64 = itype == IT_I64;
+#define STK_COMB(BBV, HGV)                                                                        \
+  STK_DISPATCH_TOK(dtype, pnch, {                                                                 \
+    if (i64)                                                                                      \
+      hipLaunchKernelGGL((k_states_pack_comb<T, NCH, BBV, int64_t, HGV>), dim3(grid), dim3(256),  \
+                         0, st, a);                                                               \
+    else                                                                                          \
+      hipLaunchKernelGGL((k_states_pack_comb<T, NCH, BBV, int32_t, HGV>), dim3(grid), dim3(256),  \
+                         0, st, a);                                                               \
+  })
+  if (b == 4 && hg == 4) STK_COMB(4, 4);
+  else if (b == 4) STK_COMB(4, 2);
+  else if (hg == 4) STK_COMB(8, 4);
+  else STK_COMB(8, 2);
+#undef STK_COMB
+  return stk_check_launch("k_states_pack_comb");
 }
 
 int stk_launch_merge(const float* m, const float* l, const float* u, const uint8_t* inc, int h,

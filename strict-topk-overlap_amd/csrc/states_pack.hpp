@@ -167,7 +167,7 @@ __device__ __forceinline__ void states_pack_wg(const StatesArgs& a, int wg) {
 // once and the heads are computed in turn from registers; otherwise each head
 // loads its own rows.  Items are ordered (KV head, pack, head group), so the
 // waves sharing a pack are adjacent and land on one XCD.
-template <typename T, int NCH, int BB, typename I, int HG>
+template <typename T, int NCH, int BB, typename I, int HG, bool COMB = false>
 __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) {
   using TT = TokTile<T, NCH, 2>;
   static_assert(BB == 4 || BB == 8, "packed blocks hold 4 or 8 tokens");
@@ -196,8 +196,18 @@ __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) 
   const int64_t gid = ld_or(ids, (int64_t)(h0 + (gi < HG ? gi : 0)) * a.s + p0 + gj, gin, (I)-1);
   uint32_t qw[TT::QW];
   t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)h0 * D, qw);
+  // hierarchical repair: the slots of the same (head, position) pairs come
+  // in the same round trip; a hit's tile is not needed, and its rows are
+  // read from block 0 (one cached line) instead
+  const int gsl = a.slot_in && gin
+                      ? a.slot_in[(int64_t)(a.slot_shared ? 0 : h0 + (gi < HG ? gi : 0)) * a.s +
+                                  p0 + gj]
+                      : -1;
   const int64_t ref = __shfl(gid, gj);
-  const bool same = __ballot(lane_id() < HG * PB && gid != ref) == 0ull;
+  const int sref = __shfl(gsl, gj);
+  // one tile load for the group when the heads agree on the IDs and on which
+  // of them are hits
+  const bool same = __ballot(lane_id() < HG * PB && (gid != ref || gsl != sref)) == 0ull;
   const T* K = reinterpret_cast<const T*>(a.k);
   const T* V = reinterpret_cast<const T*>(a.v);
   uint32_t kw[2][TT::QW], vw[TT::CH][TT::VW];
@@ -207,8 +217,11 @@ __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) 
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int tok = t.slot + 16 * u;
+      // both shuffles run in every lane: a cross-lane read inside a
+      // condition would see the lanes the condition turned off as zeros
       const int64_t bid = __shfl(gid, i * PB + tok / BB);
-      const bool ok = bid >= 0 && bid < a.n;
+      const int bsl = __shfl(gsl, i * PB + tok / BB);
+      const bool ok = bid >= 0 && bid < a.n && bsl < 0;
       const T* row = K + ((((size_t)kv * a.n + (ok ? (size_t)bid : 0)) * BB + tok % BB) * D);
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
@@ -220,7 +233,7 @@ __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) 
 #pragma unroll
     for (int j = 0; j < PB; ++j) {
       const int64_t bj = __builtin_amdgcn_readlane((int)gid, i * PB + j);   // IDs fit in 32 bits
-      const bool ok = bj >= 0 && bj < a.n;
+      const bool ok = bj >= 0 && bj < a.n && __builtin_amdgcn_readlane(gsl, i * PB + j) < 0;
       const T* vb = V + (((size_t)kv * a.n + (ok ? (size_t)bj : 0)) * BB) * D + lane_id() * TT::DPL;
 #pragma unroll
       for (int r = 0; r < BB; ++r) {
@@ -249,19 +262,32 @@ __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) 
     // per-position flags (lane j < PB): write the state, and compute it
     const int jl = lane_id() < PB ? lane_id() : 0;
     const int64_t lid = __shfl(gid, i * PB + jl);
-    bool write = lane_id() < PB && p0 + jl < a.s;
-    if (write && a.slot_in)
-      write = a.slot_in[(int64_t)(a.slot_shared ? 0 : h) * a.s + p0 + jl] < 0;
+    const bool inr = lane_id() < PB && p0 + jl < a.s;
+    const int slr = __shfl(gsl, i * PB + jl);   // in every lane (see load_tile)
+    const int sl = inr ? slr : -1;
+    const bool write = inr && sl < 0;
     bool live = write && lid >= 0 && lid < a.n;
     if (a.active_kind == 1) live = live && a.active[h] != 0;
     else if (a.active_kind == 2) live = live && a.active[(int64_t)h * a.s + p0 + jl] != 0;
     const uint64_t wmask = __ballot(write);
     const uint64_t lmask = __ballot(live);
+    // combine mode: lane j < PB requests the m, l of position j's hit with
+    // the tiles; the hits' u rows are read after the arithmetic (requesting
+    // them here would keep 16 more registers live across it)
+    // (a slot past the prediction's rows is no hit and reads nothing)
+    const bool hit = COMB && a.pm != nullptr && inr && sl >= 0 && sl < a.psp;
+    const uint64_t hmask = __ballot(hit);
+    float hm = -INFINITY, hl = 0.f;
+    if (hit) {
+      const int64_t prow = (int64_t)h * a.psp + sl;
+      hm = a.pm[prow];
+      hl = a.pl[prow];
+    }
     float s[2];
     t.scores(qw, kw, 0, TT::CH, scale, s);
     // the next head's query row, loaded while this head finishes
     if (i + 1 < HG) t.load_q(reinterpret_cast<const T*>(a.q) + (size_t)(h + 1) * D, qw);
-    if (wmask == 0ull) continue;
+    if (wmask == 0ull && !COMB) continue;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int j = (t.slot + 16 * u) / BB;
@@ -297,6 +323,52 @@ __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) 
       t.vals(vw, x, v);
 #pragma unroll
       for (int e = 0; e < TT::DPL; ++e) acc[x / BB][e] += wt * v[e];
+    }
+    if constexpr (COMB) {
+      // a hit's u row replaces its (empty) computed accumulator
+#pragma unroll
+      for (int j = 0; j < PB; ++j) {
+        if ((hmask >> j) & 1ull) {
+          const int sj = __builtin_amdgcn_readlane(sl, j);
+          const float* ur = a.pu + ((int64_t)h * a.psp + sj) * D + lane_id() * TT::DPL;
+#pragma unroll
+          for (int e = 0; e < TT::DPL; ++e) acc[j][e] = ur[e];
+        }
+      }
+      // one merged state for the pack: computed blocks, hits from the
+      // prediction, the rest empty
+      float mj[PB], lj[PB];
+      float M = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < PB; ++j) {
+        const int u = (j * BB) / 16, src = ((j * BB) % 16) * 4;
+        const bool hj = (hmask >> j) & 1ull, comp = (lmask >> j) & 1ull;
+        const float cm = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mb[u]), src));
+        const float cl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lb[u]), src));
+        const float pmj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, hm), j));
+        const float plj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, hl), j));
+        mj[j] = hj ? pmj : (comp ? cm : -INFINITY);
+        lj[j] = hj ? plj : (comp ? cl : 0.f);
+        M = fmaxf(M, mj[j]);
+      }
+      float Z = 0.f, U[TT::DPL];
+#pragma unroll
+      for (int e = 0; e < TT::DPL; ++e) U[e] = 0.f;
+#pragma unroll
+      for (int j = 0; j < PB; ++j) {
+        const float f = wexp(mj[j], M);   // 0 for an empty position
+        Z += f * lj[j];
+#pragma unroll
+        for (int e = 0; e < TT::DPL; ++e) U[e] += f * acc[j][e];
+      }
+      const int packs = (a.s + PB - 1) / PB;
+      const int64_t row = (int64_t)h * packs + p0 / PB;
+      if (lane_id() == 0) {
+        a.m[row] = M;
+        a.l[row] = Z;
+      }
+      t.store(a.u + row * D, U);
+      continue;
     }
 #pragma unroll
     for (int j = 0; j < PB; ++j) {

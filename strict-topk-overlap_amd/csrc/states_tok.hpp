@@ -33,6 +33,11 @@ struct StatesArgs {
   float* m; float* l; float* u;               // [hq, s], [hq, s, d]
   const int32_t* slot_in; int slot_shared;    // hierarchical repair: skip hits
   int remap;
+  // hierarchical exact / repair (grouped pack kernel): one merged state per
+  // pack of 32 / B positions into m, l, u [hq, packs]; with slot_in, a hit's
+  // state is the prediction's (pm, pl, pu [hq, psp(, d)]) at its slot
+  int combine;
+  const float* pm; const float* pl; const float* pu; int psp;
 };
 
 constexpr int kGrpHT = 4;   // heads sharing one loaded tile (generic-tile kernels)
