@@ -23,7 +23,8 @@ BUILD = ROOT / "_build"
 ARCH = "gfx950"
 SOURCES = ["api.cpp", "states.hip", "select.hip", "repair.hip", "signed.hip", "hier.hip", "sstep.hip",
            "bounds.hip", "indexer.hip", "paged.hip", "step.hip", "tail_dense.hip", "front_pg.hip",
-           "tail_pg.hip", "stail_pg.hip", "cache.hip", "srepair.hip"]
+           "tail_pg.hip", "stail_pg.hip", "cache.hip", "srepair.hip",
+           "hier_mfma.hip"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",

@@ -523,6 +523,37 @@ def test_hierarchical_paths(dtype):
             check(out, exp_shared, ("shared", hits))
 
 
+@pytest.mark.parametrize("dtype,b,g,shared,itype,sharp", [
+    (torch.bfloat16, 4, 12, True, torch.int32, 1.0),      # c4's group tile
+    (torch.bfloat16, 4, 12, True, torch.int32, 8.0),      # near one-hot rows
+    (torch.bfloat16, 8, 16, False, torch.int64, 1.0),     # per-head rows: one pass per head
+    (torch.float16, 4, 8, False, torch.int32, 8.0),
+    (torch.float16, 8, 12, True, torch.int64, 1.0),
+    (torch.float16, 4, 16, True, torch.int32, 0.01),      # nearly flat rows
+])
+def test_hierarchical_exact_group_tile(dtype, b, g, shared, itype, sharp):
+    """gqa_hierarchical.exact on the matrix-core group tile (D = 128, 8-16
+    query heads per KV head, B = 4 or 8): selections shared by the group (one
+    tile per pack) or per head, a ragged last pack, sharp and flat softmax
+    rows (the P.V weights travel as a high and a low 16-bit part), against
+    the FP64 oracle at |err| <= 3e-4 + 3e-4 |ref| (tests/check_correctness.py:22)."""
+    from strict_topk import gqa_hierarchical as impl
+    hkv, n, d, sa = 2, 300, 128, 45
+    h = hkv * g
+    gen = torch.Generator().manual_seed(g * 100 + b + int(shared))
+    q = (torch.randn((h, d), generator=gen) * sharp).to(dtype)
+    k = torch.randn((hkv, n, b, d), generator=gen).to(dtype)
+    v = torch.randn((hkv, n, b, d), generator=gen).to(dtype)
+    if shared:
+        a = torch.randperm(n, generator=gen)[:sa].expand(h, -1).contiguous()
+    else:
+        a = torch.stack([torch.randperm(n, generator=gen)[:sa] for _ in range(h)])
+    a = a.to(itype)
+    qn, kn, vn, an = np_(q, k, v, a)
+    expected = O.attention(qn, kn, vn, an)
+    check(impl.exact(*dev(q, k, v, a)), expected, ("group tile", dtype, b, g, shared, sharp))
+
+
 # ----------------------------------------------------------- graph replays
 def _capture(fn):
     s = torch.cuda.Stream()
