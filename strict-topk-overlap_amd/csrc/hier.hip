@@ -250,7 +250,7 @@ STK_API int stk_hier_exact(const void* q, const void* k, const void* v, int dtyp
     // whole group on the matrix cores, then one LSE merge over the packs
     const int packs = (sa + 32 / b - 1) / (32 / b);
     int rc = stk_launch_hier_mfma(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa, m, l,
-                                  u, st);
+                                  u, 0, st);
     if (rc) return rc;
     return stk_launch_merge(m, l, u, nullptr, hq, packs, d, out, st);
   }

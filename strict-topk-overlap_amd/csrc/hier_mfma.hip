@@ -72,7 +72,9 @@ __device__ __forceinline__ uint32_t word(const uint4& v, int k) {
   return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
 }
 
-template <typename T, int BB, typename I>
+// BLK: per-block states [hq, s] (the block partials) instead of one merged
+// state per pack [hq, packs]
+template <typename T, int BB, typename I, bool BLK>
 __global__ __launch_bounds__(256) void k_hier_mfma(StatesArgs a) {
   using Ops = HmOps<T>;
   constexpr int D = kHmD, PB = kHmTok / BB, KS = D / 32, NT = D / 16;
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(256) void k_hier_mfma(StatesArgs a) {
   float mrow = -INFINITY, lrow = 0.f;   // head c's max and sum
   // the pack for the heads in rmask, on head th's IDs (every shuffle and
   // MFMA below runs in all lanes)
-  auto pass = [&](int th, uint32_t rmask) {
+  auto pass = [&](int th, uint32_t rmask, bool group) {
     const int xb = th * PB;   // head th's pairs lie in one 64-pair word
     const uint64_t cw = xb < STK_WAVE ? cm0 : cm1;
     const uint32_t cmask = (uint32_t)(cw >> (xb & 63)) & ((1u << PB) - 1u);
@@ -171,6 +173,113 @@ __global__ __launch_bounds__(256) void k_hier_mfma(StatesArgs a) {
       sv[e] = ok ? st[e / 4][e & 3] * scale : -INFINITY;
       mx = fmaxf(mx, sv[e]);
     }
+    if constexpr (BLK) {
+      // ---- per-block states.  Token k(g, e) lies in block
+      // (16 (e / 4) + 4 g + (e & 3)) / B: each half of a lane's tokens is one
+      // block (B = 8: shared with lane group g ^ 1), so a block's max and sum
+      // stay in the lane (one exchange for B = 8)
+      float p[8], mb[2], lb[2];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        float x = fmaxf(fmaxf(sv[4 * hf], sv[4 * hf + 1]), fmaxf(sv[4 * hf + 2], sv[4 * hf + 3]));
+        if constexpr (BB == 8) x = fmaxf(x, __shfl_xor(x, 16));
+        float y = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[4 * hf + e] = wexp(sv[4 * hf + e], x);
+          y += p[4 * hf + e];
+        }
+        if constexpr (BB == 8) y += __shfl_xor(y, 16);
+        mb[hf] = x;
+        lb[hf] = y;
+      }
+      // m and l from the lanes of their head (column c)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int j = (16 * hf + 4 * g) / BB;
+        if (on && p0 + j < a.s && (BB == 4 || (g & 1) == 0)) {
+          const int64_t row = (int64_t)(h0 + c) * a.s + p0 + j;
+          a.m[row] = mb[hf];
+          a.l[row] = lb[hf];
+        }
+      }
+      uint32_t ah[4], al[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t h0w, l0w, h1w, l1w;
+        Ops::split(p[2 * q] * Ops::kPScale, h0w, l0w);
+        Ops::split(p[2 * q + 1] * Ops::kPScale, h1w, l1w);
+        ah[q] = h0w | (h1w << 16);
+        al[q] = l0w | (l1w << 16);
+      }
+      uint4 bv[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int sh = 16 * (t & 1);
+        uint32_t bw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bw[q] = ((word(vb[2 * q], t / 2) >> sh) & 0xffffu) |
+                  (((word(vb[2 * q + 1], t / 2) >> sh) & 0xffffu) << 16);
+        bv[t] = make_uint4(bw[0], bw[1], bw[2], bw[3]);
+      }
+      // the block of P's words q (elements 2q, 2q + 1)
+      auto blk_of = [&](int q) { return (16 * (q / 2) + 4 * g + 2 * (q & 1)) / BB; };
+      constexpr float inv = 1.f / Ops::kPScale;
+      auto block_u = [&](const uint32_t (&wh)[4], const uint32_t (&wl)[4], int keep,
+                         f32x4_t (&uj)[NT]) {
+        uint32_t kh[4], kl[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          kh[q] = blk_of(q) == keep ? wh[q] : 0u;
+          kl[q] = blk_of(q) == keep ? wl[q] : 0u;
+        }
+        const uint4 xh = make_uint4(kh[0], kh[1], kh[2], kh[3]);
+        const uint4 xl = make_uint4(kl[0], kl[1], kl[2], kl[3]);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          uj[t] = Ops::mma(xh, bv[t], f32x4_t{0.f, 0.f, 0.f, 0.f});
+          uj[t] = Ops::mma(xl, bv[t], uj[t]);
+        }
+      };
+      auto store_u = [&](int64_t row, const f32x4_t (&uj)[NT], int i) {
+        float4* dst = reinterpret_cast<float4*>(a.u + row * D + 8 * c);
+        dst[0] = make_float4(uj[0][i] * inv, uj[1][i] * inv, uj[2][i] * inv, uj[3][i] * inv);
+        dst[1] = make_float4(uj[4][i] * inv, uj[5][i] * inv, uj[6][i] * inv, uj[7][i] * inv);
+      };
+      f32x4_t uj[NT];
+      if (group) {
+        // the group's heads share the tokens: block j's U for all heads at
+        // once (P restricted to block j); output rows are heads 4 g + i
+        for (int j = 0; j < PB; ++j) {
+          block_u(ah, al, j, uj);
+          if (p0 + j < a.s) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int hr = 4 * g + i;
+              if (hr < G) store_u((int64_t)(h0 + hr) * a.s + p0 + j, uj, i);
+            }
+          }
+        }
+      } else {
+        // one head: the MFMA rows become the pack's blocks.  Lane (c, g)
+        // takes head th's words (lane 16 g + th) and keeps those of block c;
+        // output rows are blocks 4 g + i
+        uint32_t th_h[4], th_l[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          th_h[q] = __shfl(ah[q], 16 * g + th);
+          th_l[q] = __shfl(al[q], 16 * g + th);
+        }
+        block_u(th_h, th_l, c, uj);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * g + i;
+          if (r < PB && p0 + r < a.s) store_u((int64_t)(h0 + th) * a.s + p0 + r, uj, i);
+        }
+      }
+      return;
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     float p[8], ls = 0.f;
@@ -213,10 +322,11 @@ __global__ __launch_bounds__(256) void k_hier_mfma(StatesArgs a) {
   };
   const uint32_t all = (1u << G) - 1u;
   if (same) {
-    pass(0, all);
+    pass(0, all, true);
   } else {
-    for (int th = 0; th < G; ++th) pass(th, 1u << th);
+    for (int th = 0; th < G; ++th) pass(th, 1u << th, false);
   }
+  if constexpr (BLK) return;
   // ---- the pack's state per head: lane (c, g) holds heads 4 g + i,
   // dimensions 8 c .. 8 c + 7 (tile t = dimension 8 c + t)
 #pragma unroll
@@ -252,7 +362,7 @@ bool stk_hier_mfma_covers(int dtype, int hq, int hkv, int b, int d, uintptr_t al
 
 int stk_launch_hier_mfma(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
                          int n, int b, int d, const void* ids, int itype, int s, float* m,
-                         float* l, float* u, hipStream_t st) {
+                         float* l, float* u, int blocks, hipStream_t st) {
   const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                           reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(u);
   if (!stk_hier_mfma_covers(dtype, hq, hkv, b, d, align) || s <= 0) return STK_EINVAL;
@@ -265,12 +375,19 @@ int stk_launch_hier_mfma(const void* q, const void* k, const void* v, int dtype,
   const int grid = (int)((items + 3) / 4);
   a.remap = grid >= 8 ? 1 : 0;
   const bool i64 = itype == IT_I64;
-#define STK_HM(TT, BBV)                                                                    \
-  do {                                                                                     \
-    if (i64)                                                                               \
-      hipLaunchKernelGGL((k_hier_mfma<TT, BBV, int64_t>), dim3(grid), dim3(256), 0, st, a); \
-    else                                                                                   \
-      hipLaunchKernelGGL((k_hier_mfma<TT, BBV, int32_t>), dim3(grid), dim3(256), 0, st, a); \
+#define STK_HM1(TT, BBV, IT)                                                                \
+  do {                                                                                      \
+    if (blocks)                                                                             \
+      hipLaunchKernelGGL((k_hier_mfma<TT, BBV, IT, true>), dim3(grid), dim3(256), 0, st, a); \
+    else                                                                                    \
+      hipLaunchKernelGGL((k_hier_mfma<TT, BBV, IT, false>), dim3(grid), dim3(256), 0, st, a); \
+  } while (0)
+#define STK_HM(TT, BBV)             \
+  do {                              \
+    if (i64)                        \
+      STK_HM1(TT, BBV, int64_t);    \
+    else                            \
+      STK_HM1(TT, BBV, int32_t);    \
   } while (0)
   if (dtype == DT_BF16) {
     if (b == 4) STK_HM(bf16s, 4);
@@ -280,5 +397,6 @@ int stk_launch_hier_mfma(const void* q, const void* k, const void* v, int dtype,
     else STK_HM(f16s, 8);
   }
 #undef STK_HM
+#undef STK_HM1
   return stk_check_launch("k_hier_mfma");
 }

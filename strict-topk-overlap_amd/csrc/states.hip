@@ -711,6 +711,14 @@ static int launch_states(StatesArgs& a, int dtype, bool with_v, bool slot, hipSt
   const uintptr_t align = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
                           reinterpret_cast<uintptr_t>(a.v);
   const int pnch = with_v && !slot ? pack_nch(dtype, a.d, a.b, align) : 0;
+  if (pnch && !a.slot_in && a.active_kind == 0 &&
+      stk_hier_mfma_covers(dtype, a.hq, a.hkv, a.b, a.d,
+                           align | reinterpret_cast<uintptr_t>(a.u))) {
+    // 8-16 query heads per KV head: the group's block states on the matrix
+    // cores (hier_mfma.hip)
+    return stk_launch_hier_mfma(a.q, a.k, a.v, dtype, a.hq, a.hkv, a.n, a.b, a.d, a.ids, a.itype,
+                                a.s, a.m, a.l, a.u, 1, st);
+  }
   if (pnch) {
     const int64_t packs = (int64_t)a.hq * ((a.s + 32 / a.b - 1) / (32 / a.b));
     const int pgrid = (int)((packs + 3) / 4);

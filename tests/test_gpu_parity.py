@@ -532,11 +532,13 @@ def test_hierarchical_paths(dtype):
     (torch.float16, 4, 16, True, torch.int32, 0.01),      # nearly flat rows
 ])
 def test_hierarchical_exact_group_tile(dtype, b, g, shared, itype, sharp):
-    """gqa_hierarchical.exact on the matrix-core group tile (D = 128, 8-16
-    query heads per KV head, B = 4 or 8): selections shared by the group (one
-    tile per pack) or per head, a ragged last pack, sharp and flat softmax
-    rows (the P.V weights travel as a high and a low 16-bit part), against
-    the FP64 oracle at |err| <= 3e-4 + 3e-4 |ref| (tests/check_correctness.py:22)."""
+    """gqa_hierarchical.exact and .partials on the matrix-core group tile
+    (D = 128, 8-16 query heads per KV head, B = 4 or 8): selections shared by
+    the group (one tile per pack) or per head (the block states then take the
+    layout whose MFMA rows are one head's blocks), a ragged last pack, sharp
+    and flat softmax rows (the P.V weights travel as a high and a low 16-bit
+    part).  Outputs against the FP64 oracle at |err| <= 3e-4 + 3e-4 |ref|
+    (tests/check_correctness.py:22); block states as in the packed-states test."""
     from strict_topk import gqa_hierarchical as impl
     hkv, n, d, sa = 2, 300, 128, 45
     h = hkv * g
@@ -551,7 +553,14 @@ def test_hierarchical_exact_group_tile(dtype, b, g, shared, itype, sharp):
     a = a.to(itype)
     qn, kn, vn, an = np_(q, k, v, a)
     expected = O.attention(qn, kn, vn, an)
-    check(impl.exact(*dev(q, k, v, a)), expected, ("group tile", dtype, b, g, shared, sharp))
+    what = ("group tile", dtype, b, g, shared, sharp)
+    check(impl.exact(*dev(q, k, v, a)), expected, what)
+    st = impl.partials(*dev(q, k, v, a))
+    ref = O.block_states(qn, kn, vn, an)
+    m, l, u = (x.cpu().double().numpy() for x in (st.m, st.l, st.u))
+    np.testing.assert_allclose(m, ref.m, rtol=1e-5, atol=1e-5, err_msg=str(what))
+    np.testing.assert_allclose(l, ref.l, rtol=1e-4, atol=1e-6, err_msg=str(what))
+    np.testing.assert_allclose(u, ref.u, rtol=1e-4, atol=1e-4, err_msg=str(what))
 
 
 # ----------------------------------------------------------- graph replays
