@@ -532,7 +532,7 @@ def test_hierarchical_paths(dtype):
     (torch.float16, 4, 16, True, torch.int32, 0.01),      # nearly flat rows
 ])
 def test_hierarchical_exact_group_tile(dtype, b, g, shared, itype, sharp):
-    """gqa_hierarchical.exact and .partials on the matrix-core group tile
+    """gqa_hierarchical.exact, .partials and the repairs on the matrix-core group tile
     (D = 128, 8-16 query heads per KV head, B = 4 or 8): selections shared by
     the group (one tile per pack) or per head (the block states then take the
     layout whose MFMA rows are one head's blocks), a ragged last pack, sharp
@@ -561,6 +561,17 @@ def test_hierarchical_exact_group_tile(dtype, b, g, shared, itype, sharp):
     np.testing.assert_allclose(m, ref.m, rtol=1e-5, atol=1e-5, err_msg=str(what))
     np.testing.assert_allclose(l, ref.l, rtol=1e-4, atol=1e-6, err_msg=str(what))
     np.testing.assert_allclose(u, ref.u, rtol=1e-4, atol=1e-4, err_msg=str(what))
+    # the repair on the same tile: misses from K/V, hits from the prediction's
+    # block states at their slots (predictions of 40 blocks: none, some or
+    # all of the selection, the rest wrong)
+    qd, kd, vd, ad = dev(q, k, v, a)
+    for hits in (0, 20, 40):
+        pd = C.prediction_rows(a, n, 40, hits).to(DEV)
+        st = impl.partials(qd, kd, vd, pd)
+        check(impl.repair_saved(qd, kd, vd, ad, pd, st), expected, what + ("saved", hits))
+        if shared:
+            check(impl.repair_saved_shared(qd, kd, vd, ad, pd, st), expected,
+                  what + ("saved_shared", hits))
 
 
 # ----------------------------------------------------------- graph replays
