@@ -15,8 +15,8 @@
 //   C  every wave reads the whole histogram and finds the threshold bin t
 //      (keys above it, keys in it) with two DPP scans, so no barrier;
 //   D  if bin t is taken whole, done; otherwise its keys (a few) are listed
-//      in LDS and every wave ranks them by (key, -index) from registers,
-//      one barrier.
+//      in LDS, wave 0 ranks them by (key, -index) from registers and
+//      publishes the last one taken, two barriers.
 // The bin map is monotone non-decreasing in the key (every rounding step is
 // monotone, NaN keys, whose key is 0, go to bin 0), so the selection is the
 // exact one whatever the ranges and roundings are.  Rows whose range is
@@ -38,6 +38,8 @@ struct TopkBinsLds {
   int ncand;
   uint64_t ck[kBinCands];
   int ci[kBinCands];
+  uint64_t star_key;       // the last selected key of the threshold bin
+  int star_idx;            // and its index
   TopkLds radix;           // the fallback's scratch
 };
 
@@ -148,21 +150,28 @@ __device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], 
           L.ci[x] = base + i;
         }
       __syncthreads();
-      const uint64_t kc = lane < cnt ? L.ck[lane] : 0ull;
-      const int ic = lane < cnt ? L.ci[lane] : 0x7fffffff;
-      int rank = 0;
-      for (int j = 0; j < cnt; ++j) {
-        const uint32_t jh = (uint32_t)__builtin_amdgcn_readlane((int)(kc >> 32), j);
-        const uint32_t jl = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kc, j);
-        const int ij = __builtin_amdgcn_readlane(ic, j);
-        const uint64_t kj = ((uint64_t)jh << 32) | jl;
-        rank += (kj > kc) || (kj == kc && ij < ic);
+      // wave 0 ranks them (a loop over the candidates; every wave doing it
+      // would run it once per wave on each SIMD) and publishes the last one
+      // taken through LDS
+      if (wave_id() == 0) {
+        const uint64_t kc = lane < cnt ? L.ck[lane] : 0ull;
+        const int ic = lane < cnt ? L.ci[lane] : 0x7fffffff;
+        int rank = 0;
+        for (int j = 0; j < cnt; ++j) {
+          const uint32_t jh = (uint32_t)__builtin_amdgcn_readlane((int)(kc >> 32), j);
+          const uint32_t jl = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kc, j);
+          const int ij = __builtin_amdgcn_readlane(ic, j);
+          const uint64_t kj = ((uint64_t)jh << 32) | jl;
+          rank += (kj > kc) || (kj == kc && ij < ic);
+        }
+        if (lane < cnt && rank == need - 1) {
+          L.star_key = kc;
+          L.star_idx = ic;
+        }
       }
-      const int star = __ffsll((long long)__ballot(lane < cnt && rank == need - 1)) - 1;
-      const uint64_t ks = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(kc >> 32), star)
-                           << 32) |
-                          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kc, star);
-      const int is = __builtin_amdgcn_readlane(ic, star);
+      __syncthreads();
+      const uint64_t ks = L.star_key;
+      const int is = L.star_idx;
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         const bool sel = bin[i] > t ||
