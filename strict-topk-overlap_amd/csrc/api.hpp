@@ -58,9 +58,10 @@ int stk_launch_states(const void* q, const void* k, const void* v, int dtype, in
                       const uint8_t* active, int active_kind, const void* pred, int ptype, int sp,
                       int32_t* slot, float* m, float* l, float* u, bool with_v, hipStream_t st);
 // The KV group's query heads on the matrix cores (hier_mfma.hip): one merged
-// state per (query head, pack of 32 tokens) into m, l, u [hq, packs], or with
-// blocks != 0 the block states [hq, s]; bf16 / fp16, D = 128, B = 4 or 8,
-// 8 <= hq / hkv <= 16, 16-byte aligned Q, K, V and u.
+// state per (query head, four packs of 32 tokens) into m, l, u
+// [hq, ceil(packs / 4)], or with blocks != 0 the block states [hq, s];
+// bf16 / fp16, D = 128, B = 4 or 8, 8 <= hq / hkv <= 16, 16-byte aligned Q,
+// K, V and u.
 bool stk_hier_mfma_covers(int dtype, int hq, int hkv, int b, int d, uintptr_t align);
 int stk_launch_hier_mfma(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
                          int n, int b, int d, const void* ids, int itype, int s, float* m,

@@ -246,13 +246,13 @@ STK_API int stk_hier_exact(const void* q, const void* k, const void* v, int dtyp
   const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                           reinterpret_cast<uintptr_t>(v);
   if (stk_hier_mfma_covers(dtype, hq, hkv, b, d, align | reinterpret_cast<uintptr_t>(u))) {
-    // small blocks, 8-16 query heads per KV head: the pack states of the
-    // whole group on the matrix cores, then one LSE merge over the packs
+    // small blocks, 8-16 query heads per KV head: the whole group on the
+    // matrix cores, one state per four packs, then one LSE merge
     const int packs = (sa + 32 / b - 1) / (32 / b);
     int rc = stk_launch_hier_mfma(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa, m, l,
                                   u, 0, st);
     if (rc) return rc;
-    return stk_launch_merge(m, l, u, nullptr, hq, packs, d, out, st);
+    return stk_launch_merge(m, l, u, nullptr, hq, (packs + 3) / 4, d, out, st);
   }
   if (stk_states_comb_covers(dtype, hq, hkv, b, d, align)) {
     // small blocks: one merged state per pack of 32 / B positions, no

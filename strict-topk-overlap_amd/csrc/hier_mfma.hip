@@ -81,9 +81,20 @@ __global__ __launch_bounds__(256) void k_hier_mfma(StatesArgs a) {
   static_assert(kHmMaxG * PB <= 2 * STK_WAVE, "two (head, position) pairs per lane");
   const int packs = (a.s + PB - 1) / PB;
   const int wg = a.remap ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
-  const int64_t item = (int64_t)wg * (blockDim.x / STK_WAVE) + wave_id();
-  if (item >= (int64_t)a.hkv * packs) return;
-  const int kv = (int)(item / packs), pack = (int)(item % packs);
+  // BLK: one wave per (KV head, pack).  Otherwise a workgroup takes four
+  // consecutive packs of one KV head (a wave past the last pack computes
+  // an empty state) and merges them before writing
+  const int pgroups = (packs + 3) / 4;
+  int kv, pack;
+  if constexpr (BLK) {
+    const int64_t item = (int64_t)wg * (blockDim.x / STK_WAVE) + wave_id();
+    if (item >= (int64_t)a.hkv * packs) return;
+    kv = (int)(item / packs);
+    pack = (int)(item % packs);
+  } else {
+    kv = wg / pgroups;
+    pack = (wg % pgroups) * 4 + wave_id();
+  }
   const int G = a.hq / a.hkv, h0 = kv * G, p0 = pack * PB;
   const int lane = lane_id(), c = lane & 15, g = lane >> 4;
   const I* ids = reinterpret_cast<const I*>(a.ids);
@@ -327,22 +338,49 @@ __global__ __launch_bounds__(256) void k_hier_mfma(StatesArgs a) {
     for (int th = 0; th < G; ++th) pass(th, 1u << th, false);
   }
   if constexpr (BLK) return;
-  // ---- the pack's state per head: lane (c, g) holds heads 4 g + i,
+  // ---- the pack's state per head to LDS: lane (c, g) holds heads 4 g + i,
   // dimensions 8 c .. 8 c + 7 (tile t = dimension 8 c + t)
+  __shared__ __align__(16) float s_u[4][kHmMaxG][D];
+  __shared__ float s_m[4][kHmMaxG], s_l[4][kHmMaxG];
+  const int w = wave_id();
+  constexpr float inv = 1.f / Ops::kPScale;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int hr = 4 * g + i;
     const float mi = __shfl(mrow, hr), li = __shfl(lrow, hr);
-    if (hr < G) {
-      const int64_t row = (int64_t)(h0 + hr) * packs + pack;
-      constexpr float inv = 1.f / Ops::kPScale;
-      float4* dst = reinterpret_cast<float4*>(a.u + row * D + 8 * c);
-      dst[0] = make_float4(ut[0][i] * inv, ut[1][i] * inv, ut[2][i] * inv, ut[3][i] * inv);
-      dst[1] = make_float4(ut[4][i] * inv, ut[5][i] * inv, ut[6][i] * inv, ut[7][i] * inv);
-      if (c == 0) {
-        a.m[row] = mi;
-        a.l[row] = li;
-      }
+    float4* dst = reinterpret_cast<float4*>(&s_u[w][hr][8 * c]);
+    dst[0] = make_float4(ut[0][i] * inv, ut[1][i] * inv, ut[2][i] * inv, ut[3][i] * inv);
+    dst[1] = make_float4(ut[4][i] * inv, ut[5][i] * inv, ut[6][i] * inv, ut[7][i] * inv);
+    if (c == 0) {
+      s_m[w][hr] = mi;
+      s_l[w][hr] = li;
+    }
+  }
+  __syncthreads();
+  // ---- one state per (head, four packs): wave w merges heads 4 w .. 4 w + 3,
+  // lane l dimensions 2 l, 2 l + 1
+  const int grp = wg % pgroups;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hr = 4 * w + i;
+    if (hr >= G) break;
+    float M = -INFINITY;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) M = fmaxf(M, s_m[x][hr]);
+    float L = 0.f, u0 = 0.f, u1 = 0.f;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const float f = wexp(s_m[x][hr], M);   // 0 for an empty pack
+      const float2 ux = *reinterpret_cast<const float2*>(&s_u[x][hr][2 * lane]);
+      L += f * s_l[x][hr];
+      u0 += f * ux.x;
+      u1 += f * ux.y;
+    }
+    const int64_t row = (int64_t)(h0 + hr) * pgroups + grp;
+    *reinterpret_cast<float2*>(a.u + row * D + 2 * lane) = make_float2(u0, u1);
+    if (lane == 0) {
+      a.m[row] = M;
+      a.l[row] = L;
     }
   }
 }
@@ -371,8 +409,10 @@ int stk_launch_hier_mfma(const void* q, const void* k, const void* v, int dtype,
   a.hq = hq; a.hkv = hkv; a.n = n; a.b = b; a.d = d; a.s = s;
   a.m = m; a.l = l; a.u = u;
   const int packs = (s + kHmTok / b - 1) / (kHmTok / b);
+  // block mode: one wave per (KV head, pack); merged mode: one workgroup per
+  // (KV head, four packs)
   const int64_t items = (int64_t)hkv * packs;
-  const int grid = (int)((items + 3) / 4);
+  const int grid = blocks ? (int)((items + 3) / 4) : hkv * ((packs + 3) / 4);
   a.remap = grid >= 8 ? 1 : 0;
   const bool i64 = itype == IT_I64;
 #define STK_HM1(TT, BBV, IT)                                                                \
