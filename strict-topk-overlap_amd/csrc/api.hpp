@@ -66,10 +66,11 @@ bool stk_hier_mfma_covers(int dtype, int hq, int hkv, int b, int d, uintptr_t al
 int stk_launch_hier_mfma(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
                          int n, int b, int d, const void* ids, int itype, int s, float* m,
                          float* l, float* u, int blocks, hipStream_t st);
-// Hierarchical exact / repair in one launch: one merged state per pack of
-// 32 / B positions ([hq, packs] into m, l, u); with slot_in, hits take the
-// prediction's states (pm, pl, pu [hq, psp]).  Covers bf16 / fp16 (and FP32)
-// packed shapes (B = 4 or 8) with an even number of query heads per KV head.
+// Hierarchical exact / repair in one launch: one merged state per four packs
+// of 32 / B positions ([hq, ceil(packs / 4)] into m, l, u); with slot_in, hits
+// take the prediction's states (pm, pl, pu [hq, psp]).  Covers bf16 / fp16
+// (and FP32) packed shapes (B = 4 or 8) with an even number of query heads
+// per KV head.
 bool stk_states_comb_covers(int dtype, int hq, int hkv, int b, int d, uintptr_t align);
 int stk_launch_states_comb(const void* q, const void* k, const void* v, int dtype, int hq,
                            int hkv, int n, int b, int d, const void* ids, int itype, int s,

@@ -262,7 +262,7 @@ STK_API int stk_hier_exact(const void* q, const void* k, const void* v, int dtyp
     int rc = stk_launch_states_comb(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa,
                                     nullptr, 0, nullptr, nullptr, nullptr, 0, m, l, u, st);
     if (rc) return rc;
-    return stk_launch_merge(m, l, u, nullptr, hq, packs, d, out, st);
+    return stk_launch_merge(m, l, u, nullptr, hq, (packs + 3) / 4, d, out, st);
   }
   int rc = stk_launch_states(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa, nullptr, 0,
                              nullptr, 0, 0, nullptr, m, l, u, true, st);
@@ -306,7 +306,7 @@ STK_API int stk_hier_repair(const void* q, const void* k, const void* v, int dty
     rc = stk_launch_states_comb(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa, slot,
                                 shared ? 1 : 0, pm, pl, pu, sp, m, l, u, st);
     if (rc) return rc;
-    return stk_launch_merge(m, l, u, nullptr, hq, packs, d, out, st);
+    return stk_launch_merge(m, l, u, nullptr, hq, (packs + 3) / 4, d, out, st);
   }
   rc = stk_launch_states_skip(q, k, v, dtype, hq, hkv, n, b, d, selected, sel_dtype, sa, slot,
                               shared ? 1 : 0, m, l, u, st);

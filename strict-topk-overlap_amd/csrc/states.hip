@@ -840,8 +840,9 @@ int stk_launch_states_comb(const void* q, const void* k, const void* v, int dtyp
   if (!pnch || G % 2 != 0 || s <= 0) return STK_EINVAL;
   if (slot_in && (!pm || !pl || !pu || psp <= 0)) return STK_EINVAL;
   const int hg = G % 4 == 0 ? 4 : 2;
-  const int64_t items = (int64_t)hkv * ((s + 32 / b - 1) / (32 / b)) * (G / hg);
-  const int grid = (int)((items + 3) / 4);
+  // one workgroup per (KV head, four packs, head group)
+  const int pgroups = ((s + 32 / b - 1) / (32 / b) + 3) / 4;
+  const int grid = hkv * pgroups * (G / hg);
   a.remap = grid >= 8 ? 1 : 0;
   const bool i64 = itype == IT_I64;
 #define STK_COMB(BBV, HGV)                                                                        \

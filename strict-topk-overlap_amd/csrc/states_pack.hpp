@@ -178,15 +178,31 @@ __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) 
   const int packs = (a.s + PB - 1) / PB;
   const int G = a.hq / a.hkv;
   const int hgs = G / HG;
-  const int64_t item = (int64_t)wg * waves + wave_id();
-  if (item >= (int64_t)a.hkv * packs * hgs) return;
-  const int hg = (int)(item % hgs);
-  const int64_t rest = item / hgs;
-  const int pack = (int)(rest % packs);
-  const int kv = (int)(rest / packs);
+  // COMB: a workgroup takes four consecutive packs of one head group (a wave
+  // past the last pack computes an empty state) and merges them in LDS;
+  // workgroups are ordered (KV head, four packs, head group), so the head
+  // groups of the same packs are adjacent and land on one XCD
+  const int pgroups = (packs + 3) / 4;
+  int hg, pack, kv;
+  if constexpr (COMB) {
+    hg = wg % hgs;
+    const int rest = wg / hgs;
+    pack = (rest % pgroups) * 4 + wave_id();
+    kv = rest / pgroups;
+  } else {
+    const int64_t item = (int64_t)wg * waves + wave_id();
+    if (item >= (int64_t)a.hkv * packs * hgs) return;
+    hg = (int)(item % hgs);
+    const int64_t rest = item / hgs;
+    pack = (int)(rest % packs);
+    kv = (int)(rest / packs);
+  }
   const int h0 = kv * G + hg * HG;
   const int p0 = pack * PB;
   const I* ids = reinterpret_cast<const I*>(a.ids);
+  // COMB: the four waves' pack states, merged after the head loop
+  __shared__ float s_cu[COMB ? 4 : 1][COMB ? HG : 1][COMB ? D : 1];
+  __shared__ float s_cm[COMB ? 4 : 1][COMB ? HG : 1], s_cl[COMB ? 4 : 1][COMB ? HG : 1];
   TT t;
   t.init();
   // ---- round trip 1: the group's IDs at the pack (lane i * PB + j holds
@@ -361,13 +377,12 @@ __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) 
 #pragma unroll
         for (int e = 0; e < TT::DPL; ++e) U[e] += f * acc[j][e];
       }
-      const int packs = (a.s + PB - 1) / PB;
-      const int64_t row = (int64_t)h * packs + p0 / PB;
       if (lane_id() == 0) {
-        a.m[row] = M;
-        a.l[row] = Z;
+        s_cm[wave_id()][i] = M;
+        s_cl[wave_id()][i] = Z;
       }
-      t.store(a.u + row * D, U);
+#pragma unroll
+      for (int e = 0; e < TT::DPL; ++e) s_cu[wave_id()][i][lane_id() * TT::DPL + e] = U[e];
       continue;
     }
 #pragma unroll
@@ -380,6 +395,32 @@ __device__ __forceinline__ void states_pack_grp_wg(const StatesArgs& a, int wg) 
         a.l[row] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lb[u]), src));
       }
       t.store(a.u + row * D, acc[j]);
+    }
+  }
+  if constexpr (COMB) {
+    // one state per (head, four packs): wave x merges head x of the group
+    __syncthreads();
+    const int x = wave_id();
+    if (x < HG) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int y = 0; y < 4; ++y) M = fmaxf(M, s_cm[y][x]);
+      float L = 0.f, U[TT::DPL];
+#pragma unroll
+      for (int e = 0; e < TT::DPL; ++e) U[e] = 0.f;
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        const float f = wexp(s_cm[y][x], M);   // 0 for an empty pack
+        L += f * s_cl[y][x];
+#pragma unroll
+        for (int e = 0; e < TT::DPL; ++e) U[e] += f * s_cu[y][x][lane_id() * TT::DPL + e];
+      }
+      const int64_t row = (int64_t)(h0 + x) * pgroups + pack / 4;
+      if (lane_id() == 0) {
+        a.m[row] = M;
+        a.l[row] = L;
+      }
+      t.store(a.u + row * D, U);
     }
   }
 }
