@@ -41,6 +41,15 @@ __device__ __forceinline__ void repair_membership(const GqaRepairArgs& a, int h,
                                                   int* nh, int* nm, bool staged) {
   const int n = a.kv.n;
   const bool use_map = n <= kRepairMapN;
+  // the predicted row's IDs are requested with the selected row's (up to
+  // two per thread; longer rows load theirs after the map is cleared)
+  const bool pre = use_map && a.sp <= 2 * (int)blockDim.x;
+  int64_t pv[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int p = threadIdx.x + r * (int)blockDim.x;
+    pv[r] = pre && p < a.sp ? load_id(a.p, a.ptype, (int64_t)h * a.sp + p) : -1;
+  }
   if (use_map)
     for (int i = threadIdx.x; i < n; i += blockDim.x) map[i] = 0;
   if (!staged)
@@ -51,9 +60,15 @@ __device__ __forceinline__ void repair_membership(const GqaRepairArgs& a, int h,
       pids[p] = (int)load_id(a.p, a.ptype, (int64_t)h * a.sp + p);
   __syncthreads();
   if (use_map) {
-    for (int p = threadIdx.x; p < a.sp; p += blockDim.x) {
-      int64_t id = load_id(a.p, a.ptype, (int64_t)h * a.sp + p);
-      if (id >= 0 && id < n) atomicMax(&map[id], p + 1);
+    if (pre) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        if (pv[r] >= 0 && pv[r] < n) atomicMax(&map[pv[r]], threadIdx.x + r * (int)blockDim.x + 1);
+    } else {
+      for (int p = threadIdx.x; p < a.sp; p += blockDim.x) {
+        int64_t id = load_id(a.p, a.ptype, (int64_t)h * a.sp + p);
+        if (id >= 0 && id < n) atomicMax(&map[id], p + 1);
+      }
     }
     __syncthreads();
   }
@@ -75,9 +90,12 @@ __device__ __forceinline__ void repair_membership(const GqaRepairArgs& a, int h,
     nhit += slot >= 0;
     nmiss += slot < 0 && id >= 0 && id < n;
   }
-  int total_hit, total_miss;
-  int hpos = block_excl_scan(nhit, tmp, &total_hit);
-  int mpos = block_excl_scan(nmiss, tmp, &total_miss);
+  // one scan of packed counts (at most 8 positions per thread, so both
+  // totals stay below 2^16)
+  int total;
+  const int pre_sum = block_excl_scan1(nhit | (nmiss << 16), tmp, &total);
+  int hpos = pre_sum & 0xffff, mpos = pre_sum >> 16;
+  const int total_hit = total & 0xffff, total_miss = total >> 16;
   for (int j = j0, c = 0; j < j1; ++j, ++c) {
     if (my_slot[c] >= 0) rows[hpos++] = my_slot[c];
     else if (my_id[c] >= 0 && my_id[c] < n) ids[mpos++] = my_id[c];   // compacted in place
