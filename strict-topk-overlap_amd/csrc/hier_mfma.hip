@@ -1,6 +1,7 @@
 // Hierarchical exact attention on the matrix cores: one wave per (KV head,
 // pack of 32 tokens) computes the pack's softmax state for all G <= 16 query
-// heads of the KV group with 16x16x32 MFMAs.
+// heads of the KV group with 16x16x32 MFMAs, and a workgroup merges its four
+// waves' packs in LDS before writing.
 //
 // Reference: strict_topk/gqa_hierarchical.py:22-112 (exact: block states,
 // then two merge levels).  The LSE merge is associative, so one state per
@@ -73,7 +74,7 @@ __device__ __forceinline__ uint32_t word(const uint4& v, int k) {
 }
 
 // BLK: per-block states [hq, s] (the block partials) instead of one merged
-// state per pack [hq, packs]
+// state per four packs [hq, ceil(packs / 4)]
 template <typename T, int BB, typename I, bool BLK>
 __global__ __launch_bounds__(256) void k_hier_mfma(StatesArgs a) {
   using Ops = HmOps<T>;
