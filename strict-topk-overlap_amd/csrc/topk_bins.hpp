@@ -10,8 +10,8 @@
 //   A  the row's range: per-wave max / min of the keys' high 32 bits (DPP),
 //      one barrier;
 //   B  a 1024-bin histogram, linear in the score value over that range
-//      (bin = (s - lo) * 1024 / (hi - lo) in FP32, clamped), one LDS atomic
-//      per key on mostly distinct addresses, one barrier;
+//      (bin = (s - lo) * 1024 / (hi - lo) in FP32, clamped), and the sums of
+//      its 16-bin groups, two LDS atomics per key, one barrier;
 //   C  every wave reads the whole histogram and finds the threshold bin t
 //      (keys above it, keys in it) with two DPP scans, so no barrier;
 //   D  if bin t is taken whole, done; otherwise its keys (a few) are listed
@@ -30,10 +30,12 @@
 namespace stk {
 
 constexpr int kBins = 1024;
+static_assert(kBins / 16 == STK_WAVE, "one 16-bin group per lane");
 constexpr int kBinCands = 64;
 
 struct TopkBinsLds {
   __align__(16) int hist[kBins];
+  int grp[kBins / 16];     // sums of 16 consecutive bins (phase C reads one per lane)
   uint32_t red[2][16];     // per-wave max / min of the keys' high words
   int ncand;
   uint64_t ck[kBinCands];
@@ -89,6 +91,7 @@ __device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], 
     L.red[1][wave_id()] = hmin;
   }
   for (int i = threadIdx.x; i < kBins; i += blockDim.x) L.hist[i] = 0;
+  if (threadIdx.x < kBins / 16) L.grp[threadIdx.x] = 0;
   if (threadIdx.x == 0) L.ncand = 0;
   __syncthreads();
   between();
@@ -111,15 +114,15 @@ __device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], 
     for (int i = 0; i < KPT; ++i) {
       const float x = (key_value(key[i]) - lo) * inv;   // NaN for key 0
       bin[i] = x >= (float)(kBins - 1) ? kBins - 1 : (x > 0.f ? (int)x : 0);
-      if (base + i < n) atomicAdd(&L.hist[bin[i]], 1);
+      if (base + i < n) {
+        atomicAdd(&L.hist[bin[i]], 1);
+        atomicAdd(&L.grp[bin[i] >> 4], 1);
+      }
     }
     __syncthreads();
-    // ---- C: threshold bin, every wave alike.  Lane l sums bins
+    // ---- C: threshold bin, every wave alike.  Lane l takes the sum of bins
     // [kBins - 16 (l + 1), kBins - 16 l), lane 0 the top ones.
-    const int4* h4 = reinterpret_cast<const int4*>(L.hist + kBins - 16 * (lane + 1));
-    const int4 b0 = h4[0], b1 = h4[1], b2 = h4[2], b3 = h4[3];
-    const int s = b0.x + b0.y + b0.z + b0.w + b1.x + b1.y + b1.z + b1.w + b2.x + b2.y + b2.z +
-                  b2.w + b3.x + b3.y + b3.z + b3.w;
+    const int s = L.grp[kBins / 16 - 1 - lane];
     const int cum = wave_incl_scan_dpp(s);
     const int L16 = __ffsll((long long)__ballot(cum >= k)) - 1;
     const int above16 = __builtin_amdgcn_readlane(cum - s, L16);
