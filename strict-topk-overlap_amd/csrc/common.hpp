@@ -219,6 +219,18 @@ __device__ __forceinline__ float wave_sum_u(float v) {
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (STK_WAVE - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / STK_WAVE; }
 
+// Map a launch-order workgroup index to a logical index so that every XCD
+// (workgroups are dealt round-robin over 8 XCDs) receives one contiguous
+// range of logical workgroups.  Consecutive logical items share KV heads, so
+// their tiles meet in the same XCD-local L2.  A bijection on [0, total).
+__device__ __forceinline__ int xcd_remap(int w, int total) {
+  constexpr int X = 8;
+  int xcd = w % X, r = w / X;
+  int base = total / X, extra = total % X;
+  int start = xcd * base + (xcd < extra ? xcd : extra);
+  return start + r;
+}
+
 template <typename F>
 __device__ __forceinline__ float xor_reduce(float v, int from, int to, F op) {
   // combine lanes with xor offsets from, 2*from, ..., to (inclusive)

@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kRepairThreads) void k_gqa_repair(GqaRepairArgs a) 
   extern __shared__ int lds_i[];
   __shared__ int tmp[kRepairWaves];
   __shared__ float wm[kRepairWaves], wl[kRepairWaves];
-  gqa_repair_head<Stream, CHUNKS, VROW>(a, blockIdx.x, lds_i, tmp, wm, wl, false);
+  gqa_repair_head<Stream, CHUNKS, VROW>(a, xcd_remap(blockIdx.x, gridDim.x), lds_i, tmp, wm, wl, false);
 }
 
 }  // namespace stk

@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kTailThreads) void k_srepair(SRepairArgs a) {
   __shared__ __align__(16) float s_hu[kTailWaves][D];
   __shared__ __align__(16) float s_nu[kTailWaves][D];
   __shared__ __align__(16) float s_wu[kTailWaves][D];
-  const int h = blockIdx.x, tid = threadIdx.x, w = wave_id();
+  const int h = xcd_remap(blockIdx.x, gridDim.x), tid = threadIdx.x, w = wave_id();
   const int sa = a.sa, sp = a.sp, n = a.kv.n, b = a.kv.b;
   const int nmap = n < kSrMap ? n : kSrMap;
   const bool hybrid = a.hybrid != 0;

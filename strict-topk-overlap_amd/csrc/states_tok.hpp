@@ -11,18 +11,6 @@
 
 namespace stk {
 
-// Map a launch-order workgroup index to a logical index so that every XCD
-// (workgroups are dealt round-robin over 8 XCDs) receives one contiguous
-// range of logical workgroups.  Consecutive logical items share KV heads, so
-// their tiles meet in the same XCD-local L2.
-__device__ __forceinline__ int xcd_remap(int w, int total) {
-  constexpr int X = 8;
-  int xcd = w % X, r = w / X;
-  int base = total / X, extra = total % X;
-  int start = xcd * base + (xcd < extra ? xcd : extra);
-  return start + r;
-}
-
 struct StatesArgs {
   const void* q; const void* k; const void* v;
   const void* ids; int itype;

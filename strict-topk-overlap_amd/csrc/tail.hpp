@@ -69,7 +69,7 @@ __device__ __forceinline__ void tail_head(const TailArgs& a) {
   __shared__ __align__(16) float s_hu[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_wu[kTailWaves][D];
   __shared__ int mtk[PG ? kTailMaxK : 1];   // PG: tokens of each listed miss
-  const int h = blockIdx.x;
+  const int h = xcd_remap(blockIdx.x, gridDim.x);   // a KV group's heads on one XCD
   const int nrow = a.kv.n, sp = a.sp;
   const int tid = threadIdx.x, w = wave_id();
   const int G = a.kv.hq / a.kv.hkv;

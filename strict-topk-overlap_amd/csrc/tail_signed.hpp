@@ -93,7 +93,7 @@ __device__ __forceinline__ void stail_head(const STailArgs& a) {
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves];
   __shared__ float s_wu[kTailWaves][D];
   __shared__ int mtk[PG ? kTailMaxK : 1];   // PG: tokens of each listed miss
-  const int h = blockIdx.x;
+  const int h = xcd_remap(blockIdx.x, gridDim.x);   // a KV group's heads on one XCD
   const int nrow = a.kv.n, sp = a.sp;
   const int tid = threadIdx.x, w = wave_id();
   const int G = a.kv.hq / a.kv.hkv;
