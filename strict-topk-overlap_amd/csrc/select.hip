@@ -31,6 +31,7 @@ namespace stk {
 constexpr int kTopkThreads = 256;
 constexpr int kTopkWide = 1024;     // threads of k_topk_wide (16 waves)
 constexpr int kWideRows = 4;        // rows up to which k_topk_wide is used
+constexpr int kFewRows = 256;       // rows up to which a row gets four keys per thread
 template <typename Q, int P, int STEPS, bool FULL, int GT>
 __global__ __launch_bounds__(256) void k_score(ScoreArgs a) {
   score_wg<Q, P, STEPS, FULL, GT>(a, blockIdx.x);
@@ -231,8 +232,7 @@ int stk_launch_score(const void* q, int q_dtype, const void* lo, const void* hi,
   return stk_check_launch("k_score");
 }
 
-// 1024-thread rows for a few long rows (the shared selection's single row):
-// measured on MI355X, 32 rows of 2048 keys are faster at 256 threads.
+// 1024-thread rows for a few long rows (the shared selection's single row).
 static bool wide_topk(int rows, int n) { return rows <= kWideRows && n > 1024 && n <= 16384; }
 
 int stk_launch_topk(const uint64_t* keys, int rows, int n, int k, int32_t* ids, hipStream_t st) {
@@ -244,6 +244,17 @@ int stk_launch_topk(const uint64_t* keys, int rows, int n, int k, int32_t* ids, 
     else if (n <= 4096) hipLaunchKernelGGL(k_topk_wide<4>, grid, wb, 0, st, t);
     else if (n <= 8192) hipLaunchKernelGGL(k_topk_wide<8>, grid, wb, 0, st, t);
     else hipLaunchKernelGGL(k_topk_wide<16>, grid, wb, 0, st, t);
+    return stk_check_launch("k_topk_wide");
+  }
+  // up to 256 rows of 1024 < n <= 8192 keys: four keys per thread up to 4096
+  // keys (512 or 1024 threads), eight above.  Measured on MI355X against 256
+  // threads (select_blocks, IDs identical): 32 rows of 2048 keys 9.3 -> 8.5 us,
+  // of 4000 keys 14.0 -> 11.7 us, of 8000 keys 25.8 -> 21.3 us; 128 rows of
+  // 4000 keys 25.5 -> 22.9 us.  Rows past 256 keep the 256-thread kernels.
+  if (rows <= kFewRows && n > 1024 && n <= 8192) {
+    if (n <= 2048) hipLaunchKernelGGL(k_topk_wide<4>, grid, dim3(512), 0, st, t);
+    else if (n <= 4096) hipLaunchKernelGGL(k_topk_wide<4>, grid, dim3(kTopkWide), 0, st, t);
+    else hipLaunchKernelGGL(k_topk_wide<8>, grid, dim3(kTopkWide), 0, st, t);
     return stk_check_launch("k_topk_wide");
   }
   if (n <= 256) hipLaunchKernelGGL(k_topk<1>, grid, block, 0, st, t);

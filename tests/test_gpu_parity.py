@@ -93,6 +93,24 @@ def test_select_ties_and_row_lengths(n, topk):
     assert ids[1].cpu().tolist() == list(range(topk))
 
 
+@pytest.mark.parametrize("n,topk", [(1025, 64), (2048, 2048), (3000, 64), (4096, 1000),
+                                    (4097, 64), (6000, 700), (8192, 8192)])
+def test_select_ties_many_rows(n, topk):
+    """The launch for up to 256 rows of 1024 < n <= 8192 keys (four or eight
+    keys per thread): tied scores, every row length bracket, k == n."""
+    from strict_topk import gqa
+    gen = torch.Generator().manual_seed(7 * n + topk)
+    hq, hkv, d = 16, 4, 16
+    q = torch.randint(-2, 3, (hq, d), generator=gen).to(torch.bfloat16)
+    lo = torch.randint(-3, 1, (hkv, n, d), generator=gen).float()
+    hi = lo + torch.randint(0, 3, (hkv, n, d), generator=gen).float()
+    q[3].zero_()
+    ref = O.select_blocks(*np_(q, lo, hi), topk)
+    ids = gqa.select_blocks(*dev(q, lo, hi), topk)
+    assert ids.cpu().numpy().tolist() == ref.tolist()
+    assert ids[3].cpu().tolist() == list(range(topk))
+
+
 def test_select_nonfinite_bounds():
     """-inf/+inf bounds and NaN scores: NaN ranks below -inf."""
     from strict_topk import gqa
