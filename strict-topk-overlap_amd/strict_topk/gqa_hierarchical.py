@@ -3,7 +3,13 @@
 Drop-in for the reference ``strict_topk/gqa_hierarchical.py`` (``partials``
 :55-61, ``exact`` :111-112, ``repair_saved`` :133-134,
 ``repair_saved_shared`` :137-144): per-block states, a level-1 merge of 32
-positions and a final LSE merge.
+positions and a final LSE merge.  The LSE merge is associative, so the
+library merges in the order its kernels like: ``exact`` computes one state
+per pack of 32 tokens for a whole KV group on the matrix cores
+(``k_hier_mfma``, 8-16 query heads per KV head at D = 128) or on the vector
+units (``k_states_pack_comb``), four packs merged in LDS, then one merge
+over the packs; the repairs take the hits' states from the prediction and
+recompute the rest the same way; ``partials`` returns per-block states.
 """
 import torch
 
