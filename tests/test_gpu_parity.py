@@ -93,14 +93,18 @@ def test_select_ties_and_row_lengths(n, topk):
     assert ids[1].cpu().tolist() == list(range(topk))
 
 
-@pytest.mark.parametrize("n,topk", [(1025, 64), (2048, 2048), (3000, 64), (4096, 1000),
-                                    (4097, 64), (6000, 700), (8192, 8192)])
-def test_select_ties_many_rows(n, topk):
-    """The launch for up to 256 rows of 1024 < n <= 8192 keys (four or eight
-    keys per thread): tied scores, every row length bracket, k == n."""
+@pytest.mark.parametrize("hq,hkv,n,topk", [(16, 4, 1025, 64), (16, 4, 2048, 2048),
+                                            (16, 4, 3000, 64), (16, 4, 4096, 1000),
+                                            (16, 4, 4097, 64), (16, 4, 6000, 700),
+                                            (16, 4, 8192, 8192), (288, 4, 2048, 64),
+                                            (288, 4, 4000, 300), (288, 4, 8000, 64)])
+def test_select_ties_many_rows(hq, hkv, n, topk):
+    """Up to 256 rows of 1024 < n <= 8192 keys take four or eight keys per
+    thread, more rows the 256-thread kernels: tied scores, every row length
+    bracket, k == n."""
     from strict_topk import gqa
-    gen = torch.Generator().manual_seed(7 * n + topk)
-    hq, hkv, d = 16, 4, 16
+    gen = torch.Generator().manual_seed(7 * n + topk + hq)
+    d = 16
     q = torch.randint(-2, 3, (hq, d), generator=gen).to(torch.bfloat16)
     lo = torch.randint(-3, 1, (hkv, n, d), generator=gen).float()
     hi = lo + torch.randint(0, 3, (hkv, n, d), generator=gen).float()
