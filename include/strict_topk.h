@@ -251,9 +251,10 @@ int stk_step_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk
 /* The full speculative decode step of benchmarks/run_benchmark.py:99-118
  * (overlap_run: gqa.select_blocks || gqa.partials on the predicted blocks,
  * then gqa_light.repair_saved_light / gqa.repair_saved, or gqa.repair_union
- * with union_mode 1) in two launches on one stream: a grid whose workgroups
- * either score blocks or compute the predicted blocks' states, then one
- * workgroup per query head doing the exact top-K and the repair.  Outputs:
+ * with union_mode 1) on one stream: one launch where stk_step1_supported
+ * says so, otherwise two launches (a grid whose workgroups either score
+ * blocks or compute the predicted blocks' states, then one workgroup per
+ * query head doing the exact top-K and the repair).  Outputs:
  * selected[Hq,topk] int32 (ascending IDs, as stk_select_blocks), the
  * prediction state m,l[Hq,sp], u[Hq,sp,D] (as stk_block_partials) and
  * out[Hq,D].  bf16/fp16 only, int32 predicted IDs, D in {64, 128, 256}. */
@@ -262,6 +263,27 @@ int stk_speculative_step(const void* q, const void* k, const void* v, int dtype,
                          int topk, const void* predicted, int pred_dtype, int sp,
                          int union_mode, int32_t* selected, float* m, float* l, float* u,
                          float* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* 1 when stk_speculative_step (and stk_speculative_step_noalloc) run the
+ * shape as ONE launch: bf16/fp16, B = 32, D in {64, 128}, at most four query
+ * heads per KV head, SP * D <= 8192, Hq * (ceil(N / 64) + SP) < 16384, within
+ * the shapes of stk_step_supported.  The one launch is a grid whose workgroups score
+ * blocks, compute the predicted blocks' states, or (the last Hq workgroups)
+ * wait for their head's scores, run the top-K and the repair while the
+ * states still stream, then wait for the states and merge; the roles hand
+ * over through flags the library keeps in static device memory, one slot per
+ * stream (64 slots per device; with every slot taken the step runs as two
+ * launches).  Results are the two launches' results, bit for bit.  No
+ * reference counterpart beyond the step it computes
+ * (benchmarks/run_benchmark.py:99-118). */
+int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
+                        int pred_dtype);
+
+/* Slots of the current device whose one-launch step ever timed out waiting
+ * for a flag (each wait gives up after 20 ms, so every launch ends); 0 in any
+ * correct run.  A host-side query that copies from the device (it waits for
+ * the device); for tests. */
+int stk_step1_timeouts(void);
 
 /* Allocation-free variant of stk_speculative_step.  It has no counterpart in
  * the reference: it is for callers that cannot allocate (code under HIP graph

@@ -402,6 +402,65 @@ __device__ __forceinline__ uint64_t wave_and64(uint64_t v) {
   return v;
 }
 
+
+// ------------------------------------------------ agent-scope publication
+// Accesses coherent at agent scope (global_{load,store} ... sc1): a store
+// goes past the XCD-local L2 to the device's coherence point, and a load
+// never takes a stale line from the L2.  A producer publishes data written
+// this way with wait_stores() and then a flag store; a consumer that sees the
+// flag set (reading it this way) and then reads the data this way sees the
+// data.  No cache-wide fence (L2 write-back) is needed, because every
+// published word was itself written coherently.  (These are the code
+// sequences of relaxed agent-scope atomics on gfx950.)
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  st_agent(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+// two floats at an 8-byte aligned address, one store
+__device__ __forceinline__ void st_agent2(float* p, float a, float b) {
+  st_agent(reinterpret_cast<uint64_t*>(p),
+           ((uint64_t)__float_as_uint(b) << 32) | __float_as_uint(a));
+}
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agentf(const float* p) {
+  return __uint_as_float(ld_agent(reinterpret_cast<const uint32_t*>(p)));
+}
+// Wait until every memory access of this wave has completed, stores
+// included (gfx9 counts both in vmcnt), and keep the compiler from moving
+// memory accesses across the wait.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Longest wait for a flag, in ticks of the 100 MHz real-time counter
+// (20 ms); past it the waiter records an error and goes on, so every wave
+// ends whatever the flags hold.
+constexpr uint64_t kSpinTicks = 2000000ull;
+
+// Wave-level bounded wait until flag[i] != 0 for every i < cnt; false (and
+// *err incremented) on time-out.  Every lane returns together.
+__device__ __forceinline__ bool wait_flags(const uint32_t* flag, int cnt, uint32_t* err) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (true) {
+    int ready = 1;
+    for (int i = lane_id(); i < cnt; i += STK_WAVE) ready &= ld_agent(flag + i) != 0u;
+    if (__all(ready)) return true;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
+      if (lane_id() == 0) atomicAdd(err, 1u);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 __device__ __forceinline__ bool is_bad(float x) { return !(fabsf(x) <= 3.402823466e38f); }
 
 }  // namespace stk

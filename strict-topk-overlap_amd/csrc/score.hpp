@@ -51,6 +51,7 @@ struct ScoreArgs {
   int chunks;            // workgroups per KV head
   float* scores;         // optional FP32 [hq, n]
   uint64_t* keys;        // optional [hq, n]
+  uint32_t* sflag;       // SIG: [hq, chunks], set once a chunk's keys are published
 };
 
 // Physical lane (0..15 inside a row) -> logical lane of the summation order.
@@ -111,7 +112,13 @@ __device__ __forceinline__ double score_rowsum(double (&v)[C], int l16) {
 // element by element.  PG: paged, batched bounds (lo/hi are pages [P, D],
 // a.n is the block table's row width, a row's blocks past its request's
 // count are not scored, and a block on an invalid page gets key 0).
-template <typename Q, int P, int STEPS, bool FULL, int GT, bool PG = false>
+// WV: waves per workgroup (a chunk is WV * 4 * STEPS blocks).  SIG (the
+// one-launch step): the keys are stored agent-coherent and, once all of the
+// workgroup's stores have completed, the chunk's flag of every query head of
+// the group is set; the query values are requested before the bounds (one
+// stage: G <= GT and GT * 64 * P <= blockDim).
+template <typename Q, int P, int STEPS, bool FULL, int GT, bool PG = false, bool SIG = false,
+          int WV = kScoreWaves>
 __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
                                          const Paging& pg = Paging{}) {
   constexpr int C = GT * STEPS;           // (head, block) sums per wave
@@ -126,7 +133,7 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
   const int l16 = lane & 15;
   const int c = score_lane(l16);              // logical lane
   const int sub = lane >> 4;                  // block within a 4-block step
-  const int wave_base = (chunk * kScoreWaves + wave_id()) * (4 * STEPS);
+  const int wave_base = (chunk * WV + wave_id()) * (4 * STEPS);
   // PG: the table entries and the row's block count are requested together
   // (the entries' loads are bounded by the table width, not by the count)
   int pgs[PG ? STEPS : 1];
@@ -138,7 +145,26 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
     }
   }
   const int nv = PG ? pg_blocks(pg, kv, a.n) : a.n;   // blocks of this row
-  if (PG && chunk * kScoreWaves * 4 * STEPS >= nv) return;   // whole workgroup
+  if (PG && chunk * WV * 4 * STEPS >= nv) return;   // whole workgroup
+  const Q* qbase = reinterpret_cast<const Q*>(a.q) + (size_t)h0 * a.d;
+  // SIG: this thread's query value goes out before the bounds, so the
+  // staging below does not wait behind their round trip
+  float qpre = 0.f;
+  if constexpr (SIG) {
+    const int x = threadIdx.x;
+    const int gi = x / (64 * P), dim = x % (64 * P);
+    const bool ok = x < QN && gi < G && dim < a.d;
+    const Q qr = qbase[ok ? (size_t)gi * a.d + dim : 0];
+    qpre = ok ? cvt(qr) : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  auto stage_q = [&] {
+    if ((int)threadIdx.x < QN) {
+      s_q[threadIdx.x] = (double)qpre;
+      s_m[threadIdx.x] = qpre >= 0.f ? 0u : ~0u;   // lo where q < 0 or q is NaN
+    }
+    __syncthreads();
+  };
   // every lo/hi load of the wave is issued before any arithmetic, with no
   // branch around a load: blocks past n read row 0 and are not stored
   float4 lv[STEPS][P], hv[STEPS][P];
@@ -190,6 +216,7 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
         hv[s][j] = make_float4(__uint_as_float(h2.x), __uint_as_float(h2.y), 0.f, 0.f);
       }
     }
+    if constexpr (SIG) stage_q();   // while the bounds travel
 #pragma unroll
     for (int s = 0; s < STEPS; ++s)
 #pragma unroll
@@ -230,18 +257,20 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
         }
       }
     }
+    if constexpr (SIG) stage_q();
   }
-  const Q* qbase = reinterpret_cast<const Q*>(a.q) + (size_t)h0 * a.d;
   for (int gb = 0; gb < G; gb += GT) {
-    if (gb) __syncthreads();   // previous stage fully read
-    for (int x = threadIdx.x; x < QN; x += blockDim.x) {
-      const int gi = x / (64 * P), dim = x % (64 * P);
-      const bool ok = gb + gi < G && dim < a.d;
-      const float qv = ok ? cvt(qbase[(size_t)(gb + gi) * a.d + dim]) : 0.f;
-      s_q[x] = (double)qv;
-      s_m[x] = qv >= 0.f ? 0u : ~0u;   // lo where q < 0 or q is NaN
+    if constexpr (!SIG) {   // SIG: staged once, above
+      if (gb) __syncthreads();   // previous stage fully read
+      for (int x = threadIdx.x; x < QN; x += blockDim.x) {
+        const int gi = x / (64 * P), dim = x % (64 * P);
+        const bool ok = gb + gi < G && dim < a.d;
+        const float qv = ok ? cvt(qbase[(size_t)(gb + gi) * a.d + dim]) : 0.f;
+        s_q[x] = (double)qv;
+        s_m[x] = qv >= 0.f ? 0u : ~0u;   // lo where q < 0 or q is NaN
+      }
+      __syncthreads();
     }
-    __syncthreads();
     double acc[C];
 #pragma unroll
     for (int i = 0; i < C; ++i) acc[i] = 0.0;
@@ -280,8 +309,16 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
       if (r == 0.0) r = 0.0;
       const size_t o = (size_t)(h0 + gb + gi) * a.n + nb;
       if (a.scores) a.scores[o] = (float)r;
-      if (a.keys) a.keys[o] = (PG && ((dead >> s) & 1)) ? 0ull : score_key(r);
+      const uint64_t key = (PG && ((dead >> s) & 1)) ? 0ull : score_key(r);
+      if constexpr (SIG) st_agent(a.keys + o, key);
+      else if (a.keys) a.keys[o] = key;
     }
+  }
+  if constexpr (SIG) {
+    // publish the chunk to every query head of the group
+    wait_stores();
+    __syncthreads();
+    if ((int)threadIdx.x < G) st_agent(a.sflag + (size_t)(h0 + threadIdx.x) * a.chunks + chunk, 1u);
   }
 }
 

@@ -26,6 +26,7 @@ struct StatesArgs {
   // state is the prediction's (pm, pl, pu [hq, psp(, d)]) at its slot
   int combine;
   const float* pm; const float* pl; const float* pu; int psp;
+  uint32_t* tflag;                            // SIG: [hq * s], set once an item's state is published
 };
 
 constexpr int kGrpHT = 4;   // heads sharing one loaded tile (generic-tile kernels)
@@ -46,7 +47,9 @@ constexpr int kGrpHT = 4;   // heads sharing one loaded tile (generic-tile kerne
 // block is streamed chunk by chunk.  PG: paged, batched KV (a.n is the block
 // table's row width; an ID at or past its request's block count, or on an
 // invalid page, gets the empty state).
-template <typename T, int NCH, int UP, typename I, bool ONE, bool PG = false>
+// SIG (the one-launch step): the state is stored agent-coherent and, once
+// the wave's stores have completed, the item's flag is set.
+template <typename T, int NCH, int UP, typename I, bool ONE, bool PG = false, bool SIG = false>
 __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg,
                                               const Paging& pg = Paging{}) {
   using TT = TokTile<T, NCH, UP>;
@@ -103,11 +106,21 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg,
       else t.template update<false, false>(qw, kw, vw, t0, a.b, scale, m, l, acc);
     }
   }
-  if (lane_id() == 0) {
-    a.m[item] = m;
-    a.l[item] = l;
+  if constexpr (SIG) {
+    if (lane_id() == 0) {
+      st_agent(a.m + item, m);
+      st_agent(a.l + item, l);
+    }
+    t.store_agent(a.u + item * a.d, acc);
+    wait_stores();
+    if (lane_id() == 0) st_agent(a.tflag + item, 1u);
+  } else {
+    if (lane_id() == 0) {
+      a.m[item] = m;
+      a.l[item] = l;
+    }
+    t.store(a.u + item * a.d, acc);
   }
-  t.store(a.u + item * a.d, acc);
 }
 
 }  // namespace stk

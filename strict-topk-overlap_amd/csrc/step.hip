@@ -19,7 +19,7 @@
 // stk_gqa_repair; results are identical up to FP32 reduction order.
 #include <mutex>
 
-#include "step_launch.hpp"
+#include "step1.hpp"
 
 namespace stk {
 
@@ -69,6 +69,67 @@ FrontArgs make_front_args(const void* q, const void* k, const void* v, int dtype
 }  // namespace stk
 
 using namespace stk;
+
+// ---- flag slots of the one-launch step
+//
+// k_step1's roles hand over through flags that must be zero before a launch
+// and that every launch leaves zero.  They live in `g_step1_ctl`, static
+// device memory (zero when the library is loaded), in kCtlSlots slots of
+// kCtlSlotWords words: each stream that runs the step takes a slot of its own
+// on first use, so launches in flight on different streams never share flags,
+// and launches on one stream are ordered.  The last word of a slot counts
+// timed-out waits.  With every slot taken (or a shape whose flags exceed a
+// slot) the step runs as two launches.  In host code `g_step1_ctl` names a
+// host-side stand-in: its device address comes from hipGetSymbolAddress.
+static constexpr int kCtlSlots = 64;
+static constexpr size_t kCtlSlotWords = 16384;
+static __device__ __align__(256) uint32_t g_step1_ctl[kCtlSlots * kCtlSlotWords];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_ctl_mu;
+static struct {
+  uint32_t* base;
+  hipStream_t streams[kCtlSlots];
+  int used;
+} g_ctl_tab[kMaxDevices];
+
+// The slot of `stream` (nullptr when none is free or `words` exceed a slot).
+static int ctl_slot(hipStream_t stream, size_t words, uint32_t** out) {
+  *out = nullptr;
+  if (words > kCtlSlotWords - 1) return STK_OK;
+  hipDevice_t dev = 0;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) {
+    stk_set_error("hipStreamGetDevice failed: %s", hipGetErrorString(e));
+    return STK_EHIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return STK_OK;
+  std::lock_guard<std::mutex> guard(g_ctl_mu);
+  auto& tab = g_ctl_tab[dev];
+  if (!tab.base) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_step1_ctl));
+    const hipError_t restore = cur != dev ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess || restore != hipSuccess || !p) {
+      stk_set_error("flag slots on device %d: %s", (int)dev,
+                    hipGetErrorString(e != hipSuccess ? e : restore));
+      return STK_EHIP;
+    }
+    tab.base = static_cast<uint32_t*>(p);
+  }
+  int slot = -1;
+  for (int i = 0; i < tab.used; ++i)
+    if (tab.streams[i] == stream) slot = i;
+  if (slot < 0 && tab.used < kCtlSlots) {
+    slot = tab.used++;
+    tab.streams[slot] = stream;
+  }
+  if (slot >= 0) *out = tab.base + (size_t)slot * kCtlSlotWords;
+  return STK_OK;
+}
 
 int stk::launch_front(int dtype, const FrontArgs& f, const StepShape& s, hipStream_t st) {
   return launch::front<false>(dtype, f, s, st);
@@ -120,6 +181,13 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
   t.p = static_cast<const int32_t*>(predicted); t.sp = sp;
   t.pm = m; t.pl = l; t.pu = u; t.uni = union_mode ? 1 : 0; t.out = out;
   hipStream_t st = (hipStream_t)stream;
+  if (front && tail && step1_covers(dtype, hq, hkv, b, d, s)) {
+    // one launch, its flags in this stream's slot (none free: two launches)
+    uint32_t* ctl = nullptr;
+    const int rc = ctl_slot(st, step1_ctl_words(hq, n, sp), &ctl);
+    if (rc) return rc;
+    if (ctl) return launch_step1(dtype, f, t, s, ctl, ctl + kCtlSlotWords - 1, st);
+  }
   if (front) {
     const int rc = launch_front(dtype, f, s, st);
     if (rc) return rc;
@@ -139,6 +207,30 @@ STK_API int stk_speculative_step(const void* q, const void* k, const void* v, in
                    workspace_bytes, stream, true, true);
 }
 
+STK_API int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk,
+                                int sp, int pred_dtype) {
+  StepShape s{};
+  if (hq <= 0 || hkv <= 0 || hq % hkv) return 0;
+  if (plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, 0, &s)) return 0;
+  return step1_covers(dtype, hq, hkv, b, d, s) &&
+         step1_ctl_words(hq, n, sp) <= kCtlSlotWords ? 1 : 0;
+}
+
+STK_API int stk_step1_timeouts(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  int count = 0;
+  for (int i = 0; i < kCtlSlots; ++i) {
+    uint32_t v = 0;
+    if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_step1_ctl), sizeof(v),
+                            ((size_t)i * kCtlSlotWords + kCtlSlotWords - 1) * sizeof(uint32_t),
+                            hipMemcpyDeviceToHost) != hipSuccess)
+      return -1;
+    count += v != 0;
+  }
+  return count;
+}
+
 // ---- the allocation-free variant of stk_speculative_step
 //
 // Its score keys live in `scratch`, one array per GPU, sized for
@@ -152,7 +244,6 @@ STK_API int stk_speculative_step(const void* q, const void* k, const void* v, in
 constexpr size_t kNoAllocMaxKeys = (size_t)1 << 19;
 static __device__ __align__(256) uint64_t scratch[kNoAllocMaxKeys];
 
-static constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_dev[kMaxDevices];
 

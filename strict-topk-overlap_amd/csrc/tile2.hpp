@@ -211,6 +211,17 @@ struct TokTile {
 #pragma unroll
     for (int e = 0; e < DPL; ++e) dst[lane_id() * DPL + e] = acc[e] * scale;
   }
+
+  // store() with agent-scope coherent stores (dst 8-byte aligned)
+  __device__ __forceinline__ void store_agent(float* dst, const float* acc) const {
+    float* p = dst + lane_id() * DPL;
+    if constexpr (DPL == 1) {
+      st_agent(p, acc[0]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < DPL; e += 2) st_agent2(p + e, acc[e], acc[e + 1]);
+    }
+  }
 };
 
 // Token passes per chunk for block size B: the largest UP in {2, 1} with

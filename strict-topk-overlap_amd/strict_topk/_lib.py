@@ -59,6 +59,8 @@ _SIGS = {
     "stk_step_supported": (I, [I, I, I, I, I, I, I, I, I]),
     "stk_speculative_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, I,
                                  P, P, P, P, P, P, Z, P]),
+    "stk_step1_supported": (I, [I, I, I, I, I, I, I, I, I]),
+    "stk_step1_timeouts": (I, []),
     "stk_step_noalloc_max_keys": (Z, []),
     "stk_speculative_step_noalloc": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, I,
                                          P, P, P, P, P, P]),

@@ -70,3 +70,36 @@ def test_noalloc_step_rejects_oversized_key_rows(lib):
     rc = L.stk_speculative_step_noalloc(fake, fake, fake, 2, 128, 8, 8192, 32, 128, fake, fake,
                                         0, 64, fake, 0, 64, 0, fake, fake, fake, fake, fake, None)
     assert rc == -1 and b"524288" in L.stk_last_error()
+
+
+def _doc_bindings():
+    """(name, kind, count) for every `<lib>.stk_*.argtypes = [...]` assignment
+    and every `<lib>.stk_*(...)` call in INTEGRATION.md's Python blocks."""
+    import ast
+    text = (ROOT / "INTEGRATION.md").read_text()
+    found = []
+    for block in re.findall(r"```python\n(.*?)```", text, flags=re.S):
+        for node in ast.walk(ast.parse(block)):
+            if isinstance(node, ast.Assign) and isinstance(node.value, ast.List):
+                for tgt in node.targets:
+                    if (isinstance(tgt, ast.Attribute) and tgt.attr == "argtypes" and
+                            isinstance(tgt.value, ast.Attribute) and
+                            tgt.value.attr.startswith("stk_")):
+                        found.append((tgt.value.attr, "argtypes", len(node.value.elts)))
+            elif (isinstance(node, ast.Call) and isinstance(node.func, ast.Attribute) and
+                  node.func.attr.startswith("stk_")):
+                found.append((node.func.attr, "call", len(node.args)))
+    return found
+
+
+def test_documented_binding_matches_header():
+    """The reference-side ctypes binding shown in INTEGRATION.md declares and
+    passes exactly the parameters the header declares."""
+    decls = _declarations()
+    found = _doc_bindings()
+    names = {name for name, _, _ in found}
+    assert {"stk_select_blocks", "stk_select_workspace_bytes"} <= names
+    assert any(kind == "argtypes" for _, kind, _ in found)
+    assert any(kind == "call" for _, kind, _ in found)
+    wrong = [(name, kind, n, decls.get(name)) for name, kind, n in found if decls.get(name) != n]
+    assert not wrong, wrong

@@ -1,0 +1,171 @@
+"""The one-launch speculative step (k_step1) against the same step as two
+launches (stk_step_front, then stk_step_tail) on identical inputs.
+
+The one launch hands keys and states between workgroups through flags in
+per-stream slots of static device memory; the two launches hand them over at
+the kernel boundary.  The arithmetic is the same, so selected IDs, prediction
+states and outputs must agree bit for bit; the oracle checks the outputs as
+well.  The cases cover every covered shape class (G = 1..4, D = 64 / 128,
+four, eight and sixteen keys per tail thread, ragged N), repeated graph
+replays with inputs changed in place, two streams at once, and shape changes
+on one stream (flags left zero by every launch); no wait may ever time out.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import stk_oracle as O
+from tests import cases as C
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from strict_topk import _lib
+    _lib.lib()
+
+
+def _inputs(hq, hkv, n, d, topk, overlap, dtype, seed):
+    from stk_harness.configs import make_qkv, perturb
+    q, k, v, lo, hi = make_qkv(hq, hkv, d, 32, n, dtype, True, seed)
+    ref_ids = O.select_blocks(C.f64(q), lo.numpy(), hi.numpy(), topk)
+    p = perturb(torch.from_numpy(ref_ids), n, topk, overlap, seed % 97)
+    host = (q, k, v, lo, hi, p)
+    lo16, hi16 = lo.to(dtype), hi.to(dtype)
+    dev = tuple(t.cuda() for t in (q, k, v, lo16, hi16, p))
+    return host, dev, ref_ids
+
+
+def _two_launches(q, k, v, lo, hi, p, topk, union):
+    """The step as its two separate launches (no flags involved)."""
+    from strict_topk import _lib
+    from strict_topk.kernels import _allocate_state, _args
+    hq, d = q.shape
+    hkv, n, b, _ = k.shape
+    sp = p.shape[1]
+    dev = q.device
+    state = _allocate_state(hq, sp, d, dev)
+    sel = torch.empty((hq, topk), dtype=torch.int32, device=dev)
+    out = torch.empty((hq, d), dtype=torch.float32, device=dev)
+    ws = _lib.workspace(_lib.size("stk_step_workspace_bytes", hq, hkv, n, d, topk), dev)
+    _lib.call("stk_step_front", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi),
+              _lib.bounds_code(lo, q), topk, _lib.ptr(p), 0, sp, _lib.ptr(state.m),
+              _lib.ptr(state.l), _lib.ptr(state.u), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
+    _lib.call("stk_step_tail", *_args(q, k, v), topk, _lib.ptr(p), 0, sp, 1 if union else 0,
+              _lib.ptr(state.m), _lib.ptr(state.l), _lib.ptr(state.u), _lib.ptr(sel),
+              _lib.ptr(out), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
+    return sel, state, out
+
+
+def _covered(q, k, topk, p):
+    from strict_topk import _lib
+    hkv, n, b, d = k.shape
+    return _lib.lib().stk_step1_supported(_lib.dtype_code(q), q.shape[0], hkv, n, b, d, topk,
+                                          p.shape[1], _lib.id_code(p)) == 1
+
+
+def _timeouts():
+    from strict_topk import _lib
+    torch.cuda.synchronize()
+    return _lib.lib().stk_step1_timeouts()
+
+
+def _same(res, ref):
+    sel, state, out = ref
+    assert torch.equal(res.selected, sel)
+    assert torch.equal(res.state.m, state.m) and torch.equal(res.state.l, state.l)
+    assert torch.equal(res.state.u, state.u)
+    assert torch.equal(res.output, out)
+
+
+@pytest.mark.parametrize("hq,hkv,n,d,topk,overlap,dtype,union", [
+    (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, False),    # c3
+    (32, 8, 2048, 128, 64, 1.0, torch.bfloat16, False),    # c3, every selected block predicted
+    (32, 8, 2048, 128, 64, 0.75, torch.bfloat16, False),   # c3, 16 misses per head
+    (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, True),     # c3, repair_union
+    (16, 8, 512, 128, 64, 0.9, torch.bfloat16, False),     # c2 (G = 2)
+    (4, 4, 64, 64, 8, 0.75, torch.float16, False),         # c1 (G = 1, D = 64)
+    (12, 3, 4000, 64, 50, 0.5, torch.float16, False),      # eight keys per tail thread
+    (8, 8, 7000, 128, 16, 0.9, torch.bfloat16, False),     # sixteen keys per tail thread
+    (6, 2, 333, 128, 40, 0.6, torch.bfloat16, False),      # G = 3, N not a chunk multiple
+])
+def test_step1_matches_two_launches(hq, hkv, n, d, topk, overlap, dtype, union):
+    from strict_topk import step
+    host, (q, k, v, lo, hi, p), ref_ids = _inputs(hq, hkv, n, d, topk, overlap, dtype,
+                                                  20261203 + n + hq)
+    assert _covered(q, k, topk, p)
+    ref = _two_launches(q, k, v, lo, hi, p, topk, union)
+    res = step.speculative_step(q, k, v, lo, hi, p, topk, union=union)
+    assert res.selected.cpu().numpy().tolist() == ref_ids.tolist()
+    _same(res, ref)
+    if not union:
+        qn, kn, vn = (C.f64(t) for t in host[:3])
+        m = C.error_metrics(C.f64(res.output), O.attention(qn, kn, vn, ref_ids))
+        assert m["passed"], m
+    assert _timeouts() == 0
+
+
+def test_step1_not_covered_runs_two_launches():
+    """Shapes outside the one launch (D = 256, B = 16, G > 4, SP * D > 8192)
+    report so and still compute the step."""
+    from strict_topk import _lib
+    L = _lib.lib()
+    assert L.stk_step1_supported(2, 32, 8, 2048, 32, 128, 64, 64, 0) == 1
+    assert L.stk_step1_supported(2, 8, 4, 300, 32, 256, 40, 40, 0) == 0    # D = 256
+    assert L.stk_step1_supported(2, 8, 4, 300, 16, 128, 40, 40, 0) == 0    # B = 16
+    assert L.stk_step1_supported(2, 40, 4, 300, 32, 128, 40, 40, 0) == 0   # G = 10
+    assert L.stk_step1_supported(2, 32, 8, 2048, 32, 128, 64, 65, 0) == 0  # SP * D > 8192
+    assert L.stk_step1_supported(0, 32, 8, 2048, 32, 128, 64, 64, 0) == 0  # fp32
+
+
+def test_step1_graph_replays_follow_inputs():
+    """A captured sequence of one-launch steps replayed after the query and
+    the predictions change in place: every replay equals the two launches on
+    that replay's inputs (the flags are zero again after every launch)."""
+    from strict_topk import step
+    from stk_harness import timing
+    _, (q, k, v, lo, hi, p), _ = _inputs(32, 8, 2048, 128, 64, 0.9, torch.bfloat16, 20261103)
+    qs = [q.clone() for _ in range(3)]
+    g, outs = timing.capture(lambda: [step.speculative_step(x, k, v, lo, hi, p, 64) for x in qs])
+    gen = torch.Generator().manual_seed(5)
+    for rep in range(4):
+        for x in qs:
+            x.copy_(torch.randn(x.shape, generator=gen).to(x.dtype))
+        if rep % 2:
+            p.copy_(torch.roll(p, 1, dims=0))
+        g.replay()
+        torch.cuda.synchronize()
+        for x, res in zip(qs, outs):
+            _same(res, _two_launches(x, k, v, lo, hi, p, 64, False))
+    assert _timeouts() == 0
+
+
+def test_step1_two_streams_and_shape_changes():
+    """Steps on two streams at once take separate flag slots; shapes change
+    from step to step on one stream."""
+    from strict_topk import step
+    a = _inputs(32, 8, 2048, 128, 64, 0.9, torch.bfloat16, 20261104)[1]
+    b = _inputs(16, 8, 512, 128, 64, 0.75, torch.bfloat16, 20261105)[1]
+    c = _inputs(4, 4, 64, 64, 8, 0.75, torch.float16, 20261106)[1]
+    refs = {name: _two_launches(*t, topk, False) for name, t, topk in
+            (("a", a, 64), ("b", b, 64), ("c", c, 8))}
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    got = {"a": [], "b": [], "c": []}
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            got["a"].append(step.speculative_step(*a, 64))
+            got["c"].append(step.speculative_step(*c, 8))
+        with torch.cuda.stream(s2):
+            got["b"].append(step.speculative_step(*b, 64))
+            got["a"].append(step.speculative_step(*a, 64))
+    torch.cuda.synchronize()
+    for name, results in got.items():
+        for res in results:
+            _same(res, refs[name])
+    assert _timeouts() == 0
