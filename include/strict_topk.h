@@ -292,11 +292,22 @@ int stk_step1_timeouts(void);
  * workspace: the score keys live in a fixed array of device memory inside the
  * library, one per GPU (4 MiB, held until the process ends), so Hq * N may
  * not exceed stk_step_noalloc_max_keys() (524288); larger shapes return
- * STK_EINVAL.  The call allocates nothing, not even on its first use on a
- * device (it then only looks up the array's address).  Calls on one GPU share
- * the array: calls that overlap in time on one GPU (on concurrent streams)
- * race and must be ordered by the caller. */
+ * STK_EINVAL.  Shapes of stk_step1_supported run as one launch, with the
+ * flags in the library's per-stream slots.  The call allocates nothing, not
+ * even on its first use on a device (it then only looks up the array's and
+ * the slots' addresses; that first use must not be under stream capture, see
+ * stk_step_prepare).  Calls on one GPU share the array: calls that overlap in
+ * time on one GPU (on concurrent streams) race and must be ordered by the
+ * caller. */
 size_t stk_step_noalloc_max_keys(void);
+
+/* Looks up, on the current device, the device memory the fused step keeps in
+ * the library (the allocation-free step's array and the one-launch step's
+ * flag slots).  The step entry points do this on a device's first call, and
+ * refuse to (STK_EINVAL) when that first call is made under stream capture:
+ * a caller that captures before any eager call makes this call first,
+ * outside the capture.  It has no reference counterpart. */
+int stk_step_prepare(void);
 
 int stk_speculative_step_noalloc(const void* q, const void* k, const void* v, int dtype, int hq,
                                  int hkv, int n, int b, int d, const void* lo, const void* hi,

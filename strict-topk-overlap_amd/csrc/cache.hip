@@ -127,8 +127,11 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
   __syncthreads();
   const int now = *a.clock;
   int32_t* trow = a.table + (size_t)grp * a.nb;
+  const int32_t* hrow = a.host_table + (size_t)grp * a.nb;
   const size_t s0 = (size_t)grp * a.c;
-  // resident ones are stamped, missing ones listed
+  // resident ones are stamped, missing ones listed; a block with no valid
+  // host page is neither (it stays non-resident: the tail gives it the
+  // empty state, as the paged steps do for an invalid page)
   for (int w = tid; w < words; w += kSwapThreads) {
     uint32_t bits = need[w];
     while (bits) {
@@ -138,8 +141,11 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
       if (s >= 0) {
         a.slot_stamp[s] = now;
       } else {
-        const int x = atomicAdd(&nload, 1);
-        if (x < kMaxNeed) loads[x] = j;
+        const int hp = hrow[j];
+        if (hp >= 0 && hp < a.host_pages) {
+          const int x = atomicAdd(&nload, 1);
+          if (x < kMaxNeed) loads[x] = j;
+        }
       }
     }
   }
@@ -170,17 +176,23 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
     vict[pos] = (int)(s0 + s);
   });
   __syncthreads();
-  // the copy list: host page and device slot of each missing block (a block
-  // left without a slot, which C >= G * K rules out, is copied nowhere)
-  const int32_t* hrow = a.host_table + (size_t)grp * a.nb;
+  // the copy list: host page and device slot of each listed block (a block
+  // left without a slot, which C >= G * K rules out, is copied nowhere and
+  // not counted)
+  __shared__ int ncopy;
+  if (tid == 0) ncopy = 0;
+  __syncthreads();
   for (int x = tid; x < nl; x += kSwapThreads) {
     const int hp = hrow[loads[x]];
     const bool ok = hp >= 0 && hp < a.host_pages && vict[x] >= 0;
     a.src[(size_t)grp * kMaxNeed + x] = ok ? hp : -1;
     a.dst[(size_t)grp * kMaxNeed + x] = ok ? vict[x] : -1;
+    const int c = __popcll(__ballot(ok));
+    if (lane_id() == __ffsll((long long)__ballot(1)) - 1) atomicAdd(&ncopy, c);
   }
+  __syncthreads();
   const int chunks = a.b * a.d * a.esize / 16;   // 16-byte chunks per page
-  if (tid == 0) atomicAdd(a.h2d, (unsigned long long)nl * 2ull * chunks * 16ull);
+  if (tid == 0) atomicAdd(a.h2d, (unsigned long long)ncopy * 2ull * chunks * 16ull);
 }
 
 // The listed pages: workgroup (group, part) copies pages part, part + 16,

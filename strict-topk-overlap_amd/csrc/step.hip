@@ -93,6 +93,12 @@ static struct {
   int used;
 } g_ctl_tab[kMaxDevices];
 
+// True when `stream` is being captured into a graph.
+static bool capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 // The slot of `stream` (nullptr when none is free or `words` exceed a slot).
 static int ctl_slot(hipStream_t stream, size_t words, uint32_t** out) {
   *out = nullptr;
@@ -107,6 +113,11 @@ static int ctl_slot(hipStream_t stream, size_t words, uint32_t** out) {
   std::lock_guard<std::mutex> guard(g_ctl_mu);
   auto& tab = g_ctl_tab[dev];
   if (!tab.base) {
+    if (capturing(stream)) {
+      stk_set_error("the step's device memory is looked up on a device's first call, which "
+                    "must not be under stream capture: call stk_step_prepare() first");
+      return STK_EINVAL;
+    }
     int cur = 0;
     e = hipGetDevice(&cur);
     if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
@@ -261,6 +272,11 @@ static int scratch_address(hipStream_t stream, void** out) {
   }
   std::lock_guard<std::mutex> guard(g_scratch_mu);
   if (!g_scratch_dev[dev]) {
+    if (capturing(stream)) {
+      stk_set_error("the allocation-free step's scratch is looked up on a device's first call, "
+                    "which must not be under stream capture: call stk_step_prepare() first");
+      return STK_EINVAL;
+    }
     int cur = 0;
     e = hipGetDevice(&cur);
     if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
@@ -279,6 +295,15 @@ static int scratch_address(hipStream_t stream, void** out) {
 }
 
 STK_API size_t stk_step_noalloc_max_keys(void) { return kNoAllocMaxKeys; }
+
+STK_API int stk_step_prepare(void) {
+  hipStream_t st = nullptr;   // the null stream of the current device: never capturing
+  void* ws = nullptr;
+  int rc = scratch_address(st, &ws);
+  if (rc) return rc;
+  uint32_t* ctl = nullptr;
+  return ctl_slot(st, 0, &ctl);
+}
 
 STK_API int stk_speculative_step_noalloc(const void* q, const void* k, const void* v, int dtype,
                                          int hq, int hkv, int n, int b, int d, const void* lo,

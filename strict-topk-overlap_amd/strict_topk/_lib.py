@@ -62,6 +62,7 @@ _SIGS = {
     "stk_step1_supported": (I, [I, I, I, I, I, I, I, I, I]),
     "stk_step1_timeouts": (I, []),
     "stk_step_noalloc_max_keys": (Z, []),
+    "stk_step_prepare": (I, []),
     "stk_speculative_step_noalloc": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, I,
                                          P, P, P, P, P, P]),
     "stk_step_front": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, P, P, P, P, Z, P]),
@@ -156,3 +157,19 @@ def call(name, *args):
 
 def size(name, *args):
     return int(getattr(lib(), name)(*args))
+
+
+_prepared = set()
+
+
+def prepare(device):
+    """Look up the fused step's device memory (the allocation-free step's
+    scratch, the one-launch step's flag slots) on ``device`` once, outside
+    any stream capture: the C entry points refuse a device's first lookup
+    under capture."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx in _prepared or torch.cuda.is_current_stream_capturing():
+        return
+    with torch.cuda.device(idx):
+        call("stk_step_prepare")
+    _prepared.add(idx)

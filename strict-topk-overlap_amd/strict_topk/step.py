@@ -70,12 +70,13 @@ def serial_step(q, k, v, lo, hi, topk):
     return sel, gqa.exact(q, k, v, sel)
 
 
-def supported(q, k, lo, topk, predicted):
+def supported(q, k, lo, topk, predicted, v=None, hi=None):
     """True when the fused kernels serve this shape: bf16/fp16, int32
     predictions, D in {64, 128, 256}, B a multiple of 16, N <= 8192, K and SP
-    <= 256, SP * D <= 32768, and 16-byte aligned Q/K/V/LO."""
+    <= 256, SP * D <= 32768, and 16-byte aligned Q/K/V/LO/HI (V and HI are
+    checked when given)."""
     hkv, n, b, d = k.shape
-    if any(t.data_ptr() % 16 for t in (q, k, lo)):
+    if any(t.data_ptr() % 16 for t in (q, k, lo, v, hi) if t is not None):
         return False
     return bool(_lib.lib().stk_step_supported(_lib.dtype_code(q), q.shape[0], hkv, n, b, d,
                                               int(topk), predicted.shape[1],
@@ -96,8 +97,9 @@ def speculative_step(q, k, v, lo, hi, predicted, topk, union=False):
     if topk < 1 or topk > n:
         raise RuntimeError("selected index k out of range")
     sp = predicted.shape[1]
-    if supported(q, k, lo, topk, predicted):
+    if supported(q, k, lo, topk, predicted, v, hi):
         dev = q.device
+        _lib.prepare(dev)
         selected = torch.empty((hq, topk), device=dev, dtype=torch.int32)
         state = _allocate_state(hq, sp, d, dev)
         out = torch.empty((hq, d), device=dev, dtype=torch.float32)
@@ -117,6 +119,27 @@ def speculative_step(q, k, v, lo, hi, predicted, topk, union=False):
     return StepResult(selected, state, out)
 
 
+def check_into(into, hq, sp, topk, d, device):
+    """ValueError unless ``into`` (a StepResult) holds this step's outputs:
+    contiguous int32 selected [Hq, topk], float32 state m, l [Hq, SP] and
+    u [Hq, SP, D] and float32 output [Hq, D], all on ``device``, u 16-byte
+    aligned.  The kernels write every element of these shapes, so a
+    mismatched ``into`` would be written past its ends."""
+    def ok(t, shape, dtype):
+        return (isinstance(t, torch.Tensor) and tuple(t.shape) == shape and t.dtype == dtype
+                and t.device == device and t.is_contiguous())
+    st = getattr(into, "state", None)
+    if not (ok(getattr(into, "selected", None), (hq, topk), torch.int32) and st is not None
+            and ok(getattr(st, "m", None), (hq, sp), torch.float32)
+            and ok(getattr(st, "l", None), (hq, sp), torch.float32)
+            and ok(getattr(st, "u", None), (hq, sp, d), torch.float32)
+            and ok(getattr(into, "output", None), (hq, d), torch.float32)):
+        raise ValueError("into must hold contiguous int32 selected[Hq,topk], float32 "
+                         "state m,l[Hq,SP], u[Hq,SP,D] and output[Hq,D] on Q's device")
+    if st.u.data_ptr() % 16:
+        raise ValueError("into.state.u must be 16-byte aligned")
+
+
 def speculative_step_noalloc(q, k, v, lo, hi, predicted, topk, union=False, into=None):
     """``speculative_step`` for callers that cannot allocate device memory
     (graph capture, serving loops): the library keeps the step's scratch in a
@@ -132,13 +155,16 @@ def speculative_step_noalloc(q, k, v, lo, hi, predicted, topk, union=False, into
     hq, d = q.shape
     hkv, n, b, _ = k.shape
     sp = predicted.shape[1]
-    if not supported(q, k, lo, topk, predicted):
+    if not supported(q, k, lo, topk, predicted, v, hi):
         raise ValueError("shape not supported by the fused step")
     dev = q.device
     if into is None:
         into = StepResult(torch.empty((hq, topk), device=dev, dtype=torch.int32),
                           _allocate_state(hq, sp, d, dev),
                           torch.empty((hq, d), device=dev, dtype=torch.float32))
+    else:
+        check_into(into, hq, sp, topk, d, dev)
+    _lib.prepare(dev)
     _lib.call("stk_speculative_step_noalloc", *_args(q, k, v), _lib.ptr(lo), _lib.ptr(hi),
               _lib.bounds_code(lo, q), topk,
               _lib.ptr(predicted), _lib.id_code(predicted), sp, 1 if union else 0,
@@ -180,7 +206,7 @@ def speculative_signed_step(q, k, v, lo, hi, predicted, topk, mode="hybrid", mas
     if topk < 1 or topk > n:
         raise RuntimeError("selected index k out of range")
     sp = predicted.shape[1]
-    if mode != "compact" and supported(q, k, lo, topk, predicted):
+    if mode != "compact" and supported(q, k, lo, topk, predicted, v, hi):
         dev = q.device
         selected = torch.empty((hq, topk), device=dev, dtype=torch.int32)
         state = _allocate_state(hq, sp, d, dev)

@@ -141,3 +141,38 @@ def test_host_cache_serial_path():
     m = C.error_metrics(C.f64(out[0]), O.attention(qn, kn, vn, ids, tokens=tokens))
     assert m["passed"], m
     assert int(cache.h2d_bytes.item()) > 0
+
+
+@pytest.mark.parametrize("n", [200, 16])
+def test_host_cache_invalid_host_page(n):
+    """A block whose host-table entry is -1 has no data: it scores lowest (its
+    bounds are indexed by host page), and when it is selected all the same
+    (n = topk: every block is) it gets no slot, stays non-resident, adds no
+    H2D bytes and has the empty state, as an invalid page has in the paged
+    steps."""
+    from stk_harness.configs import make_qkv, perturb
+    from strict_topk import hostcache
+    hq, hkv, b, d, topk, sp = 8, 2, 32, 128, 16, 16
+    g = hq // hkv
+    q, k, v, lo, hi = make_qkv(hq, hkv, d, b, n, torch.bfloat16, True, 4242)
+    cache = hostcache.build([(k, v)], g * topk, device=DEV, bounds_dtype=torch.bfloat16)
+    qn, kn, vn = C.f64(q), C.f64(k), C.f64(v)
+    dead = int(O.select_blocks(qn, lo.numpy(), hi.numpy(), topk)[0][3])
+    cache.host_table[0, 0, dead] = -1
+    scores = O.bound_scores(qn, lo.numpy(), hi.numpy())
+    scores[:g, dead] = -np.inf        # below every finite score
+    ids = O.topk_ids(scores, topk)
+    # (with every block selected there is none left to mispredict)
+    pred = perturb(torch.from_numpy(ids), n, sp, 0.75 if n > topk else 1.0, 9)
+    res = hostcache.speculative_step(q[None].to(DEV), cache, pred[None].to(DEV), topk)
+    torch.cuda.synchronize()
+    assert res.selected[0].cpu().numpy().tolist() == ids.tolist()
+    assert (dead in ids[0]) == (n == topk)
+    table = cache.table.cpu().numpy()
+    assert table[0, 0, dead] == -1
+    rows = [[j for j in ids[h] if not (h // g == 0 and j == dead)] for h in range(hq)]
+    m = C.error_metrics(C.f64(res.output[0]), O.attention(qn, kn, vn, rows))
+    assert m["passed"], m
+    copied = sum(len(set(np.unique(ids[kh * g:(kh + 1) * g])) - ({dead} if kh == 0 else set()))
+                 for kh in range(hkv))
+    assert int(cache.h2d_bytes.item()) == copied * 2 * b * d * 2

@@ -21,6 +21,8 @@ job counts exact.
       speculate('hybrid', 0.2, keep_mass) -> repair_signed_fused
       (strict_topk/signed_fused.py:148-193) per request.
 """
+import functools
+
 import numpy as np
 import pytest
 import torch
@@ -114,6 +116,68 @@ def test_c3_overlap_run_composition(overlap):
         assert torch.equal(eager_sel, gsel)
 
 
+@pytest.mark.parametrize("overlap,seed", [
+    (1.0, 20261103), (1.0, 20261104), (1.0, 20261105),
+    (0.9, 20261104), (0.9, 20261105), (0.75, 20261104), (0.75, 20261105),
+])
+def test_c3_step_and_composition(overlap, seed):
+    """c3 at every hit rate and seed of the sweep: the fused step (one launch)
+    and the drop-in composition (gqa_light.repair_saved_auto behind
+    overlap_run, with the bench's expected-miss fraction 1 - overlap) against
+    the oracle."""
+    from stk_harness.configs import CONFIGS, make_qkv, perturb
+    from stk_harness.timing import overlap_run
+    from strict_topk import gqa, gqa_light, step
+    c = CONFIGS["c3"]
+    q, k, v, lo, hi = make_qkv(c.hq, c.hkv, c.dim, c.block, c.blocks, c.dtype, c.hot, seed)
+    qn = C.f64(q)
+    ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), c.topk)
+    p = perturb(torch.from_numpy(ref_ids), c.blocks, c.sp, overlap, seed)
+    kn, vn, a_r = restrict(k, v, ref_ids)
+    expected = O.attention(qn, kn, vn, a_r)
+    qd, kd, vd, lod, hid, pd = (t.to(DEV) for t in (q, k, v, lo, hi, p))
+    res = step.speculative_step(qd, kd, vd, lod.to(c.dtype), hid.to(c.dtype), pd, c.topk)
+    ss, ps = torch.cuda.Stream(), torch.cuda.Stream()
+    sel, out = overlap_run(lambda: gqa.select_blocks(qd, lod, hid, c.topk),
+                           lambda: gqa.partials(qd, kd, vd, pd),
+                           lambda a, st: (a, gqa_light.repair_saved_auto(
+                               qd, kd, vd, a, pd, st, 1.0 - overlap)), ss, ps)
+    torch.cuda.synchronize()
+    assert res.selected.cpu().numpy().tolist() == ref_ids.tolist()
+    assert sel.cpu().numpy().tolist() == ref_ids.tolist()
+    check(res.output, expected, ("c3 step", overlap, seed))
+    check(out, expected, ("c3 composition", overlap, seed))
+
+
+# ------------------------------------------------------------------ c2
+def test_c2_repair_saved():
+    """c2's own strategy at its shape: gqa.select_blocks || gqa.partials, then
+    gqa.repair_saved (strict_topk/gqa.py:164-188), eagerly and through
+    overlap_run."""
+    from stk_harness.configs import CONFIGS, make_qkv, perturb
+    from stk_harness.timing import overlap_run
+    from strict_topk import gqa
+    c = CONFIGS["c2"]
+    q, k, v, lo, hi = make_qkv(c.hq, c.hkv, c.dim, c.block, c.blocks, c.dtype, c.hot, 20261103)
+    qn = C.f64(q)
+    ref_ids = O.select_blocks(qn, lo.numpy(), hi.numpy(), c.topk)
+    p = perturb(torch.from_numpy(ref_ids), c.blocks, c.sp, 0.9, 20261103)
+    kn, vn, a_r = restrict(k, v, ref_ids)
+    expected = O.attention(qn, kn, vn, a_r)
+    qd, kd, vd, lod, hid, pd = (t.to(DEV) for t in (q, k, v, lo, hi, p))
+    sel = gqa.select_blocks(qd, lod, hid, c.topk)
+    st = gqa.partials(qd, kd, vd, pd)
+    out = gqa.repair_saved(qd, kd, vd, sel, pd, st)
+    ss, ps = torch.cuda.Stream(), torch.cuda.Stream()
+    out2 = overlap_run(lambda: gqa.select_blocks(qd, lod, hid, c.topk),
+                       lambda: gqa.partials(qd, kd, vd, pd),
+                       lambda a, s: gqa.repair_saved(qd, kd, vd, a, pd, s), ss, ps)
+    torch.cuda.synchronize()
+    assert sel.cpu().numpy().tolist() == ref_ids.tolist()
+    check(out, expected, "c2 repair_saved")
+    check(out2, expected, "c2 repair_saved (overlap_run)")
+
+
 # ------------------------------------------------------------------ c4
 def test_c4_real_shape():
     from stk_harness.configs import CONFIGS, make_qkv, perturb
@@ -148,6 +212,7 @@ def test_c4_real_shape():
 
 
 # ------------------------------------------------------------------ c5
+@functools.lru_cache(maxsize=1)
 def _c5_requests(seed):
     from stk_harness.configs import C5, make_qkv, perturb
     rng = np.random.default_rng(seed)
@@ -160,7 +225,7 @@ def _c5_requests(seed):
                                    True, seed + 101 * r)
         ids = O.select_blocks(C.f64(q), lo.numpy(), hi.numpy(), C5["topk"])
         p = perturb(torch.from_numpy(ids), n, C5["topk"], float(overlaps[r]), seed + r)
-        reqs.append(dict(q=q, k=k, v=v, ids=ids, p=p, n=n))
+        reqs.append(dict(q=q, k=k, v=v, lo=lo, hi=hi, ids=ids, p=p, n=n))
         print(f"c5 request {r}: {n} blocks, overlap {overlaps[r]:.3f}", flush=True)
     return reqs
 
@@ -196,3 +261,42 @@ def test_c5_real_batch():
             check(out.output[i], ref.output, ("c5 paged signed", eps, i, r["n"]))
             if eps == 0:
                 check(out.output[i], O.attention(qn, kn, vn, a_r), ("c5 strict", i))
+
+
+def test_c5_dropin_signed_composition():
+    """The reference API's own c5 composition on three of the requests
+    (smallest, median and largest context): overlap_run(gqa.select_blocks ||
+    kernels.speculate('hybrid', 0.2, keep_mass=True)), then
+    signed_fused.repair_signed_fused (strict_topk/signed_fused.py:148-193)
+    with max_extra_mass 0.01 and 0, against the oracle."""
+    from stk_harness.configs import C5
+    from stk_harness.timing import overlap_run
+    from strict_topk import gqa, kernels, signed_fused
+    reqs = _c5_requests(20261103)
+    order = sorted(range(len(reqs)), key=lambda i: reqs[i]["n"])
+    ss, ps = torch.cuda.Stream(), torch.cuda.Stream()
+    for i in (order[0], order[len(order) // 2], order[-1]):
+        r = reqs[i]
+        qd, kd, vd, lod, hid, pd = (t.to(DEV) for t in (r["q"], r["k"], r["v"], r["lo"],
+                                                        r["hi"], r["p"]))
+        kn, vn, a_r, p_r = restrict(r["k"], r["v"], r["ids"], r["p"].numpy())
+        qn = C.f64(r["q"])
+        pred_ref = O.speculate(qn, kn, vn, p_r, "hybrid", 0.2, keep_mass=True)
+        sel, pred = overlap_run(lambda: gqa.select_blocks(qd, lod, hid, C5["topk"]),
+                                lambda: kernels.speculate(qd, kd, vd, pd, "hybrid", 0.2,
+                                                          keep_mass=True),
+                                lambda a, st: (a, st), ss, ps)
+        assert sel.cpu().numpy().tolist() == r["ids"].tolist(), i
+        for eps in (0.01, 0.0):
+            out = signed_fused.repair_signed_fused(qd, kd, vd, sel, pd, pred, max_extra_mass=eps)
+            torch.cuda.synchronize()
+            ref = O.repair_signed_fused(qn, kn, vn, a_r, p_r, pred_ref, max_extra_mass=eps)
+            assert out.fallback.cpu().numpy().tolist() == ref.fallback.tolist(), (eps, i)
+            assert out.positive_jobs.cpu().numpy().tolist() == ref.positive_jobs.tolist()
+            assert out.total_jobs.cpu().numpy().tolist() == ref.total_jobs.tolist()
+            if eps > 0:
+                assert out.approximate_heads.cpu().numpy().tolist() == \
+                    ref.approximate_heads.tolist(), i
+            check(out.output, ref.output, ("c5 drop-in signed", eps, i, r["n"]))
+            if eps == 0:
+                check(out.output, O.attention(qn, kn, vn, a_r), ("c5 drop-in strict", i))

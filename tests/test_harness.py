@@ -118,3 +118,4 @@ def test_masks_and_token_counts_validate_on_the_host():
     q = torch.zeros((r, 4, d), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="ntokens"):
         paged.exact(q, kv, 2)
+

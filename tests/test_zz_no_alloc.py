@@ -100,3 +100,47 @@ def test_noalloc_rejects_too_many_keys():
     assert step.supported(q, k, lo, 8, p)
     with pytest.raises(ValueError, match="524288"):
         step.speculative_step_noalloc(q, k, k, lo, lo, p, 8)
+
+
+_FIRST_UNDER_CAPTURE = r"""
+import sys
+sys.path[:0] = [{pkg!r}, {root!r}]
+import torch
+from strict_topk import _lib, step
+from stk_harness.configs import make_qkv
+q, k, v, lo, hi = (t.cuda() for t in make_qkv(8, 2, 128, 32, 256, torch.bfloat16, True, 11))
+lo, hi = lo.to(torch.bfloat16), hi.to(torch.bfloat16)
+gen = torch.Generator().manual_seed(3)
+p = torch.stack([torch.randperm(256, generator=gen)[:32] for _ in range(8)]).int().cuda()
+if {prepare}:
+    _lib.prepare(q.device)
+g = torch.cuda.CUDAGraph()
+try:
+    with torch.cuda.graph(g):
+        res = step.speculative_step_noalloc(q, k, v, lo, hi, p, 16)
+except Exception as e:
+    print("REFUSED", "stk_step_prepare" in str(e), flush=True)
+    sys.exit(0)
+g.replay()
+torch.cuda.synchronize()
+ref = step.speculative_step(q, k, v, lo, hi, p, 16)
+same = torch.equal(ref.selected, res.selected) and torch.equal(ref.output, res.output)
+print("CAPTURED", same, flush=True)
+"""
+
+
+@pytest.mark.parametrize("prepare,expected", [(False, "REFUSED True"), (True, "CAPTURED True")])
+def test_noalloc_first_call_under_capture(prepare, expected):
+    """In a fresh process whose first step call is under graph capture: the
+    library refuses to look up its device memory there (a clear error naming
+    stk_step_prepare), and after stk_step_prepare the captured call works and
+    matches the eager step."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    code = _FIRST_UNDER_CAPTURE.format(pkg=str(root / "strict-topk-overlap_amd"), root=str(root),
+                                       prepare=prepare)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert expected in r.stdout, (r.stdout, r.stderr[-2000:])
