@@ -11,6 +11,7 @@
 // are read through the wave Tile routine; per-block states through weighted
 // LDS reductions.  Query head h reads KV head h / (Hq / Hkv).
 #include "gqa_repair.hpp"
+#include "repair_fast.hpp"
 #include "api.hpp"
 
 namespace stk {
@@ -545,6 +546,9 @@ STK_API size_t stk_gqa_repair_workspace_bytes(int hq, int sa, int d) {
 }
 
 static int launch_gqa_repair(const GqaRepairArgs& g, int dtype, hipStream_t st) {
+  // the one-workgroup repair (repair_fast.hpp) where it covers the shape
+  const int rc = launch_repair_fast(g, dtype, st);
+  if (rc <= 0) return rc;
   const int d = g.kv.d;
   size_t lds = gqa_repair_lds(g.kv.n, g.sa, g.sp, d);
   if (lds > 160 * 1024) {
