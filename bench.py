@@ -5,11 +5,12 @@ A step is select (fused bound scorer + exact top-K) concurrently with
 speculative GQA attention over the already-known predicted blocks, then the
 strict repair -- the full path of the reference's ``overlap_run``
 (``benchmarks/run_benchmark.py:99-118``).  It runs as ``strict_topk.step``:
-one launch whose workgroups either score blocks or compute the predicted
-blocks' states, then one launch doing the top-K and the repair per query
-head.  The headline workload is config c3 (Qwen3-4B-like shape, 64K context,
-K=64, 90 % prediction overlap, bf16), the configuration the north-star
-target is stated on.
+one launch (k_step1) whose workgroups score blocks, compute the predicted
+blocks' states, or -- one per query head -- run the top-K and the repair as
+soon as their head's scores are published, while the states still stream.
+The headline workload is config c3 (Qwen3-4B-like shape, 64K context, K=64,
+90 % prediction overlap, bf16), the configuration the north-star target is
+stated on.
 
 Timing.  M consecutive decode steps are captured into one HIP graph, step i
 reading the i % M-th of M device copies of the inputs (identical values,
@@ -31,10 +32,13 @@ bit-exact, outputs within |err| <= 3e-4 + 3e-4 |ref|).
 Printed JSON line (one GPU):
   value / ms_per_step   microseconds per full c3 decode step (lower is better);
   serial_us             the serial path, paired ABBA replay timing;
-  roofline              dominant kernel (k_front: select || speculate),
-                        algorithmic bytes / average launch time measured here
-                        with HIP events on its stream; traffic from the
-                        committed rocprof counter runs;
+  roofline              the dominant kernel, k_step1 (the whole step):
+                        the step's algorithmic bytes / average launch time
+                        measured here with HIP events on its stream; traffic
+                        from the committed rocprof counter runs of the c3
+                        path; beside it, the same figures for k_front, the
+                        first of the two launches that shapes outside the
+                        one-launch step run;
   path_roofline         the whole step's algorithmic bytes against 8 TB/s;
   configs               c1, c2, c4, c5: speculative path vs serial;
   parity                oracle check of every measured output (CPU leg);
@@ -249,14 +253,43 @@ def main():
     med, _ = timing.paired(graphs, replays=max(1, 120 // M), rounds=5, seed=args.seed)
     per_step = {key: round(us / M, 3) for key, us in med.items()}
 
-    # ---- dominant-kernel roofline: k_front (select || speculate), one launch
-    # per call of stk_step_front, HIP events on its stream, input copies rotated
+    # ---- dominant-kernel roofline: the step is one kernel (k_step1: select ||
+    # speculate, top-K and repair) where stk_step1_supported says so; one
+    # launch per stk_speculative_step call, HIP events on its stream, input
+    # copies rotated, the launches captured so the host's call rate does not
+    # bound the measurement
     from strict_topk import step as step_mod  # noqa: F401  (loads the symbols)
     c = cfg
     st = step.speculate(0)
     ws = _lib.workspace(_lib.size("stk_step_workspace_bytes", c.hq, c.hkv, c.blocks, c.dim,
                                   c.topk), dev)
     L = _lib.lib()
+    one_launch = bool(L.stk_step1_supported(_lib.dtype_code(step.q), c.hq, c.hkv, c.blocks,
+                                            c.block, c.dim, c.topk, c.sp, 0))
+    sel1 = torch.empty((c.hq, c.topk), dtype=torch.int32, device=dev)
+    out1 = torch.empty((c.hq, c.dim), dtype=torch.float32, device=dev)
+    sstate = [0]
+
+    def whole_step():
+        i = sstate[0] % M
+        sstate[0] += 1
+        sq, sk, sv, slo, shi = step.sets[i]
+        rc = L.stk_speculative_step(sq.data_ptr(), sk.data_ptr(), sv.data_ptr(),
+                                    _lib.dtype_code(sq), c.hq, c.hkv, c.blocks, c.block, c.dim,
+                                    slo.data_ptr(), shi.data_ptr(), _lib.bounds_code(slo, sq),
+                                    c.topk, step.predicted.data_ptr(), 0, c.sp, 0,
+                                    sel1.data_ptr(), st.m.data_ptr(), st.l.data_ptr(),
+                                    st.u.data_ptr(), out1.data_ptr(), ws.data_ptr(), ws.numel(),
+                                    _lib.stream(dev))
+        assert rc == 0, L.stk_last_error()
+
+    nstep = 4 * M
+    g_step, _ = timing.capture(lambda: [whole_step() for _ in range(nstep)])
+    timing.warm([g_step], ms=50.0)
+    step_us = min(timing.interval_us(g_step, 20) for _ in range(5)) / nstep
+    del g_step
+    by0 = step.bytes()
+    tr_c3 = path_traffic("c3")
     state = [0]
 
     def front():
@@ -281,12 +314,27 @@ def main():
     achieved = fb / (front_us * 1e-6) / 1e9
     workload = f"{cfg.name}@{args.overlap}"
     tr = traffic_record(workload)
-    roofline = {"kernel": "k_front (select || speculate)", "bound": "hbm",
-                "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(achieved / 8000.0, 4),
-                "traffic": tr["traffic"] if tr else None,
-                "traffic_over_algorithmic": tr["traffic_over_algorithmic"] if tr else None,
-                "bytes_per_launch": fb, "us_per_launch": round(front_us, 3)}
+    front = {"kernel": "k_front (select || speculate; the first of the two launches "
+                       "that shapes outside the one-launch step run)", "bound": "hbm",
+             "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+             "frac": round(achieved / 8000.0, 4),
+             "traffic": tr["traffic"] if tr else None,
+             "traffic_over_algorithmic": tr["traffic_over_algorithmic"] if tr else None,
+             "bytes_per_launch": fb, "us_per_launch": round(front_us, 3)}
+    if one_launch and args.overlap == 0.9 and args.config == "c3" and args.bounds == "keys":
+        trs = tr_c3["fused"] if tr_c3 and "fused" in tr_c3 else None
+    else:
+        trs = None
+    s_ach = by0.full / (step_us * 1e-6) / 1e9
+    roofline = {"kernel": "k_step1 (the whole step in one launch: select || speculate, "
+                          "top-K, repair, merge)" if one_launch else
+                          "k_front + k_tail (two launches)",
+                "bound": "hbm", "achieved": round(s_ach, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(s_ach / 8000.0, 4),
+                "traffic": trs["traffic"] if trs else None,
+                "traffic_over_algorithmic": trs["traffic_over_algorithmic"] if trs else None,
+                "bytes_per_launch": by0.full, "us_per_launch": round(step_us, 3),
+                "k_front": front}
 
     # ---- block metadata (lo/hi from K at prefill, and one decode append) on
     # c3's K, rotating over the input copies; checked against torch.amin /
