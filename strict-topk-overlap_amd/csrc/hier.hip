@@ -23,26 +23,38 @@ struct MatchArgs {
   int32_t* slot;
 };
 
-// slot[row, j] = max{p : P[row, p] == A[row, j]} or -1.
-__global__ __launch_bounds__(256) void k_match_ids(MatchArgs a) {
+constexpr int kMatchThreads = 1024;
+constexpr int kMatchPerThread = 4;   // predicted IDs requested up front per thread
+
+// slot[row, j] = max{p : P[row, p] == A[row, j]} or -1.  One round trip: a
+// thread's selected ID and its first predicted IDs are requested before the
+// map is cleared, so their loads overlap the clear.
+__global__ __launch_bounds__(kMatchThreads) void k_match_ids(MatchArgs a) {
   __shared__ int32_t map[kMapN];
-  int row = blockIdx.x;
-  int j0 = blockIdx.y * 256;
+  const int row = blockIdx.x;
+  const int j = blockIdx.y * kMatchThreads + threadIdx.x;
   if (a.n <= kMapN) {
+    const int64_t aid = load_id(a.a, a.atype, (int64_t)row * a.sa + (j < a.sa ? j : 0));
+    int64_t pid[kMatchPerThread];
+#pragma unroll
+    for (int r = 0; r < kMatchPerThread; ++r) {
+      const int p = threadIdx.x + r * kMatchThreads;
+      pid[r] = load_id(a.p, a.ptype, (int64_t)row * a.sp + (p < a.sp ? p : 0));
+    }
     for (int i = threadIdx.x; i < a.n; i += blockDim.x) map[i] = -1;
     __syncthreads();
-    for (int p = threadIdx.x; p < a.sp; p += blockDim.x) {
-      int64_t id = load_id(a.p, a.ptype, (int64_t)row * a.sp + p);
+#pragma unroll
+    for (int r = 0; r < kMatchPerThread; ++r) {
+      const int p = threadIdx.x + r * kMatchThreads;
+      if (p < a.sp && pid[r] >= 0 && pid[r] < a.n) atomicMax(&map[pid[r]], p);
+    }
+    for (int p = threadIdx.x + kMatchPerThread * kMatchThreads; p < a.sp; p += blockDim.x) {
+      const int64_t id = load_id(a.p, a.ptype, (int64_t)row * a.sp + p);
       if (id >= 0 && id < a.n) atomicMax(&map[id], p);
     }
     __syncthreads();
-    int j = j0 + threadIdx.x;
-    if (j < a.sa) {
-      int64_t id = load_id(a.a, a.atype, (int64_t)row * a.sa + j);
-      a.slot[(size_t)row * a.sa + j] = (id >= 0 && id < a.n) ? map[id] : -1;
-    }
+    if (j < a.sa) a.slot[(size_t)row * a.sa + j] = (aid >= 0 && aid < a.n) ? map[aid] : -1;
   } else {
-    int j = j0 + threadIdx.x;
     if (j < a.sa) {
       int64_t id = load_id(a.a, a.atype, (int64_t)row * a.sa + j);
       int best = -1;
@@ -294,7 +306,8 @@ STK_API int stk_hier_repair(const void* q, const void* k, const void* v, int dty
   float* l = w.take<float>((size_t)hq * sa);
   float* u = w.take<float>((size_t)hq * sa * d);
   MatchArgs ma{selected, sel_dtype, sa, predicted, pred_dtype, sp, n, slot};
-  hipLaunchKernelGGL(k_match_ids, dim3(rows, (sa + 255) / 256), dim3(256), 0, st, ma);
+  hipLaunchKernelGGL(k_match_ids, dim3(rows, (sa + kMatchThreads - 1) / kMatchThreads),
+                     dim3(kMatchThreads), 0, st, ma);
   int rc = stk_check_launch("k_match_ids");
   if (rc) return rc;
   const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
