@@ -44,7 +44,7 @@ from strict_topk import step as step_mod
 
 from . import timing
 from .configs import C5, CONFIGS, make_qkv, perturb
-from .decode import HBM_PEAK, GqaStep, unique_pairs
+from .decode import HBM_PEAK, GqaStep, byte_model, unique_pairs
 
 
 @dataclass
@@ -460,6 +460,17 @@ def case_cache(dev, seed=20261103):
     sa = torch.stack(sels).cpu().numpy()
     u_a = sum(unique_pairs(x, g) for x in sa) / m
     meta = 2 * c.hkv * c.blocks * c.dim * 2
+    # The speculative path's device-side bytes: the prediction is the
+    # previous step's selection, which that step swapped in (C >= G * K
+    # slots), so every predicted block is resident (P n R = P): the front
+    # reads P's tiles and writes their states, the repair reads the hits'
+    # states and the tiles of A \ P (swapped in where not resident).  The
+    # bounds of every block are read once, as in the serial path.  H2D
+    # copies are counted apart, on both paths.
+    spec_models = [byte_model(c, sels[i].cpu().numpy(), preds[i][0].cpu().numpy(), 2, 2)
+                   for i in range(m)]
+    spec_bytes = int(sum(b.full for b in spec_models) / m)
+    spec_kv = int(sum(b.kv_full for b in spec_models) / m)
 
     def after():
         out = {}
@@ -479,11 +490,12 @@ def case_cache(dev, seed=20261103):
 
     case = Case("cache", "host-backed cache (pinned host pool, swap-in, P n R speculation): "
                 "hostcache.speculative_step against hostcache.exact", graphs, m,
-                int(meta + u_a * tile), int(u_a * tile), int(meta + u_a * tile),
+                spec_bytes, spec_kv, int(meta + u_a * tile),
                 primary="cache_step", baseline="cache_serial",
                 notes=f"c3 shape, {slots} device slots per KV head of {c.blocks} blocks, 12 "
                       "correlated queries, prediction = previous step's selection; bytes: the "
-                      "device-side algorithmic bytes (H2D reported separately)")
+                      "device-side algorithmic bytes, the speculative path's with the "
+                      "predicted blocks' tiles and states (H2D reported separately)")
     case.after = after
     case.keep = (qd, lod, hid, sels, preds, spec, ser)
     for i in (0, m - 1):
