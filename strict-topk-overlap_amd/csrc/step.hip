@@ -224,7 +224,7 @@ STK_API int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d,
   if (hq <= 0 || hkv <= 0 || hq % hkv) return 0;
   if (plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, 0, &s)) return 0;
   return step1_covers(dtype, hq, hkv, b, d, s) &&
-         step1_ctl_words(hq, n, sp) <= kCtlSlotWords ? 1 : 0;
+         step1_ctl_words(hq, n, sp) < kCtlSlotWords ? 1 : 0;   // the last word counts time-outs
 }
 
 STK_API int stk_step1_timeouts(void) {

@@ -398,9 +398,16 @@ def case_c3sweep(dev, seed=20261103):
             st = GqaStep(c, ov, seed + k_, dev, sets=m)
             steps.append(st)   # its graphs read its device copies until measured
             tag = f"{ov:g}/s{k_}"
-            for name, fn in (("fused", st.fused), ("serial", st.serial)):
+            # the reference API's own two-stream composition (overlap_run of
+            # gqa.select_blocks || gqa.partials, then repair_saved_auto) on
+            # the first seed of every hit rate
+            paths = (("fused", st.fused), ("serial", st.serial)) + \
+                ((("composed", st.full),) if k_ == 0 else ())
+            for name, fn in paths:
                 graphs[f"{name}@{tag}"], outs[f"{name}@{tag}"] = timing.capture(_seq(fn, m))
             pairs[tag] = (f"fused@{tag}", f"serial@{tag}")
+            if k_ == 0:
+                pairs[f"composed@{tag}"] = (f"composed@{tag}", f"serial@{tag}")
             if ov == 0.9 and k_ == 0:
                 by = st.bytes()
             q, k, v, lo, hi = st.host
@@ -410,11 +417,12 @@ def case_c3sweep(dev, seed=20261103):
             remap[need] = torch.arange(len(need))
             sel_r = remap[sel.long()].to(torch.int32)
             ks, vs = k[:, need], v[:, need]
-            for name in ("fused", "serial"):
+            for name in ("fused", "serial") + (("composed",) if k_ == 0 else ()):
                 checks.append((f"{name}@{tag}", "attention",
                                (q, ks, vs, sel_r, outs[f"{name}@{tag}"][-1].cpu())))
     case = Case("c3_sweep", "c3 fused step vs serial at overlap 1.0 / 0.9 / 0.75, seeds "
-                f"{seed}..{seed + 2}", graphs, m, by.full, by.kv_full, by.serial,
+                f"{seed}..{seed + 2}; the drop-in two-stream composition (repair_saved_auto) "
+                "on the first seed", graphs, m, by.full, by.kv_full, by.serial,
                 primary="fused@0.9/s0", baseline="serial@0.9/s0", pairs=pairs,
                 notes="byte counts and fractions: the 0.9 / first-seed case")
     case.keep = steps

@@ -61,6 +61,18 @@ def test_host_only_queries(lib):
     assert rc == -1 and b"divisible" in L.stk_last_error()
 
 
+def test_one_launch_support_matches_the_flag_slot(lib):
+    """stk_step1_supported reports one launch exactly when the flags,
+    Hq * (ceil(N / 64) + SP) words, fit a slot of 16384 words beside its
+    time-out counter: 16383 words fit, 16384 do not."""
+    L = lib.lib()
+    # 127 heads * (65 chunks + 64 slots) = 16383
+    assert L.stk_step1_supported(2, 127, 127, 4160, 32, 64, 64, 64, 0) == 1
+    # 128 heads * (64 chunks + 64 slots) = 16384
+    assert L.stk_step1_supported(2, 128, 32, 4096, 32, 64, 64, 64, 0) == 0
+    assert L.stk_step_supported(2, 128, 32, 4096, 32, 64, 64, 64, 0) == 1
+
+
 def test_noalloc_step_rejects_oversized_key_rows(lib):
     """The allocation-free step refuses Hq * N above its fixed scratch before
     touching a device."""
