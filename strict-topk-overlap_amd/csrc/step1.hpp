@@ -12,9 +12,10 @@
 //   states    one wave per (query head, predicted slot): the block's softmax
 //             state (states_tok.hpp); then one flag per item;
 //   tail      one workgroup per query head: waits for its chunk flags, runs
-//             the exact top-K, lists the misses and issues their tiles, waits
-//             for its state flags, then the saved / union repair and the
-//             merge (the arithmetic of tail.hpp).
+//             the exact top-K, requests its state flags while it lists the
+//             misses, then issues the missed tiles with the state rows and
+//             runs the saved / union repair and the merge (the arithmetic
+//             of tail.hpp).
 // The tails' top-K and miss tiles thus overlap the states' HBM traffic,
 // instead of following it behind a kernel boundary.
 //
@@ -105,6 +106,11 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
     if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
   };
   const uint32_t flags = topk_bins_flags<KPT>(key, n, a.k, tb, fill_map);
+  // ---- the state flags, requested now and read after the scan, so that
+  // their round trip overlaps it (slots past SP read slot 0; SP <= 128 here)
+  const int fl0 = lane_id(), fl1 = lane_id() + STK_WAVE;
+  const uint32_t fv0 = ld_agent(tflag + (fl0 < sp ? fl0 : 0));
+  const uint32_t fv1 = ld_agent(tflag + (fl1 < sp ? fl1 : 0));
   // ---- ranks of the selected IDs and the misses, one packed scan
   uint32_t mflags = 0;
 #pragma unroll
@@ -128,20 +134,18 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
     if ((mflags >> i) & 1u) miss[mpos++] = idx;
   }
   __syncthreads();
-  // ---- the state flags once, then each wave's first missed tile: if the
-  // states are published already, their rows need not wait for the tiles
-  // (loads return in order)
+  // ---- every state published (or, rarely, a wait for the last ones), then
+  // each wave's first missed tile and the state rows together.  The wait
+  // comes first: a wait issued after the tile's loads would wait for the tile
+  // too (loads return in order)
   const int kvh = h / G;
   const float scale = 1.0f / sqrtf((float)D);
   const T* K = reinterpret_cast<const T*>(a.kv.k);
   const T* V = reinterpret_cast<const T*>(a.kv.v);
   auto tile = [&](int x) { return (((size_t)kvh * n + miss[x]) * a.kv.b) * D; };
   uint32_t kw[2][TT::QW], vw[TT::CH][TT::VW];
-  vm_drain();
-  int ready = 1;
-  for (int i = lane_id(); i < sp; i += STK_WAVE) ready &= ld_agent(tflag + i) != 0u;
+  if (!__all((fv0 != 0u || fl0 >= sp) && (fv1 != 0u || fl1 >= sp))) wait_flags(tflag, sp, A.err);
   if (w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
-  if (!__all(ready)) wait_flags(tflag, sp, A.err);
   // ---- this head's prediction states (thread (rg, c4): columns 4 c4 .. +3
   // of rows rg + RG j)
   const int c4 = tid % TPR, rg = tid / TPR;
@@ -158,15 +162,12 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
     uu[j] = make_float4(__uint_as_float((uint32_t)x0), __uint_as_float((uint32_t)(x0 >> 32)),
                         __uint_as_float((uint32_t)x1), __uint_as_float((uint32_t)(x1 >> 32)));
   }
-  // ---- the misses' states with the online softmax (the first tile has
-  // arrived; the state rows travel meanwhile)
+  // ---- the first missed tile's state with the online softmax (the state
+  // rows travel meanwhile)
   float m = -INFINITY, l = 0.f, acc[TT::DPL];
 #pragma unroll
   for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
-  for (int x = w; x < nm; x += kTailWaves) {
-    if (x != w) t.load(K + tile(x), V + tile(x), 0, kw, vw);
-    t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
-  }
+  if (w < nm) t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
   // ---- the hits' (union: every valid predicted row's) partial LSE sums:
   // saved mode takes slot p when P[p] is selected and p is the highest slot
   // holding that block
@@ -211,6 +212,14 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   if (lane_id() == 0) {
     s_hl[w] = hl;
     s_hmax[w] = hm;
+  }
+  // ---- a wave's further misses (more than eight per head), once the state
+  // rows' registers are free (holding both would spill registers)
+  for (int x = w + kTailWaves; x < nm; x += kTailWaves) {
+    t.load(K + tile(x), V + tile(x), 0, kw, vw);
+    t.template update<false, false>(qw, kw, vw, 0, a.kv.b, scale, m, l, acc);
+  }
+  if (lane_id() == 0) {
     s_wm[w] = m;
     s_wl[w] = l;
   }
