@@ -335,8 +335,8 @@ int stk_step_tail(const void* q, const void* k, const void* v, int dtype, int hq
  * (strict_topk/kernels.py:450-477, _group :94-117), then
  * signed_fused.repair_signed_fused (strict_topk/signed_fused.py:148-193:
  * _schedule signed_repair.py:18-82, _corrections :30-67, _finalize :70-145),
- * in two launches on one stream (the front of stk_speculative_step, then one
- * workgroup per query head doing the top-K, the grouping, the signed
+ * in two launches on one stream (the scoring and state grid of
+ * stk_speculative_step's two-launch form, then one workgroup per query head doing the top-K, the grouping, the signed
  * corrections, the guarded merge and the strict fallback).  hybrid 1: hybrid
  * prediction, 0: saved.  Outputs: selected[Hq,topk] int32 ascending, the
  * prediction state m,l[Hq,sp], u[Hq,sp,D], out[Hq,D], fallback[Hq] and

@@ -1,9 +1,10 @@
-// The speculative decode step in two launches on one stream.
+// The speculative decode step on one stream: one launch (k_step1, step1.hpp)
+// where it covers the shape, otherwise two.
 //
 // The reference runs select and speculate on two streams and joins them
 // before the repair (benchmarks/run_benchmark.py:99-118, overlap_run).  On
-// MI355X a captured two-stream fork/join costs more than the kernels it
-// overlaps, so this file gives the same step as:
+// MI355X the two branches of a captured fork/join do not run concurrently,
+// so the overlap is scheduled inside a grid.  The two-launch form is:
 //   k_front        one grid whose workgroups are either scoring workgroups
 //                  (bound score of a chunk of blocks -> 64-bit keys) or
 //                  speculation workgroups (per-block softmax states of the

@@ -156,7 +156,7 @@ class GqaStep:
                            lambda a, st: self.finish(a, st, i), self.ss, self.ps)
 
     def fused(self, i=0, sets=None):
-        """The same step in two launches on one stream (strict_topk.step)."""
+        """The same step on one stream (strict_topk.step: one launch at c2 / c3)."""
         sets = self.sets if sets is None else sets
         q, k, v, lo, hi = sets[i % len(sets)]
         return step_mod.speculative_step(q, k, v, lo, hi, self.predicted, self.cfg.topk).output

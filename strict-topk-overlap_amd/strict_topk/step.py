@@ -6,12 +6,16 @@ The reference composes the step in its harness
 already-known predicted blocks on another, then the repair on the joined
 stream (``gqa_light.repair_saved_auto`` / ``gqa.repair_saved``, or
 ``gqa.repair_union``).  ``speculative_step`` computes the same three results
-(selected IDs, prediction state, repaired output) with two launches on the
-current stream: one grid that scores blocks and computes the predicted
-blocks' states side by side, then one workgroup per query head doing the
-exact top-K and the repair.  Shapes the fused kernels do not cover (fp32,
-other head dims, long rows) run the same steps through the individual entry
-points, still on the GPU.
+(selected IDs, prediction state, repaired output) on the current stream.
+Where the library's one-launch step covers the shape (bf16/fp16, blocks of
+32 tokens, D of 64 or 128, at most four query heads per KV head), that is
+one grid: workgroups that score blocks, workgroups that compute the
+predicted blocks' states, and one workgroup per query head that waits for
+its scores, runs the exact top-K while the states still stream, then waits
+for its states and repairs.  Other fused shapes take two launches (the
+scoring and state workgroups, then the per-head tails).  Shapes the fused
+kernels do not cover (fp32, other head dims, long rows) run the same steps
+through the individual entry points, still on the GPU.
 
 ``speculative_signed_step`` does the same for the signed strategy:
 ``select_blocks`` || ``kernels.speculate(mode, keep_mass=True)``, then
