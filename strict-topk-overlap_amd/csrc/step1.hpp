@@ -64,6 +64,8 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   constexpr int D = TT::D;
   constexpr int TPR = D / 4;              // threads per state row (16-byte columns)
   constexpr int RG = kTailThreads / TPR;  // rows per pass of the state loads
+  // SP <= RG * RPT (the launch covers no more slots): two flags per lane
+  static_assert(RG * RPT <= 2 * STK_WAVE, "the state flags are read two per lane");
   __shared__ int map[kTailMapN];
   __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
   __shared__ TopkBinsLds tb;
