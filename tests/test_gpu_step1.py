@@ -6,9 +6,10 @@ per-stream slots of static device memory; the two launches hand them over at
 the kernel boundary.  The arithmetic is the same, so selected IDs, prediction
 states and outputs must agree bit for bit; the oracle checks the outputs as
 well.  The cases cover every covered shape class (G = 1..4, D = 64 / 128,
-four, eight and sixteen keys per tail thread, ragged N), repeated graph
-replays with inputs changed in place, two streams at once, and shape changes
-on one stream (flags left zero by every launch); no wait may ever time out.
+four, eight and sixteen keys per tail thread, ragged N, K = N, one block),
+predictions with invalid and repeated IDs, repeated graph replays with inputs
+changed in place, two streams at once, and shape changes on one stream (flags
+left zero by every launch); no wait may ever time out.
 """
 import numpy as np
 import pytest
@@ -91,6 +92,8 @@ def _same(res, ref):
     (12, 3, 4000, 64, 50, 0.5, torch.float16, False),      # eight keys per tail thread
     (8, 8, 7000, 128, 16, 0.9, torch.bfloat16, False),     # sixteen keys per tail thread
     (6, 2, 333, 128, 40, 0.6, torch.bfloat16, False),      # G = 3, N not a chunk multiple
+    (4, 4, 64, 64, 64, 1.0, torch.float16, False),         # K = N: every block selected
+    (4, 2, 1, 128, 1, 1.0, torch.bfloat16, False),         # one block
 ])
 def test_step1_matches_two_launches(hq, hkv, n, d, topk, overlap, dtype, union):
     from strict_topk import step
@@ -168,4 +171,31 @@ def test_step1_two_streams_and_shape_changes():
     for name, results in got.items():
         for res in results:
             _same(res, refs[name])
+    assert _timeouts() == 0
+
+
+def test_step1_predictions_with_invalid_and_repeated_ids():
+    """Predicted rows holding -1, IDs past N and a block listed twice: the
+    one launch treats them as the two launches do (an invalid slot has the
+    empty state and is never a hit; a repeated block is a hit at its highest
+    slot), and the output is still the exact attention over the selection."""
+    from strict_topk import step
+    host, (q, k, v, lo, hi, p), ref_ids = _inputs(32, 8, 2048, 128, 64, 0.9, torch.bfloat16,
+                                                  20261207)
+    pc = p.cpu().clone()
+    pc[:, 0] = -1
+    pc[:, 1] = 2048 + 5
+    pc[::2, 2] = pc[::2, 3]             # even heads list one block twice
+    pc[1::2, 5] = -7
+    p = pc.cuda()
+    ref = _two_launches(q, k, v, lo, hi, p, 64, False)
+    res = step.speculative_step(q, k, v, lo, hi, p, 64)
+    _same(res, ref)
+    assert res.selected.cpu().numpy().tolist() == ref_ids.tolist()
+    qn, kn, vn = (C.f64(t) for t in host[:3])
+    m = C.error_metrics(C.f64(res.output), O.attention(qn, kn, vn, ref_ids))
+    assert m["passed"], m
+    # the invalid slots hold the empty state
+    assert torch.all(res.state.m[:, :2] == float("-inf"))
+    assert torch.all(res.state.l[:, :2] == 0)
     assert _timeouts() == 0
