@@ -280,10 +280,18 @@ int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d, int top
                         int pred_dtype);
 
 /* Slots of the current device whose one-launch step ever timed out waiting
- * for a flag (each wait gives up after 20 ms, so every launch ends); 0 in any
- * correct run.  A host-side query that copies from the device (it waits for
+ * for a flag (each wait gives up after 20 ms, so every launch ends, and the
+ * head that waited gets a NaN output and IDs of -1); 0 in any correct run.  A host-side query that copies from the device (it waits for
  * the device); for tests. */
 int stk_step1_timeouts(void);
+
+/* Test hook, no reference counterpart: sets the one-launch step's longest
+ * wait (spin_ticks of the 100 MHz counter; 2000000 by default) and, with
+ * drop_flags 1, makes its producers publish no flag, so that every wait times
+ * out and the kernel still ends.  A tail whose wait timed out writes NaN
+ * outputs and IDs of -1 for its head.  Clears the time-out counters of the
+ * current device (a synchronous copy).  For failure-handling tests only. */
+int stk_step1_test_hook(unsigned long long spin_ticks, int drop_flags);
 
 /* Allocation-free variant of stk_speculative_step.  It has no counterpart in
  * the reference: it is for callers that cannot allocate (code under HIP graph

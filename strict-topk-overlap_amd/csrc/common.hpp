@@ -446,14 +446,16 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 constexpr uint64_t kSpinTicks = 2000000ull;
 
 // Wave-level bounded wait until flag[i] != 0 for every i < cnt; false (and
-// *err incremented) on time-out.  Every lane returns together.
-__device__ __forceinline__ bool wait_flags(const uint32_t* flag, int cnt, uint32_t* err) {
+// *err incremented) once `spin` ticks have passed.  Every lane returns
+// together.
+__device__ __forceinline__ bool wait_flags(const uint32_t* flag, int cnt, uint32_t* err,
+                                           uint64_t spin = kSpinTicks) {
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   while (true) {
     int ready = 1;
     for (int i = lane_id(); i < cnt; i += STK_WAVE) ready &= ld_agent(flag + i) != 0u;
     if (__all(ready)) return true;
-    if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
+    if (__builtin_amdgcn_s_memrealtime() - t0 > spin) {
       if (lane_id() == 0) atomicAdd(err, 1u);
       return false;
     }

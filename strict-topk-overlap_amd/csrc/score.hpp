@@ -52,6 +52,7 @@ struct ScoreArgs {
   float* scores;         // optional FP32 [hq, n]
   uint64_t* keys;        // optional [hq, n]
   uint32_t* sflag;       // SIG: [hq, chunks], set once a chunk's keys are published
+  int drop;              // SIG, tests only: publish no flag (the consumers time out)
 };
 
 // Physical lane (0..15 inside a row) -> logical lane of the summation order.
@@ -318,7 +319,8 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
     // publish the chunk to every query head of the group
     wait_stores();
     __syncthreads();
-    if ((int)threadIdx.x < G) st_agent(a.sflag + (size_t)(h0 + threadIdx.x) * a.chunks + chunk, 1u);
+    if (!a.drop && (int)threadIdx.x < G)
+      st_agent(a.sflag + (size_t)(h0 + threadIdx.x) * a.chunks + chunk, 1u);
   }
 }
 

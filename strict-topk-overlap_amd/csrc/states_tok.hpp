@@ -27,6 +27,7 @@ struct StatesArgs {
   int combine;
   const float* pm; const float* pl; const float* pu; int psp;
   uint32_t* tflag;                            // SIG: [hq * s], set once an item's state is published
+  int drop;                                   // SIG, tests only: publish no flag
 };
 
 constexpr int kGrpHT = 4;   // heads sharing one loaded tile (generic-tile kernels)
@@ -113,7 +114,7 @@ __device__ __forceinline__ void states_tok_wg(const StatesArgs& a, int wg,
     }
     t.store_agent(a.u + item * a.d, acc);
     wait_stores();
-    if (lane_id() == 0) st_agent(a.tflag + item, 1u);
+    if (!a.drop && lane_id() == 0) st_agent(a.tflag + item, 1u);
   } else {
     if (lane_id() == 0) {
       a.m[item] = m;

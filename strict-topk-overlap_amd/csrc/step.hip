@@ -18,6 +18,7 @@
 //                  blocks' tiles).
 // The arithmetic is that of stk_select_blocks, stk_block_partials and
 // stk_gqa_repair; results are identical up to FP32 reduction order.
+#include <atomic>
 #include <mutex>
 
 #include "step1.hpp"
@@ -88,6 +89,10 @@ static __device__ __align__(256) uint32_t g_step1_ctl[kCtlSlots * kCtlSlotWords]
 
 static constexpr int kMaxDevices = 64;
 static std::mutex g_ctl_mu;
+// The one launch's longest wait and, for failure tests only, whether its
+// producers skip their flags (stk_step1_test_hook).
+static std::atomic<uint64_t> g_step1_spin{kSpinTicks};
+static std::atomic<int> g_step1_drop{0};
 static struct {
   uint32_t* base;
   hipStream_t streams[kCtlSlots];
@@ -198,7 +203,9 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
     uint32_t* ctl = nullptr;
     const int rc = ctl_slot(st, step1_ctl_words(hq, n, sp), &ctl);
     if (rc) return rc;
-    if (ctl) return launch_step1(dtype, f, t, s, ctl, ctl + kCtlSlotWords - 1, st);
+    if (ctl)
+      return launch_step1(dtype, f, t, s, ctl, ctl + kCtlSlotWords - 1, g_step1_spin.load(),
+                          g_step1_drop.load(), st);
   }
   if (front) {
     const int rc = launch_front(dtype, f, s, st);
@@ -241,6 +248,22 @@ STK_API int stk_step1_timeouts(void) {
     count += v != 0;
   }
   return count;
+}
+
+STK_API int stk_step1_test_hook(unsigned long long spin_ticks, int drop_flags) {
+  g_step1_spin.store(spin_ticks);
+  g_step1_drop.store(drop_flags ? 1 : 0);
+  const uint32_t zero = 0;
+  for (int i = 0; i < kCtlSlots; ++i) {
+    const hipError_t e = hipMemcpyToSymbol(
+        HIP_SYMBOL(g_step1_ctl), &zero, sizeof(zero),
+        ((size_t)i * kCtlSlotWords + kCtlSlotWords - 1) * sizeof(uint32_t), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      stk_set_error("clearing the time-out counters: %s", hipGetErrorString(e));
+      return STK_EHIP;
+    }
+  }
+  return STK_OK;
 }
 
 // ---- the allocation-free variant of stk_speculative_step

@@ -24,7 +24,7 @@ int launch_t(const Step1Args& a, const StepShape& s, hipStream_t st) {
 }  // namespace
 
 int launch_step1(int dtype, const FrontArgs& f, const TailArgs& t, const StepShape& s,
-                 uint32_t* ctl, uint32_t* err, hipStream_t st) {
+                 uint32_t* ctl, uint32_t* err, uint64_t spin, int drop, hipStream_t st) {
   if (!step1_covers(dtype, t.kv.hq, t.kv.hkv, t.kv.b, t.kv.d, s)) return 1;
   Step1Args a{};
   a.f = f;
@@ -37,6 +37,8 @@ int launch_step1(int dtype, const FrontArgs& f, const TailArgs& t, const StepSha
   a.f.sc.sflag = ctl;
   a.f.st.tflag = ctl + (size_t)hq * a.f.sc.chunks;
   a.err = err;
+  a.spin = spin;
+  a.f.sc.drop = a.f.st.drop = drop;
   if (dtype == DT_BF16) {
     return t.kv.d == 64 ? launch_t<bf16s, 2>(a, s, st) : launch_t<bf16s, 4>(a, s, st);
   }

@@ -47,6 +47,7 @@ struct Step1Args {
   FrontArgs f;       // f.sc.sflag [hq, chunks], f.st.tflag [hq * sp]
   TailArgs t;
   uint32_t* err;     // counts timed-out waits
+  uint64_t spin;     // longest wait, in ticks of the 100 MHz real-time counter
   int S, T, H;       // workgroups per role: scoring, states, tails
 };
 
@@ -70,6 +71,7 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   __shared__ int sel[kTailMaxK], miss[kTailMaxK], pids[kTailMaxK];
   __shared__ TopkBinsLds tb;
   __shared__ int s_scan[kTailWaves];
+  __shared__ int s_fail;   // a wave's wait timed out: the head's results are void
   __shared__ float s_hmax[kTailWaves], s_hl[kTailWaves];
   __shared__ __align__(16) float s_hu[kTailWaves][D];
   __shared__ float s_wm[kTailWaves], s_wl[kTailWaves], s_wu[kTailWaves][D];
@@ -89,8 +91,9 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   // every slot entry is written (-1 past sp): the sums below read entries
   // past sp, and LDS holds whatever an earlier workgroup left there
   if (tid < kTailMaxK) pids[tid] = pid;
+  if (tid == 0) s_fail = 0;
   // ---- this head's keys, once every chunk of its KV head is published
-  wait_flags(sflag, chunks, A.err);
+  bool ok = wait_flags(sflag, chunks, A.err, A.spin);
   uint64_t key[KPT];
   {
     const uint64_t* rk = a.keys + (size_t)h * n;
@@ -146,7 +149,8 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   const T* V = reinterpret_cast<const T*>(a.kv.v);
   auto tile = [&](int x) { return (((size_t)kvh * n + miss[x]) * a.kv.b) * D; };
   uint32_t kw[2][TT::QW], vw[TT::CH][TT::VW];
-  if (!__all((fv0 != 0u || fl0 >= sp) && (fv1 != 0u || fl1 >= sp))) wait_flags(tflag, sp, A.err);
+  if (!__all((fv0 != 0u || fl0 >= sp) && (fv1 != 0u || fl1 >= sp)))
+    ok = wait_flags(tflag, sp, A.err, A.spin) && ok;
   if (w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
   // ---- this head's prediction states (thread (rg, c4): columns 4 c4 .. +3
   // of rows rg + RG j)
@@ -226,7 +230,12 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
     s_wl[w] = l;
   }
   t.store(s_wu[w], acc);
+  if (!ok && lane_id() == 0) atomicOr(&s_fail, 1);
   __syncthreads();
+  // a timed-out wait read keys or states that may not have been published:
+  // the head's output is NaN and its IDs -1, so the failure cannot pass for a
+  // result (stk_step1_timeouts counts it)
+  const bool fail = s_fail != 0;
   // ---- every wave is past its waits: clear this head's flags for the next
   // launch (no producer writes them again in this one)
   if (tid < chunks) st_agent(sflag + tid, 0u);
@@ -243,11 +252,11 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
       num += fh * s_hu[x][tid] + f * s_wu[x][tid];
       den += fh * s_hl[x] + f * s_wl[x];
     }
-    a.out[(size_t)h * D + tid] = num / den;
+    a.out[(size_t)h * D + tid] = fail ? __builtin_nanf("") : num / den;
   }
   // the selected IDs last (stores share the loads' counter: issued earlier,
   // they would hold the waits above)
-  for (int i = tid; i < a.k; i += kTailThreads) a.ids[(size_t)h * a.k + i] = sel[i];
+  for (int i = tid; i < a.k; i += kTailThreads) a.ids[(size_t)h * a.k + i] = fail ? -1 : sel[i];
 }
 
 // T: bf16 / fp16; NCH: D / 32 (D = 64 or 128); blocks of 32 tokens; up to
@@ -272,8 +281,10 @@ bool step1_covers(int dtype, int hq, int hkv, int b, int d, const StepShape& s);
 
 // Launch k_step1 when step1_covers the shape (returns 1 otherwise, with
 // nothing launched).  ctl: step1_ctl_words(hq, n, sp) zero words (left
-// zero); err: a word incremented for every timed-out wait.
+// zero); err: a word incremented for every timed-out wait; spin: the longest
+// wait in ticks; drop (tests only): the producers publish no flag, so every
+// wait times out.
 int launch_step1(int dtype, const FrontArgs& f, const TailArgs& t, const StepShape& s,
-                 uint32_t* ctl, uint32_t* err, hipStream_t st);
+                 uint32_t* ctl, uint32_t* err, uint64_t spin, int drop, hipStream_t st);
 
 }  // namespace stk

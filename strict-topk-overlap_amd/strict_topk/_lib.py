@@ -61,6 +61,7 @@ _SIGS = {
                                  P, P, P, P, P, P, Z, P]),
     "stk_step1_supported": (I, [I, I, I, I, I, I, I, I, I]),
     "stk_step1_timeouts": (I, []),
+    "stk_step1_test_hook": (I, [ctypes.c_ulonglong, I]),
     "stk_step_noalloc_max_keys": (Z, []),
     "stk_step_prepare": (I, []),
     "stk_speculative_step_noalloc": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, I,

@@ -199,3 +199,30 @@ def test_step1_predictions_with_invalid_and_repeated_ids():
     assert torch.all(res.state.m[:, :2] == float("-inf"))
     assert torch.all(res.state.l[:, :2] == 0)
     assert _timeouts() == 0
+
+
+def test_step1_timed_out_waits_fail_loudly():
+    """With the producers' flags withheld (a test hook) and a 20 us wait
+    limit, every tail's wait times out: the kernel still ends, each head's
+    output is NaN and its IDs are -1, and stk_step1_timeouts counts it.  The
+    next launch on the same slot, with the hook off, is exact again (the
+    tails left the flags zero)."""
+    from strict_topk import _lib, step
+    L = _lib.lib()
+    _, (q, k, v, lo, hi, p), ref_ids = _inputs(32, 8, 2048, 128, 64, 0.9, torch.bfloat16,
+                                               20261208)
+    ref = _two_launches(q, k, v, lo, hi, p, 64, False)
+    torch.cuda.synchronize()
+    assert L.stk_step1_test_hook(2000, 1) == 0
+    try:
+        res = step.speculative_step(q, k, v, lo, hi, p, 64)
+        torch.cuda.synchronize()
+        assert torch.isnan(res.output).all()
+        assert (res.selected == -1).all()
+        assert L.stk_step1_timeouts() >= 1
+    finally:
+        assert L.stk_step1_test_hook(2000000, 0) == 0
+    assert L.stk_step1_timeouts() == 0
+    res = step.speculative_step(q, k, v, lo, hi, p, 64)
+    _same(res, ref)
+    assert _timeouts() == 0
