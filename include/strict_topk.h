@@ -98,11 +98,7 @@ int stk_exact_attention(const void* q, const void* k, const void* v, int dtype, 
  * saved: m,l,u[Hq,s].  hybrid: also high[Hq,s], low_m/low_l[Hq], low_u and
  * low_abs[Hq,D].  compact (capacity C from kernels.py:485): m,l,u[Hq,C],
  * retained_ids[Hq,C] (pred_dtype, rank order, -1 padded), overflow[Hq],
- * mass_m/mass_l[Hq,s] required.  Unused outputs may be NULL.  hybrid with
- * bf16/fp16 Q/K/V, B of 16 or 32, D of 64 or 128, s <= 256 and 16-byte
- * aligned rows runs as one launch (the grouping of a head starts once its
- * states are published, through the flag slots of the one-launch step; the
- * same bits as the two launches). */
+ * mass_m/mass_l[Hq,s] required.  Unused outputs may be NULL. */
 int stk_speculate(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
                   int b, int d, const void* pred, int pred_dtype, int s, int mode, float tau,
                   int capacity, float* m, float* l, float* u, uint8_t* high, float* low_m,
@@ -289,15 +285,13 @@ int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d, int top
  * the device); for tests. */
 int stk_step1_timeouts(void);
 
-/* Test hook, no reference counterpart, for the one-launch kernels (the
- * speculative step and the hybrid speculation of stk_speculate): sets their
- * longest wait (spin_ticks of the 100 MHz counter; 2000000 by default).
- * flags bit 0: their producers publish no flag, so that every wait times out
- * and the kernel still ends (a head whose wait timed out gets NaN outputs,
- * IDs of -1 and, in the speculation, no high block); bit 1: run their
- * multi-launch forms instead.  Clears the time-out counters of the current
- * device (a synchronous copy).  For tests only. */
-int stk_step1_test_hook(unsigned long long spin_ticks, int flags);
+/* Test hook, no reference counterpart: sets the one-launch step's longest
+ * wait (spin_ticks of the 100 MHz counter; 2000000 by default) and, with
+ * drop_flags 1, makes its producers publish no flag, so that every wait times
+ * out and the kernel still ends.  A tail whose wait timed out writes NaN
+ * outputs and IDs of -1 for its head.  Clears the time-out counters of the
+ * current device (a synchronous copy).  For failure-handling tests only. */
+int stk_step1_test_hook(unsigned long long spin_ticks, int drop_flags);
 
 /* Allocation-free variant of stk_speculative_step.  It has no counterpart in
  * the reference: it is for callers that cannot allocate (code under HIP graph

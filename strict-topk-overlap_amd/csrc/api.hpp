@@ -53,14 +53,6 @@ struct Carve {
   }
 };
 
-// kernels.speculate(mode='hybrid') in one launch (spec1.hip): 0 when launched,
-// 1 when the shape is not covered (nothing launched; run the two launches),
-// an error code otherwise.
-int launch_spec1(const void* q, const void* k, const void* v, int dtype, int hq, int hkv, int n,
-                 int b, int d, const void* pred, int pred_dtype, int s, float tau, float* m,
-                 float* l, float* u, uint8_t* high, float* lm, float* ll, float* lu, float* labs,
-                 hipStream_t st);
-
 int stk_launch_states(const void* q, const void* k, const void* v, int dtype, int hq, int hkv,
                       int n, int b, int d, const void* ids, int itype, int s,
                       const uint8_t* active, int active_kind, const void* pred, int ptype, int sp,

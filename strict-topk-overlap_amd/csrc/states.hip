@@ -10,7 +10,6 @@
 //   strict_topk/kernels.py:263-356 _mass_only / _compact_group / _compact_values
 //   strict_topk/kernels.py:250-260 _touch        -> k_touch
 #include "states_pack.hpp"
-#include "group.hpp"
 #include "api.hpp"
 
 namespace stk {
@@ -330,7 +329,12 @@ __global__ __launch_bounds__(256) void k_merge2(MergeArgs a) {
   }
 }
 
-// Hybrid grouping (kernels.py:94-117; GroupArgs in group.hpp).
+// Hybrid grouping (kernels.py:94-117).
+struct GroupArgs {
+  const float* m; const float* l; const float* u;
+  int h, s, d; float tau;
+  uint8_t* high; float* lm; float* ll; float* lu; float* labs;
+};
 
 __global__ __launch_bounds__(256) void k_hybrid_group(GroupArgs a) {
   __shared__ float red[32];
@@ -399,9 +403,125 @@ __global__ __launch_bounds__(256) void k_hybrid_group(GroupArgs a) {
   }
 }
 
-// The same grouping in one round trip (group.hpp).
+// The same grouping in one memory round trip, for S <= 256 state rows, D a
+// multiple of 4 (<= 1024) and 16-byte aligned rows: every thread issues its
+// m, l and the u rows it will weight at once; the row scalars pass through
+// LDS once, after which every wave forms the same global max, total mass,
+// high flags and low frame with wave reductions (no further barrier); the
+// low aggregate and its envelope are summed per (row group, column) and
+// folded through LDS.
+constexpr int kGroupRows = 256;
+constexpr int kGroupPF = 8;   // u float4s in flight per thread per pass
+
+__device__ __forceinline__ bool group_high(float m, float l, float gm, float thr) {
+  return wexp(m, gm) * l >= thr;
+}
+
 __global__ __launch_bounds__(256) void k_hybrid_group1(GroupArgs a) {
-  group1_head<false>(a, blockIdx.x);
+  __shared__ float s_m[kGroupRows], s_l[kGroupRows];
+  __shared__ float4 s_pu[256], s_pa[256];
+  const int h = blockIdx.x, tid = threadIdx.x, s = a.s, d = a.d;
+  const float* M = a.m + (size_t)h * s;
+  const float* L = a.l + (size_t)h * s;
+  const float* U = a.u + (size_t)h * s * d;
+  const float mv = tid < s ? M[tid] : -INFINITY;
+  const float lv = tid < s ? L[tid] : 0.f;
+  const int tpr = d >> 2, rgn = 256 / tpr;
+  const int c4 = tid % tpr, rg = tid / tpr;
+  const bool act = rg < rgn;
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 uu[kGroupPF];
+  auto fetch = [&](int pass) {
+#pragma unroll
+    for (int j = 0; j < kGroupPF; ++j) {
+      const int r = rg + rgn * (pass * kGroupPF + j);
+      uu[j] = act && r < s ? *reinterpret_cast<const float4*>(U + (size_t)r * d + 4 * c4) : zero;
+    }
+  };
+  fetch(0);
+  s_m[tid] = mv;
+  s_l[tid] = lv;
+  __syncthreads();
+  // ---- slot reductions, the same in every wave (lane l: rows l + 64 c)
+  float pm[4], pl[4];
+  float gm = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int p = c * STK_WAVE + lane_id();
+    pm[c] = p < s ? s_m[p] : -INFINITY;
+    pl[c] = p < s ? s_l[p] : 0.f;
+    gm = fmaxf(gm, pm[c]);
+  }
+  gm = wave_max_u(gm);
+  float tot = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) tot += wexp(pm[c], gm) * pl[c];
+  const float thr = a.tau * wave_sum_u(tot);
+  bool hi[4];
+  float lm = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const bool ok = c * STK_WAVE + lane_id() < s;
+    hi[c] = ok && group_high(pm[c], pl[c], gm, thr);
+    lm = ok && !hi[c] ? fmaxf(lm, pm[c]) : lm;
+  }
+  lm = wave_max_u(lm);
+  const float lowm = lm == -INFINITY ? 0.f : lm;
+  float z = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const bool ok = c * STK_WAVE + lane_id() < s;
+    z += ok && !hi[c] ? wexp(pm[c], lowm) * pl[c] : 0.f;
+  }
+  z = wave_sum_u(z);
+  if (wave_id() == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int p = c * STK_WAVE + lane_id();
+      if (p < s) a.high[(size_t)h * s + p] = hi[c];
+    }
+    if (lane_id() == 0) {
+      a.lm[h] = lowm;
+      a.ll[h] = z;
+    }
+  }
+  // ---- low aggregate and envelope of this thread's rows
+  float4 lu = zero, la = zero;
+  const int passes = (s + rgn * kGroupPF - 1) / (rgn * kGroupPF);
+  for (int pass = 0; pass < passes; ++pass) {
+    if (pass) fetch(pass);
+#pragma unroll
+    for (int j = 0; j < kGroupPF; ++j) {
+      const int r = rg + rgn * (pass * kGroupPF + j);
+      if (act && r < s) {
+        const float mr = s_m[r], lr = s_l[r];
+        const float wt = group_high(mr, lr, gm, thr) ? 0.f : wexp(mr, lowm);
+        const float4 x = uu[j];
+        lu.x += wt * x.x; lu.y += wt * x.y; lu.z += wt * x.z; lu.w += wt * x.w;
+        la.x += wt * fabsf(x.x); la.y += wt * fabsf(x.y);
+        la.z += wt * fabsf(x.z); la.w += wt * fabsf(x.w);
+      }
+    }
+  }
+  s_pu[tid] = lu;
+  s_pa[tid] = la;
+  __syncthreads();
+  if (tid < tpr) {
+    float4 su = zero, sa = zero;
+    for (int g = 0; g < rgn; ++g) {
+      const float4 x = s_pu[g * tpr + tid], y = s_pa[g * tpr + tid];
+      su.x += x.x; su.y += x.y; su.z += x.z; su.w += x.w;
+      sa.x += y.x; sa.y += y.y; sa.z += y.z; sa.w += y.w;
+    }
+    *reinterpret_cast<float4*>(a.lu + (size_t)h * d + 4 * tid) = su;
+    *reinterpret_cast<float4*>(a.labs + (size_t)h * d + 4 * tid) = sa;
+  }
+}
+
+static bool group1_covers(int s, int d, const float* u, const float* lu, const float* labs) {
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(u) | reinterpret_cast<uintptr_t>(lu) |
+                         reinterpret_cast<uintptr_t>(labs);
+  return s <= kGroupRows && d % 4 == 0 && d <= 1024 && (bits & 15) == 0;
 }
 
 // Compact grouping (kernels.py:281-309): rank high blocks in position order,
@@ -814,13 +934,6 @@ STK_API int stk_speculate(const void* q, const void* k, const void* v, int dtype
   STK_REQUIRE(tau >= 0.f && tau <= 1.f, "mass_threshold must be in [0,1]");
   hipStream_t st = (hipStream_t)stream;
   if (mode != 2) {
-    if (mode == 1) {
-      STK_REQUIRE(high && low_m && low_l && low_u && low_abs, "null hybrid output");
-      // the states and the grouping in one launch where it covers the shape
-      const int one = launch_spec1(q, k, v, dtype, hq, hkv, n, b, d, pred, pred_dtype, s, tau,
-                                   m, l, u, high, low_m, low_l, low_u, low_abs, st);
-      if (one <= 0) return one;
-    }
     int rc = stk_launch_states(q, k, v, dtype, hq, hkv, n, b, d, pred, pred_dtype, s, nullptr, 0,
                                nullptr, 0, 0, nullptr, m, l, u, true, st);
     if (rc || mode == 0) return rc;

@@ -21,7 +21,6 @@
 #include <atomic>
 #include <mutex>
 
-#include "flags.hpp"
 #include "step1.hpp"
 
 namespace stk {
@@ -73,24 +72,27 @@ FrontArgs make_front_args(const void* q, const void* k, const void* v, int dtype
 
 using namespace stk;
 
-// ---- flag slots of the one-launch kernels (flags.hpp)
+// ---- flag slots of the one-launch step
 //
-// `g_step1_ctl` is static device memory, zero when the library is loaded,
-// in kCtlSlots slots of kFlagSlotWords words.  With every slot taken (or a
-// shape whose flags exceed a slot) the one-launch kernels give way to their
-// multi-launch forms.  In host code `g_step1_ctl` names a host-side
-// stand-in: its device address comes from hipGetSymbolAddress.
+// k_step1's roles hand over through flags that must be zero before a launch
+// and that every launch leaves zero.  They live in `g_step1_ctl`, static
+// device memory (zero when the library is loaded), in kCtlSlots slots of
+// kCtlSlotWords words: each stream that runs the step takes a slot of its own
+// on first use, so launches in flight on different streams never share flags,
+// and launches on one stream are ordered.  The last word of a slot counts
+// timed-out waits.  With every slot taken (or a shape whose flags exceed a
+// slot) the step runs as two launches.  In host code `g_step1_ctl` names a
+// host-side stand-in: its device address comes from hipGetSymbolAddress.
 static constexpr int kCtlSlots = 64;
-static constexpr size_t kCtlSlotWords = kFlagSlotWords;
+static constexpr size_t kCtlSlotWords = 16384;
 static __device__ __align__(256) uint32_t g_step1_ctl[kCtlSlots * kCtlSlotWords];
 
 static constexpr int kMaxDevices = 64;
 static std::mutex g_ctl_mu;
-// The one-launch kernels' longest wait and, for tests only (stk_step1_test_hook),
-// whether their producers skip their flags and whether they run at all.
+// The one launch's longest wait and, for failure tests only, whether its
+// producers skip their flags (stk_step1_test_hook).
 static std::atomic<uint64_t> g_step1_spin{kSpinTicks};
 static std::atomic<int> g_step1_drop{0};
-static std::atomic<int> g_step1_off{0};
 static struct {
   uint32_t* base;
   hipStream_t streams[kCtlSlots];
@@ -103,11 +105,8 @@ static bool capturing(hipStream_t stream) {
   return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
-uint64_t stk::flag_spin() { return g_step1_spin.load(); }
-int stk::flag_drop() { return g_step1_drop.load(); }
-bool stk::flag_one_launch() { return g_step1_off.load() == 0; }
-
-int stk::flag_slot(hipStream_t stream, size_t words, bool quiet, uint32_t** out) {
+// The slot of `stream` (nullptr when none is free or `words` exceed a slot).
+static int ctl_slot(hipStream_t stream, size_t words, uint32_t** out) {
   *out = nullptr;
   if (words > kCtlSlotWords - 1) return STK_OK;
   hipDevice_t dev = 0;
@@ -121,7 +120,6 @@ int stk::flag_slot(hipStream_t stream, size_t words, bool quiet, uint32_t** out)
   auto& tab = g_ctl_tab[dev];
   if (!tab.base) {
     if (capturing(stream)) {
-      if (quiet) return STK_OK;
       stk_set_error("the step's device memory is looked up on a device's first call, which "
                     "must not be under stream capture: call stk_step_prepare() first");
       return STK_EINVAL;
@@ -200,14 +198,14 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
   t.p = static_cast<const int32_t*>(predicted); t.sp = sp;
   t.pm = m; t.pl = l; t.pu = u; t.uni = union_mode ? 1 : 0; t.out = out;
   hipStream_t st = (hipStream_t)stream;
-  if (front && tail && flag_one_launch() && step1_covers(dtype, hq, hkv, b, d, s)) {
+  if (front && tail && step1_covers(dtype, hq, hkv, b, d, s)) {
     // one launch, its flags in this stream's slot (none free: two launches)
     uint32_t* ctl = nullptr;
-    const int rc = flag_slot(st, step1_ctl_words(hq, n, sp), false, &ctl);
+    const int rc = ctl_slot(st, step1_ctl_words(hq, n, sp), &ctl);
     if (rc) return rc;
     if (ctl)
-      return launch_step1(dtype, f, t, s, ctl, ctl + kCtlSlotWords - 1, flag_spin(), flag_drop(),
-                          st);
+      return launch_step1(dtype, f, t, s, ctl, ctl + kCtlSlotWords - 1, g_step1_spin.load(),
+                          g_step1_drop.load(), st);
   }
   if (front) {
     const int rc = launch_front(dtype, f, s, st);
@@ -252,10 +250,9 @@ STK_API int stk_step1_timeouts(void) {
   return count;
 }
 
-STK_API int stk_step1_test_hook(unsigned long long spin_ticks, int flags) {
+STK_API int stk_step1_test_hook(unsigned long long spin_ticks, int drop_flags) {
   g_step1_spin.store(spin_ticks);
-  g_step1_drop.store(flags & 1);
-  g_step1_off.store((flags >> 1) & 1);
+  g_step1_drop.store(drop_flags ? 1 : 0);
   const uint32_t zero = 0;
   for (int i = 0; i < kCtlSlots; ++i) {
     const hipError_t e = hipMemcpyToSymbol(
@@ -329,7 +326,7 @@ STK_API int stk_step_prepare(void) {
   int rc = scratch_address(st, &ws);
   if (rc) return rc;
   uint32_t* ctl = nullptr;
-  return flag_slot(st, 0, false, &ctl);
+  return ctl_slot(st, 0, &ctl);
 }
 
 STK_API int stk_speculative_step_noalloc(const void* q, const void* k, const void* v, int dtype,

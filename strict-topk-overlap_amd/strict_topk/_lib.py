@@ -164,11 +164,10 @@ _prepared = set()
 
 
 def prepare(device):
-    """Look up the library's device memory (the allocation-free step's
-    scratch, the one-launch kernels' flag slots) on ``device`` once, outside
-    any stream capture: the step's C entry points refuse a device's first
-    lookup under capture, and the hybrid speculation then takes its two
-    launches."""
+    """Look up the fused step's device memory (the allocation-free step's
+    scratch, the one-launch step's flag slots) on ``device`` once, outside
+    any stream capture: the C entry points refuse a device's first lookup
+    under capture."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     if idx in _prepared or torch.cuda.is_current_stream_capturing():
         return

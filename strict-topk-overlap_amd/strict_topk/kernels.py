@@ -165,7 +165,6 @@ def speculate(q, k, v, predicted, mode='saved', mass_threshold=0.1, *, keep_mass
         high = torch.empty((h, s), device=dev, dtype=torch.bool)
         low = _allocate_state(h, 1, d, dev)
         low_abs = torch.empty((h, d), device=dev, dtype=torch.float32)
-        _lib.prepare(dev)   # the one-launch form's flag slots (looked up outside capture)
     _lib.call("stk_speculate", *_args(q, k, v), _lib.ptr(predicted), _lib.id_code(predicted), s,
               MODES[mode], float(mass_threshold), s, _lib.ptr(state.m), _lib.ptr(state.l),
               _lib.ptr(state.u), _lib.ptr(high), _lib.ptr(low.m if low else None),
