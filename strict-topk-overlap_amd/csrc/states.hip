@@ -431,11 +431,17 @@ __global__ __launch_bounds__(256) void k_hybrid_group1(GroupArgs a) {
   const bool act = rg < rgn;
   const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
   float4 uu[kGroupPF];
+  // every load is issued, rows past s (or idle threads) reading row 0 and
+  // taking zeros: a load under a condition makes the compiler keep the
+  // array in scratch memory
   auto fetch = [&](int pass) {
 #pragma unroll
     for (int j = 0; j < kGroupPF; ++j) {
       const int r = rg + rgn * (pass * kGroupPF + j);
-      uu[j] = act && r < s ? *reinterpret_cast<const float4*>(U + (size_t)r * d + 4 * c4) : zero;
+      const bool live = act && r < s;
+      const float4 x = *reinterpret_cast<const float4*>(U + (size_t)(live ? r : 0) * d +
+                                                        4 * (act ? c4 : 0));
+      uu[j] = live ? x : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
   fetch(0);
