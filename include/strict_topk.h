@@ -273,7 +273,10 @@ int stk_speculative_step(const void* q, const void* k, const void* v, int dtype,
  * states still stream, then wait for the states and merge; the roles hand
  * over through flags the library keeps in static device memory, one slot per
  * stream (64 slots per device; with every slot taken the step runs as two
- * launches).  Results are the two launches' results, bit for bit.  No
+ * launches).  A graph captured on a stream keeps that stream's slot: it must
+ * not be replayed on another stream while the capturing stream runs the step
+ * at the same time (capture on a stream of its own).  Results are the two
+ * launches' results, bit for bit.  No
  * reference counterpart beyond the step it computes
  * (benchmarks/run_benchmark.py:99-118). */
 int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
