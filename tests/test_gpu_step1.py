@@ -226,3 +226,46 @@ def test_step1_timed_out_waits_fail_loudly():
     res = step.speculative_step(q, k, v, lo, hi, p, 64)
     _same(res, ref)
     assert _timeouts() == 0
+
+
+_SLOTS_EXHAUSTED = """
+import sys
+sys.path[:0] = [{pkg!r}, {root!r}]
+import torch
+from strict_topk import _lib, step
+from stk_harness.configs import make_qkv, perturb
+from oracle import stk_oracle as O
+from tests import cases as C
+q, k, v, lo, hi = make_qkv(16, 8, 128, 32, 512, torch.bfloat16, True, 20261212)
+ids = O.select_blocks(C.f64(q), lo.numpy(), hi.numpy(), 64)
+p = perturb(torch.from_numpy(ids), 512, 64, 0.9, 5)
+q, k, v, p = (t.cuda() for t in (q, k, v, p))
+lo, hi = (t.to(torch.bfloat16).cuda() for t in (lo, hi))
+ref = step.speculative_step(q, k, v, lo, hi, p, 64)
+torch.cuda.synchronize()
+streams = [torch.cuda.Stream() for _ in range(72)]
+got = []
+for st in streams:
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        got.append(step.speculative_step(q, k, v, lo, hi, p, 64))
+torch.cuda.synchronize()
+same = all(torch.equal(r.selected, ref.selected) and torch.equal(r.output, ref.output) and
+           torch.equal(r.state.u, ref.state.u) for r in got)
+print("SAME", same, "TIMEOUTS", _lib.lib().stk_step1_timeouts())
+"""
+
+
+def test_step1_more_streams_than_slots():
+    """In a fresh process, 72 streams run the step: the first take the 64
+    flag slots and run one launch, the rest run two launches; every result is
+    the same bits and no wait times out."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    code = _SLOTS_EXHAUSTED.format(pkg=str(root / "strict-topk-overlap_amd"), root=str(root))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
+                       cwd=str(root))
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "SAME True TIMEOUTS 0" in r.stdout, (r.stdout, r.stderr[-2000:])
