@@ -24,6 +24,7 @@
 #include <cmath>
 
 #include "score.hpp"
+#include "topk_bins.hpp"
 #include "api.hpp"
 
 namespace stk {
@@ -79,12 +80,10 @@ __global__ __launch_bounds__(256) void k_indexer(IndexerArgs a) {
   }
 }
 
+// The score of `key` (lane p of its 16; every lane returns the sum).
 template <typename T, int H>
-__global__ __launch_bounds__(256) void k_indexer_v(IndexerArgs a) {
+__device__ __forceinline__ double indexer_score_v(const IndexerArgs& a, int key, int p, bool ok) {
   constexpr int D = 128;
-  const int key = blockIdx.x * (blockDim.x / kIdxLanes) + threadIdx.x / kIdxLanes;
-  const int p = threadIdx.x % kIdxLanes;
-  const bool ok = key < a.n;
   // this lane's 8 dims of the key row (one 16-byte load) and of every query
   const uint4 kr = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.ik) +
                                                    (size_t)(ok ? key : 0) * D + 8 * p);
@@ -117,18 +116,78 @@ __global__ __launch_bounds__(256) void k_indexer_v(IndexerArgs a) {
   double sc = 0.0;
 #pragma unroll
   for (int hh = 0; hh < H; ++hh) sc += relu_nan(key_tree(part[hh]));
-  sc = sc * a.inv;
+  return sc * a.inv;
+}
+
+template <typename T, int H>
+__global__ __launch_bounds__(256) void k_indexer_v(IndexerArgs a) {
+  const int key = blockIdx.x * (blockDim.x / kIdxLanes) + threadIdx.x / kIdxLanes;
+  const int p = threadIdx.x % kIdxLanes;
+  const bool ok = key < a.n;
+  const double sc = indexer_score_v<T, H>(a, key, p, ok);
   if (ok && p == 0) {
     if (a.scores) a.scores[key] = (float)sc;
     a.keys[key] = score_key(sc);
   }
 }
 
-// ids[r, :] = ids[0, :] for r in [1, rows)
+// ids[r, :] = ids[0, :] for r in [1, rows): x = column, rows from blockIdx.y
 __global__ __launch_bounds__(256) void k_rows_copy(int32_t* ids, int rows, int k) {
-  const int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (x >= (int64_t)(rows - 1) * k) return;
-  ids[k + x] = ids[x % k];
+  const int x = blockIdx.x * blockDim.x + threadIdx.x;
+  if (x >= k) return;
+  const int32_t v = ids[x];
+  for (int r = blockIdx.y + 1; r < rows; r += gridDim.y) ids[(size_t)r * k + x] = v;
+}
+
+// ---- the shared top-K and its rows
+//
+// The selection is one row of n keys, the same for every query head, so the
+// output is rows copies of topk IDs (393 KB at 48 rows of 2048).  T
+// workgroups of 1024 threads each rank the whole row (value bins,
+// topk_bins.hpp, KPT keys per thread), stage the ranked IDs in LDS and write
+// rows j, j + T, ... (16 bytes per store where the rows allow it): the rows
+// leave from T CUs at once, where one workgroup alone would take several
+// microseconds to store them, and no copy kernel follows.
+constexpr int kShThreads = 1024;
+constexpr int kShMaxN = 16 * kShThreads;   // KPT <= 16
+constexpr int kShMaxK = 8192;              // ranked IDs staged in LDS
+constexpr int kShRowsPer = 4;              // output rows per workgroup
+
+struct SharedTopkArgs {
+  const uint64_t* keys;
+  int n, k, rows;
+  int32_t* ids;   // [rows, k]
+  int vec;        // k % 4 == 0 and ids 16-byte aligned
+};
+
+template <int KPT>
+__global__ __launch_bounds__(kShThreads) void k_topk_shared(SharedTopkArgs a) {
+  __shared__ TopkBinsLds tb;
+  __shared__ int s_scan[kShThreads / STK_WAVE];
+  __shared__ __align__(16) int s_ids[kShMaxK];
+  const int tid = threadIdx.x;
+  uint64_t key[KPT];
+  topk_load<KPT>(a.keys, a.n, key);
+  const uint32_t flags = topk_bins_flags<KPT>(key, a.n, a.k, tb, [] {});
+  int total;
+  int pos = block_excl_scan1(__popc(flags), s_scan, &total);
+#pragma unroll
+  for (int i = 0; i < KPT; ++i)
+    if ((flags >> i) & 1u) s_ids[pos++] = tid * KPT + i;
+  __syncthreads();
+  if (a.vec) {
+    const int k4 = a.k / 4;
+    const int4* src = reinterpret_cast<const int4*>(s_ids);
+    for (int r = blockIdx.x; r < a.rows; r += gridDim.x) {
+      int4* o = reinterpret_cast<int4*>(a.ids + (size_t)r * a.k);
+      for (int x = tid; x < k4; x += kShThreads) o[x] = src[x];
+    }
+  } else {
+    for (int r = blockIdx.x; r < a.rows; r += gridDim.x) {
+      int32_t* o = a.ids + (size_t)r * a.k;
+      for (int x = tid; x < a.k; x += kShThreads) o[x] = s_ids[x];
+    }
+  }
 }
 
 }  // namespace stk
@@ -154,6 +213,22 @@ static int launch_indexer(const void* iq, const void* ik, int dtype, int h, int 
   else if (dtype == DT_F16) hipLaunchKernelGGL(k_indexer<f16s>, grid, block, 0, st, a);
   else hipLaunchKernelGGL(k_indexer<float>, grid, block, 0, st, a);
   return stk_check_launch("k_indexer");
+}
+
+// The shared top-K and its rows (k_topk_shared) for n <= 16384 and
+// topk <= 8192: 0 once launched, 1 when the shape is not covered.
+static int launch_topk_shared(const uint64_t* keys, int n, int topk, int rows, int32_t* ids,
+                              hipStream_t st) {
+  if (n > kShMaxN || topk > kShMaxK) return 1;
+  SharedTopkArgs a{keys, n, topk, rows, ids,
+                   topk % 4 == 0 && (reinterpret_cast<uintptr_t>(ids) & 15) == 0};
+  const dim3 grid((rows + kShRowsPer - 1) / kShRowsPer), block(kShThreads);
+  if (n <= kShThreads) hipLaunchKernelGGL(k_topk_shared<1>, grid, block, 0, st, a);
+  else if (n <= 2 * kShThreads) hipLaunchKernelGGL(k_topk_shared<2>, grid, block, 0, st, a);
+  else if (n <= 4 * kShThreads) hipLaunchKernelGGL(k_topk_shared<4>, grid, block, 0, st, a);
+  else if (n <= 8 * kShThreads) hipLaunchKernelGGL(k_topk_shared<8>, grid, block, 0, st, a);
+  else hipLaunchKernelGGL(k_topk_shared<16>, grid, block, 0, st, a);
+  return stk_check_launch("k_topk_shared");
 }
 
 extern "C" {
@@ -185,11 +260,12 @@ STK_API int stk_indexer_select(const void* iq, const void* ik, int dtype, int h,
   uint64_t* keys = static_cast<uint64_t*>(workspace);
   int rc = launch_indexer(iq, ik, dtype, h, n, d, scores, keys, st);
   if (rc) return rc;
+  rc = launch_topk_shared(keys, n, topk, rows, ids, st);
+  if (rc <= 0) return rc;   // launched, or an error
   rc = stk_launch_topk(keys, 1, n, topk, ids, st);
   if (rc || rows == 1) return rc;
-  const int64_t rest = (int64_t)(rows - 1) * topk;
-  hipLaunchKernelGGL(k_rows_copy, dim3((unsigned)((rest + 255) / 256)), dim3(256), 0, st, ids,
-                     rows, topk);
+  const dim3 grid((unsigned)((topk + 255) / 256), (unsigned)(rows - 1 < 65535 ? rows - 1 : 65535));
+  hipLaunchKernelGGL(k_rows_copy, grid, dim3(256), 0, st, ids, rows, topk);
   return stk_check_launch("k_rows_copy");
 }
 

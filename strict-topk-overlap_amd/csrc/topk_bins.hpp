@@ -10,13 +10,14 @@
 //   A  the row's range: per-wave max / min of the keys' high 32 bits (DPP),
 //      one barrier;
 //   B  a 1024-bin histogram, linear in the score value over that range
-//      (bin = (s - lo) * 1024 / (hi - lo) in FP32, clamped), and the sums of
-//      its 16-bin groups, two LDS atomics per key, one barrier;
+//      (bin = (s - lo) * 1024 / (hi - lo) in FP32, clamped), and, up to four
+//      keys per thread, the sums of its 16-bin groups: one or two LDS
+//      atomics per key, one barrier;
 //   C  every wave reads the whole histogram and finds the threshold bin t
 //      (keys above it, keys in it) with two DPP scans, so no barrier;
 //   D  if bin t is taken whole, done; otherwise its keys (a few) are listed
-//      in LDS, wave 0 ranks them by (key, -index) from registers and
-//      publishes the last one taken, two barriers.
+//      in LDS, wave 0 ranks them by (key, -index) and publishes the last one
+//      taken, two barriers.
 // The bin map is monotone non-decreasing in the key (every rounding step is
 // monotone, NaN keys, whose key is 0, go to bin 0), so the selection is the
 // exact one whatever the ranges and roundings are.  Rows whose range is
@@ -75,6 +76,11 @@ __device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], 
   const int nwaves = blockDim.x / STK_WAVE;
   const int base = threadIdx.x * KPT;
   const int lane = lane_id();
+  // Up to four keys per thread the 16-bin group sums are kept with LDS
+  // atomics during the histogram (phase C then reads one word per lane);
+  // with more keys those atomics, 64 words for the whole row, contend, and
+  // phase C sums its 16 bins from the histogram instead (four 16-byte reads).
+  constexpr bool kGroupAtomics = KPT <= 4;
   // ---- A: range of the finite-or-infinite, non-NaN keys (key 0 is NaN)
   uint32_t hmax = 0u, hmin = 0xffffffffu;
 #pragma unroll
@@ -116,13 +122,24 @@ __device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], 
       bin[i] = x >= (float)(kBins - 1) ? kBins - 1 : (x > 0.f ? (int)x : 0);
       if (base + i < n) {
         atomicAdd(&L.hist[bin[i]], 1);
-        atomicAdd(&L.grp[bin[i] >> 4], 1);
+        if constexpr (kGroupAtomics) atomicAdd(&L.grp[bin[i] >> 4], 1);
       }
     }
     __syncthreads();
     // ---- C: threshold bin, every wave alike.  Lane l takes the sum of bins
     // [kBins - 16 (l + 1), kBins - 16 l), lane 0 the top ones.
-    const int s = L.grp[kBins / 16 - 1 - lane];
+    int s;
+    if constexpr (kGroupAtomics) {
+      s = L.grp[kBins / 16 - 1 - lane];
+    } else {
+      const int4* h4 = reinterpret_cast<const int4*>(L.hist + kBins - 16 * (lane + 1));
+      s = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int4 v = h4[q];
+        s += (v.x + v.y) + (v.z + v.w);
+      }
+    }
     const int cum = wave_incl_scan_dpp(s);
     const int L16 = __ffsll((long long)__ballot(cum >= k)) - 1;
     const int above16 = __builtin_amdgcn_readlane(cum - s, L16);
@@ -155,17 +172,30 @@ __device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], 
       __syncthreads();
       // wave 0 ranks them (a loop over the candidates; every wave doing it
       // would run it once per wave on each SIMD) and publishes the last one
-      // taken through LDS
+      // taken through LDS.  With eight or more keys per thread (long rows,
+      // whose threshold bins can hold tens of candidates) candidate j is read
+      // by every lane from LDS, one broadcast read whose loads pipeline;
+      // otherwise it comes from lane j's registers, three lane reads per
+      // candidate, the form the fused steps' tails are tuned with.
       if (wave_id() == 0) {
         const uint64_t kc = lane < cnt ? L.ck[lane] : 0ull;
         const int ic = lane < cnt ? L.ci[lane] : 0x7fffffff;
         int rank = 0;
-        for (int j = 0; j < cnt; ++j) {
-          const uint32_t jh = (uint32_t)__builtin_amdgcn_readlane((int)(kc >> 32), j);
-          const uint32_t jl = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kc, j);
-          const int ij = __builtin_amdgcn_readlane(ic, j);
-          const uint64_t kj = ((uint64_t)jh << 32) | jl;
-          rank += (kj > kc) || (kj == kc && ij < ic);
+        if constexpr (KPT >= 8) {
+#pragma unroll 8
+          for (int j = 0; j < cnt; ++j) {
+            const uint64_t kj = L.ck[j];
+            const int ij = L.ci[j];
+            rank += (kj > kc) || (kj == kc && ij < ic);
+          }
+        } else {
+          for (int j = 0; j < cnt; ++j) {
+            const uint32_t jh = (uint32_t)__builtin_amdgcn_readlane((int)(kc >> 32), j);
+            const uint32_t jl = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kc, j);
+            const int ij = __builtin_amdgcn_readlane(ic, j);
+            const uint64_t kj = ((uint64_t)jh << 32) | jl;
+            rank += (kj > kc) || (kj == kc && ij < ic);
+          }
         }
         if (lane < cnt && rank == need - 1) {
           L.star_key = kc;

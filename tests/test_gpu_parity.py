@@ -188,6 +188,70 @@ def test_indexer_scores_and_shared_select(dtype, h, n, d, topk):
     assert ids.cpu().numpy().tolist() == O.indexer_select(C.f64(iq), C.f64(ik), topk, 6).tolist()
 
 
+def _indexer_inputs(dtype, n, seed, ties=True):
+    gen = torch.Generator().manual_seed(seed)
+    iq = torch.randn((4, 128), generator=gen).to(dtype)
+    ik = torch.randn((n, 128), generator=gen).to(dtype)
+    if ties and n >= 12:
+        t = min(40, n // 6)
+        ik[n // 3: n // 3 + t] = torch.randint(-1, 2, (t, 128), generator=gen).to(dtype)
+        ik[n // 2: n // 2 + t] = ik[n // 3: n // 3 + t]
+    return iq, ik
+
+
+@pytest.mark.parametrize("dtype,n,topk,rows", [
+    (torch.bfloat16, 8192, 2048, 48),    # c4's shape: 12 workgroups write 4 rows each
+    (torch.float16, 16384, 8192, 5),     # the largest shape of k_topk_shared (16 keys per thread)
+    (torch.bfloat16, 16384, 1, 1),
+    (torch.bfloat16, 1, 1, 1),
+    (torch.float16, 100, 37, 9),         # topk not a multiple of 4: 4-byte stores
+    (torch.bfloat16, 1025, 1025, 3),     # topk = n
+    (torch.bfloat16, 4099, 4000, 13),
+    (torch.float16, 20000, 300, 2),      # past 16384 keys: top-K, then the row copy
+    (torch.float16, 20000, 300, 70),
+])
+def test_shared_select_rows(dtype, n, topk, rows):
+    """The shared selection (benchmarks/selector_window.py:76-84): every
+    workgroup of k_topk_shared ranks the whole row and writes its share of
+    the rows; past its shapes the top-K writes row 0 and k_rows_copy the
+    rest.  IDs bit-exact against the oracle in every row, with exact ties in
+    the keys."""
+    from strict_topk import indexer
+    iq, ik = _indexer_inputs(dtype, n, n + topk)
+    ids = indexer.select_shared(iq.to(DEV), ik.to(DEV), topk, rows)
+    torch.cuda.synchronize()
+    assert ids.shape == (rows, topk)
+    assert ids.cpu().numpy().tolist() == \
+        O.indexer_select(C.f64(iq), C.f64(ik), topk, rows).tolist()
+
+
+def test_shared_select_in_a_graph():
+    """The selection captured in a graph and replayed while the indexer
+    query changes in place: every replay equals the eager call on the same
+    inputs, and the last one the oracle."""
+    from strict_topk import indexer
+    iq, ik = _indexer_inputs(torch.bfloat16, 8192, 7)
+    iqd, ikd = iq.to(DEV), ik.to(DEV)
+    indexer.select_shared(iqd, ikd, 2048, 48)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            out = indexer.select_shared(iqd, ikd, 2048, 48)
+    torch.cuda.current_stream().wait_stream(s)
+    gen = torch.Generator().manual_seed(11)
+    for _ in range(4):
+        iqd.copy_(torch.randn((4, 128), generator=gen).to(torch.bfloat16))
+        g.replay()
+        torch.cuda.synchronize()
+        eager = indexer.select_shared(iqd, ikd, 2048, 48)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    ref = O.indexer_select(C.f64(iqd.cpu()), C.f64(ik), 2048, 48)
+    assert out.cpu().numpy().tolist() == ref.tolist()
+
+
 def test_select_rejects_bad_k():
     from strict_topk import gqa
     q = torch.randn((4, 8), device=DEV)
