@@ -660,6 +660,39 @@ def test_hierarchical_exact_group_tile(dtype, b, g, shared, itype, sharp):
                   what + ("saved_shared", hits))
 
 
+@pytest.mark.parametrize("n", [300, 8192])
+def test_hier_shared_repair_slots(n):
+    """repair_saved_shared's hits use the prediction's state at the highest
+    slot holding the block (gqa_hierarchical.py:10-19, _match_ids).  The
+    predicted row repeats some selected blocks, and the state at each
+    repeat's lower slot is overwritten with a wrong one, which a lower-slot
+    match would merge; it also holds invalid IDs (-1, n + 3), which match
+    nothing."""
+    from strict_topk import gqa_hierarchical as impl
+    h, hkv, b, d, sa = 24, 2, 4, 128, 64
+    gen = torch.Generator().manual_seed(n)
+    q = torch.randn((h, d), generator=gen).to(torch.bfloat16)
+    k = torch.randn((hkv, n, b, d), generator=gen).to(torch.bfloat16)
+    v = torch.randn((hkv, n, b, d), generator=gen).to(torch.bfloat16)
+    a = torch.randperm(n, generator=gen)[:sa].to(torch.int32)
+    sel = a.expand(h, -1).contiguous()
+    others = torch.tensor([x for x in torch.randperm(n, generator=gen)[:200].tolist()
+                           if x not in set(a.tolist())][:12], dtype=torch.int32)
+    # slots: 0..7 the blocks a[0:8] (later repeated), then hits a[8:40],
+    # wrong blocks, invalid IDs, and the repeats of a[0:8] at the top
+    prow = torch.cat([a[:8], a[8:40], others, torch.tensor([-1, n + 3], dtype=torch.int32),
+                      a[:8]])
+    pred = prow.expand(h, -1).contiguous()
+    qn, kn, vn, an = np_(q, k, v, sel)
+    expected = O.attention(qn, kn, vn, an)
+    qd, kd, vd, sd, pd = dev(q, k, v, sel, pred)
+    st = impl.partials(qd, kd, vd, pd)
+    st.m[:, :8] = 50.0      # the lower copies: a merge of these would dominate
+    st.l[:, :8] = 1.0
+    st.u[:, :8] = 1000.0
+    check(impl.repair_saved_shared(qd, kd, vd, sd, pd, st), expected, ("shared slots", n))
+
+
 # ----------------------------------------------------------- graph replays
 def _capture(fn):
     s = torch.cuda.Stream()
