@@ -152,6 +152,7 @@ constexpr int kShThreads = 1024;
 constexpr int kShMaxN = 16 * kShThreads;   // KPT <= 16
 constexpr int kShMaxK = 8192;              // ranked IDs staged in LDS
 constexpr int kShRowsPer = 4;              // output rows per workgroup
+constexpr int kShMaxWgs = 64;              // past 256 rows a workgroup writes more than four
 
 struct SharedTopkArgs {
   const uint64_t* keys;
@@ -222,7 +223,8 @@ static int launch_topk_shared(const uint64_t* keys, int n, int topk, int rows, i
   if (n > kShMaxN || topk > kShMaxK) return 1;
   SharedTopkArgs a{keys, n, topk, rows, ids,
                    topk % 4 == 0 && (reinterpret_cast<uintptr_t>(ids) & 15) == 0};
-  const dim3 grid((rows + kShRowsPer - 1) / kShRowsPer), block(kShThreads);
+  const int wgs = (rows + kShRowsPer - 1) / kShRowsPer;
+  const dim3 grid(wgs < kShMaxWgs ? wgs : kShMaxWgs), block(kShThreads);
   if (n <= kShThreads) hipLaunchKernelGGL(k_topk_shared<1>, grid, block, 0, st, a);
   else if (n <= 2 * kShThreads) hipLaunchKernelGGL(k_topk_shared<2>, grid, block, 0, st, a);
   else if (n <= 4 * kShThreads) hipLaunchKernelGGL(k_topk_shared<4>, grid, block, 0, st, a);

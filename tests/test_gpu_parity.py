@@ -207,6 +207,7 @@ def _indexer_inputs(dtype, n, seed, ties=True):
     (torch.float16, 100, 37, 9),         # topk not a multiple of 4: 4-byte stores
     (torch.bfloat16, 1025, 1025, 3),     # topk = n
     (torch.bfloat16, 4099, 4000, 13),
+    (torch.bfloat16, 1000, 100, 300),    # 64 workgroups, some writing five rows
     (torch.float16, 20000, 300, 2),      # past 16384 keys: top-K, then the row copy
     (torch.float16, 20000, 300, 70),
 ])
