@@ -94,11 +94,21 @@ def _same(res, ref):
     (6, 2, 333, 128, 40, 0.6, torch.bfloat16, False),      # G = 3, N not a chunk multiple
     (4, 4, 64, 64, 64, 1.0, torch.float16, False),         # K = N: every block selected
     (4, 2, 1, 128, 1, 1.0, torch.bfloat16, False),         # one block
+    (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, "fp32"),   # c3 with the reference's FP32 bounds
+    (4, 4, 64, 64, 8, 0.75, torch.float16, "fp32"),        # c1 as the benchmark runs it
 ])
 def test_step1_matches_two_launches(hq, hkv, n, d, topk, overlap, dtype, union):
+    """The one launch against its two launches (bit-equal IDs, states and
+    outputs) and the oracle.  union: repair_union; "fp32": saved repair with
+    FP32 block bounds (the scorer's other load path)."""
     from strict_topk import step
+    fp32 = union == "fp32"
+    union = union is True
     host, (q, k, v, lo, hi, p), ref_ids = _inputs(hq, hkv, n, d, topk, overlap, dtype,
                                                   20261203 + n + hq)
+    if fp32:
+        lo, hi = host[3].cuda(), host[4].cuda()
+        assert lo.dtype == torch.float32
     assert _covered(q, k, topk, p)
     ref = _two_launches(q, k, v, lo, hi, p, topk, union)
     res = step.speculative_step(q, k, v, lo, hi, p, topk, union=union)
