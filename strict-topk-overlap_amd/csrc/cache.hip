@@ -117,35 +117,32 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
   for (int w = tid; w < words; w += kSwapThreads) need[w] = 0u;
   for (int x = tid; x < kMaxNeed; x += kSwapThreads) vict[x] = -1;
   if (tid == 0) nload = 0;
-  __syncthreads();
-  // the union of the group's selected blocks
-  const int32_t* gids = a.ids + (size_t)grp * a.g * a.k;
-  for (int x = tid; x < a.g * a.k; x += kSwapThreads) {
-    const int id = gids[x];
-    if (id >= 0 && id < n) atomicOr(&need[id >> 5], 1u << (id & 31));
-  }
-  __syncthreads();
   const int now = *a.clock;
   int32_t* trow = a.table + (size_t)grp * a.nb;
   const int32_t* hrow = a.host_table + (size_t)grp * a.nb;
   const size_t s0 = (size_t)grp * a.c;
-  // resident ones are stamped, missing ones listed; a block with no valid
-  // host page is neither (it stays non-resident: the tail gives it the
-  // empty state, as the paged steps do for an invalid page)
-  for (int w = tid; w < words; w += kSwapThreads) {
-    uint32_t bits = need[w];
-    while (bits) {
-      const int j = 32 * w + __ffs(bits) - 1;
-      bits &= bits - 1u;
-      const int s = trow[j];
+  __syncthreads();
+  // the union of the group's selected blocks: the thread that sets a block's
+  // bit handles it, its slot and host page requested together (one round
+  // trip for the whole union).  Resident blocks are stamped, missing ones
+  // listed; a block with no valid host page is neither (it stays
+  // non-resident: the tail gives it the empty state, as the paged steps do
+  // for an invalid page).
+  const int32_t* gids = a.ids + (size_t)grp * a.g * a.k;
+  for (int x = tid; x < a.g * a.k; x += kSwapThreads) {
+    const int id = gids[x];
+    const bool in = id >= 0 && id < n;
+    const uint32_t bit = 1u << (in ? (id & 31) : 0);
+    const bool first = in && !(atomicOr(&need[in ? id >> 5 : 0], in ? bit : 0u) & bit);
+    const int j = first ? id : 0;
+    const int s = trow[j];
+    const int hp = hrow[j];
+    if (first) {
       if (s >= 0) {
         a.slot_stamp[s] = now;
-      } else {
-        const int hp = hrow[j];
-        if (hp >= 0 && hp < a.host_pages) {
-          const int x = atomicAdd(&nload, 1);
-          if (x < kMaxNeed) loads[x] = j;
-        }
+      } else if (hp >= 0 && hp < a.host_pages) {
+        const int y = atomicAdd(&nload, 1);
+        if (y < kMaxNeed) loads[y] = j;
       }
     }
   }
