@@ -107,6 +107,7 @@ struct SwapArgs {
 __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
   __shared__ uint32_t need[kTailMapN / 32];
   __shared__ int loads[kMaxNeed];
+  __shared__ int loads_hp[kMaxNeed];   // the listed blocks' host pages
   __shared__ int vict[kMaxNeed];
   __shared__ TopkLds tl;
   __shared__ int nload;
@@ -121,6 +122,15 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
   int32_t* trow = a.table + (size_t)grp * a.nb;
   const int32_t* hrow = a.host_table + (size_t)grp * a.nb;
   const size_t s0 = (size_t)grp * a.c;
+  // this thread's slots' blocks and stamps, for the victim keys below (the
+  // stamps written in between belong to needed slots, whose keys ignore them)
+  int sblk[kSlotsPerThread], sstamp[kSlotsPerThread];
+#pragma unroll
+  for (int i = 0; i < kSlotsPerThread; ++i) {
+    const int sl = tid * kSlotsPerThread + i;
+    sblk[i] = sl < a.c ? a.slot_block[s0 + sl] : -1;
+    sstamp[i] = sl < a.c ? a.slot_stamp[s0 + sl] : 0;
+  }
   __syncthreads();
   // the union of the group's selected blocks: the thread that sets a block's
   // bit handles it, its slot and host page requested together (one round
@@ -142,7 +152,10 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
         a.slot_stamp[s] = now;
       } else if (hp >= 0 && hp < a.host_pages) {
         const int y = atomicAdd(&nload, 1);
-        if (y < kMaxNeed) loads[y] = j;
+        if (y < kMaxNeed) {
+          loads[y] = j;
+          loads_hp[y] = hp;
+        }
       }
     }
   }
@@ -157,15 +170,15 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
 #pragma unroll
   for (int i = 0; i < kSlotsPerThread; ++i) {
     const int s = tid * kSlotsPerThread + i;
-    const int blk = s < a.c ? a.slot_block[s0 + s] : -1;
+    const int blk = sblk[i];
     const bool busy = blk >= 0 && blk < a.nb && ((need[blk >> 5] >> (blk & 31)) & 1u);
-    const uint64_t stamp = blk < 0 ? 0ull : (uint64_t)(uint32_t)(a.slot_stamp[s0 + s] + 1);
+    const uint64_t stamp = blk < 0 ? 0ull : (uint64_t)(uint32_t)(sstamp[i] + 1);
     vkey[i] = busy ? 0ull : ~((stamp << 20) | (uint64_t)s);
   }
   topk_select_keys<kSlotsPerThread>(vkey, a.c, nl, tl, [&](int pos, int s, int i) {
     if (vkey[i] == 0ull) return;   // a needed slot (C >= G * K rules this out)
     const int j = loads[pos];
-    const int old = a.slot_block[s0 + s];
+    const int old = sblk[i];
     if (old >= 0 && old < a.nb) trow[old] = -1;
     a.slot_block[s0 + s] = j;
     a.slot_stamp[s0 + s] = now;
@@ -180,7 +193,7 @@ __global__ __launch_bounds__(kSwapThreads) void k_swap_in(SwapArgs a) {
   if (tid == 0) ncopy = 0;
   __syncthreads();
   for (int x = tid; x < nl; x += kSwapThreads) {
-    const int hp = hrow[loads[x]];
+    const int hp = loads_hp[x];
     const bool ok = hp >= 0 && hp < a.host_pages && vict[x] >= 0;
     a.src[(size_t)grp * kMaxNeed + x] = ok ? hp : -1;
     a.dst[(size_t)grp * kMaxNeed + x] = ok ? vict[x] : -1;
