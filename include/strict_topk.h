@@ -251,8 +251,9 @@ int stk_step_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk
 /* The full speculative decode step of benchmarks/run_benchmark.py:99-118
  * (overlap_run: gqa.select_blocks || gqa.partials on the predicted blocks,
  * then gqa_light.repair_saved_light / gqa.repair_saved, or gqa.repair_union
- * with union_mode 1) on one stream: one launch where stk_step1_supported
- * says so, otherwise two launches (a grid whose workgroups either score
+ * with union_mode 1) on one stream: one workgroup per query head where
+ * stk_step_small_supported says so, else one launch where
+ * stk_step1_supported says so, otherwise two launches (a grid whose workgroups either score
  * blocks or compute the predicted blocks' states, then one workgroup per
  * query head doing the exact top-K and the repair).  Outputs:
  * selected[Hq,topk] int32 (ascending IDs, as stk_select_blocks), the
@@ -281,6 +282,21 @@ int stk_speculative_step(const void* q, const void* k, const void* v, int dtype,
  * (benchmarks/run_benchmark.py:99-118). */
 int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
                         int pred_dtype);
+
+/* 1 when stk_speculative_step (and stk_speculative_step_noalloc) run the
+ * shape in one workgroup per query head, with no hand-off between
+ * workgroups: bf16/fp16, B = 32, D in {64, 128}, N <= 64, TOPK and SP in
+ * [1, 8], int32 predicted IDs, bounds FP32 or of the K/V type (16-byte
+ * aligned pointers assumed; others take the paths above).  Such a head's
+ * bounds, then its misses' tiles, are two dependent memory round trips of
+ * its own workgroup; its predicted tiles travel beside them.  The selected
+ * IDs are those of every other path (the same FP64 scores); the states and
+ * the output equal the oracle's within the step's tolerance, and since a
+ * miss is merged as two 16-token halves their bits may differ from the
+ * other paths'.  No reference counterpart beyond the step it computes
+ * (benchmarks/run_benchmark.py:99-118). */
+int stk_step_small_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
+                             int pred_dtype, int bounds_dtype);
 
 /* Slots of the current device whose one-launch step ever timed out waiting
  * for a flag (each wait gives up after 20 ms, so every launch ends, and the

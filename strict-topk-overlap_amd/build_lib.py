@@ -24,7 +24,7 @@ ARCH = "gfx950"
 SOURCES = ["api.cpp", "states.hip", "select.hip", "repair.hip", "signed.hip", "hier.hip", "sstep.hip",
            "bounds.hip", "indexer.hip", "paged.hip", "step.hip", "tail_dense.hip", "front_pg.hip",
            "tail_pg.hip", "stail_pg.hip", "cache.hip", "srepair.hip",
-           "hier_mfma.hip", "step1.hip", "repair_fast.hip"]
+           "hier_mfma.hip", "step1.hip", "repair_fast.hip", "step_small.hip"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",

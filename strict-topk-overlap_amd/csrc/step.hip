@@ -22,6 +22,7 @@
 #include <mutex>
 
 #include "step1.hpp"
+#include "step_small.hpp"
 
 namespace stk {
 
@@ -198,6 +199,11 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
   t.p = static_cast<const int32_t*>(predicted); t.sp = sp;
   t.pm = m; t.pl = l; t.pu = u; t.uni = union_mode ? 1 : 0; t.out = out;
   hipStream_t st = (hipStream_t)stream;
+  if (front && tail && small_covers(dtype, hq, hkv, n, b, d, topk, sp, bounds_dtype, align)) {
+    // small shapes: one workgroup per query head, no hand-off
+    SmallArgs sa{q, k, v, lo, hi, hq, hkv, n, d, t.p, sp, topk, t.uni, selected, m, l, u, out};
+    return launch_small(dtype, sa, bounds_dtype, st);
+  }
   if (front && tail && step1_covers(dtype, hq, hkv, b, d, s)) {
     // one launch, its flags in this stream's slot (none free: two launches)
     uint32_t* ctl = nullptr;
@@ -233,6 +239,14 @@ STK_API int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d,
   if (plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, 0, &s)) return 0;
   return step1_covers(dtype, hq, hkv, b, d, s) &&
          step1_ctl_words(hq, n, sp) < kCtlSlotWords ? 1 : 0;   // the last word counts time-outs
+}
+
+STK_API int stk_step_small_supported(int dtype, int hq, int hkv, int n, int b, int d, int topk,
+                                     int sp, int pred_dtype, int bounds_dtype) {
+  StepShape s{};
+  if (hq <= 0 || hkv <= 0 || hq % hkv) return 0;
+  if (plan_step(dtype, hq, hkv, n, b, d, topk, sp, pred_dtype, 0, &s)) return 0;
+  return small_covers(dtype, hq, hkv, n, b, d, topk, sp, bounds_dtype, 0) ? 1 : 0;
 }
 
 STK_API int stk_step1_timeouts(void) {

@@ -1,0 +1,359 @@
+// The speculative step for small shapes in one launch, one workgroup per
+// query head and no hand-off between workgroups.
+//
+// The reference's step (benchmarks/run_benchmark.py:99-118, overlap_run:
+// selector.select_blocks || kernels.speculate('saved'), joined, then
+// kernels.repair or gqa.repair_union) is, per query head, the bound scores of
+// its KV head's blocks (selector.py:8-20), their top-K, the predicted blocks'
+// softmax states (kernels.py:42-71) and the strict repair's LSE merge
+// (kernels.py:120-247).  When a head has at most 64 blocks and at most eight
+// selected and eight predicted rows, one workgroup of sixteen waves holds all
+// of it, in two roles that meet only in LDS:
+//   * selection, waves 0..7 (launched first): wave 0 requests the predicted
+//     IDs ahead of everything and publishes them as soon as they arrive;
+//     every wave requests the bounds of eight blocks and the query, scores
+//     them in FP64, publishes the keys, adds its partial ranks (its eight
+//     blocks against all 64), and once every rank is in, each wave finds the
+//     selection and the misses by ballot and requests its miss half-tiles
+//     (a miss is split in two 16-token halves, so up to sixteen halves run
+//     on eight waves); wave 0 writes the IDs while those tiles travel;
+//   * prediction, waves 8..15: wave 8 + p waits for the IDs, requests slot
+//     p's tile and computes and stores its softmax state.
+// The merge after the one barrier reads every row (predicted states, miss
+// halves) from LDS.  Critical path: two dependent memory round trips (the
+// bounds, then the miss tiles) and two LDS hand-offs (keys, ranks).  The
+// one-launch step for larger shapes (k_step1) hands keys and states between
+// workgroups through flags in memory, which costs more than the work here.
+//
+// Contracts as everywhere in the library: scores in FP64 in the fixed order
+// (lane c of 16 sums dims 64 j + 4 c + t, j then t ascending, then the xor
+// butterfly 8, 4, 2, 1; oracle bound_scores), keys order-preserving (NaN
+// lowest), the top-K's ties toward the lower block index and IDs ascending;
+// saved repair: a predicted slot counts when its block is selected and it is
+// the highest slot holding that block; union: every predicted slot with a
+// valid block; selected blocks in no predicted slot are computed from K/V.
+#include "score.hpp"
+#include "tile2.hpp"
+#include "step_small.hpp"
+
+namespace stk {
+
+namespace {
+
+// Intra-workgroup hand-offs between waves through LDS counters.  The fences
+// order LDS only: a wave's global loads in flight (a tile it has requested)
+// do not hold back its signal.  A waiting wave sleeps between its reads.
+__device__ __forceinline__ void lds_signal(int* c) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  if (lane_id() == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_wait(int* c, int v) {
+  while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < v)
+    __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Keeps loaded values live at one point, so that the compiler sinks none of
+// their LDS reads into a branch (a select on a loaded value can otherwise
+// become a branch around the read) and issues them all before the first use.
+template <int N>
+__device__ __forceinline__ void pin(float (&x)[N]) {
+  static_assert(N % 8 == 0, "groups of eight");
+#pragma unroll
+  for (int i = 0; i < N; i += 8)
+    asm volatile("" : "+v"(x[i]), "+v"(x[i + 1]), "+v"(x[i + 2]), "+v"(x[i + 3]),
+                 "+v"(x[i + 4]), "+v"(x[i + 5]), "+v"(x[i + 6]), "+v"(x[i + 7]));
+}
+
+template <typename T, int NCH, bool LB16>
+__global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
+  using TT = TokTile<T, NCH, 2>;   // 32 tokens: one block per chunk
+  using TH = TokTile<T, NCH, 1>;   // 16 tokens: half a block (the misses)
+  constexpr int D = TT::D;
+  constexpr int P = D / 64;         // 64-dim scoring passes
+  constexpr int SW = kSmallRoleWaves;
+  constexpr int STEPS = kSmallMaxN / (SW * 4);   // 4-block scoring steps per wave
+  constexpr int RM = 2 * kSmallMaxRows;          // the misses' half-block rows
+  constexpr int R = kSmallMaxRows + RM;          // merged rows: predicted | miss halves
+  static_assert(R % 8 == 0 && TH::QW == TT::QW && TH::DPL == TT::DPL,
+                "rows read as 4-wide vectors; the half tile shares the query layout");
+  __shared__ uint64_t s_key[kSmallMaxN];
+  __shared__ int s_rank[kSmallMaxN];
+  __shared__ int s_pred[kSmallMaxN];   // 1: some predicted slot holds the block
+  __shared__ int s_pid[kSmallMaxRows];
+  __shared__ __align__(16) int s_on[R];
+  __shared__ int s_kdone, s_rdone, s_pdone;
+  __shared__ __align__(16) float s_m[R];
+  __shared__ __align__(16) float s_l[R];
+  __shared__ __align__(16) float s_u[R][D];
+  const int h = blockIdx.x, tid = threadIdx.x, w = wave_id(), lane = lane_id();
+  const int n = a.n, sp = a.sp, K = a.k;
+  const int kv = h / (a.hq / a.hkv);
+  const T* K_ = reinterpret_cast<const T*>(a.kk);
+  const T* V_ = reinterpret_cast<const T*>(a.vv);
+  const size_t blk_elems = (size_t)32 * D;
+  const T* qrow = reinterpret_cast<const T*>(a.q) + (size_t)h * D;
+  const float scale = 1.0f / sqrtf((float)D);
+  if (tid < kSmallMaxN) {
+    s_rank[tid] = 0;
+    s_pred[tid] = 0;
+  }
+  if (tid < R) s_on[tid] = 0;
+  if (tid == 0) s_kdone = s_rdone = s_pdone = 0;
+  __syncthreads();
+  TT t;
+  t.init();
+  uint32_t qw[TT::QW];
+  if (w >= SW) {
+    // ---- predicted role, wave SW + ps (ps < SP): slot ps's ID (published
+    // by wave 0), then its tile, then its state (an invalid ID reads block 0
+    // and keeps the empty state)
+    const int ps = w - SW;
+    if (ps < sp) {
+      t.load_q(qrow, qw);
+      lds_wait(&s_pdone, 1);
+      const int pid = s_pid[ps];
+      const bool pvalid = pid >= 0;
+      uint32_t kw[2][TT::QW], vw[TT::CH][TT::VW];
+      const size_t off = ((size_t)kv * n + (pvalid ? pid : 0)) * blk_elems;
+      t.load(K_ + off, V_ + off, 0, kw, vw);
+      float m = -INFINITY, l = 0.f, acc[TT::DPL];
+#pragma unroll
+      for (int e = 0; e < TT::DPL; ++e) acc[e] = 0.f;
+      if (pvalid) t.template update<false, false>(qw, kw, vw, 0, 32, scale, m, l, acc);
+      const size_t row = (size_t)h * sp + ps;
+      if (lane == 0) {
+        a.m[row] = m;
+        a.l[row] = l;
+        s_m[ps] = m;
+        s_l[ps] = l;
+      }
+      t.store(a.u + row * D, acc);
+      t.store(s_u[ps], acc);
+    }
+  } else {
+    // ---- selection role, wave sw: the bound scores of its blocks (every
+    // load issued before any arithmetic).  Lane l16 of a 16-lane row is
+    // logical lane c of the summation order (score_lane), so that the row
+    // sum is DPP moves only
+    const int sw = w;
+    const int l16 = lane & 15, c = score_lane(l16), sub = lane >> 4;
+    // wave 0 requests the predicted IDs first (the predicted role waits for
+    // them; the bounds behind them take longer to arrive)
+    int pidv = -1;
+    if (sw == 0 && lane < sp) pidv = a.p[(size_t)h * sp + lane];
+    uint2 q2[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) q2[j] = *reinterpret_cast<const uint2*>(qrow + 64 * j + 4 * c);
+    using BV = std::conditional_t<LB16, uint2, float4>;
+    BV lb[STEPS][P], hb[STEPS][P];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int nb = (s * SW + sw) * 4 + sub;
+      const size_t row = ((size_t)kv * n + (nb < n ? nb : 0)) * D;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        const size_t e = row + 64 * j + 4 * c;
+        if constexpr (LB16) {
+          lb[s][j] = *reinterpret_cast<const uint2*>(reinterpret_cast<const T*>(a.lo) + e);
+          hb[s][j] = *reinterpret_cast<const uint2*>(reinterpret_cast<const T*>(a.hi) + e);
+        } else {
+          lb[s][j] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.lo) + e);
+          hb[s][j] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.hi) + e);
+        }
+      }
+    }
+    t.load_q(qrow, qw);
+    __builtin_amdgcn_sched_barrier(0);
+    if (sw == 0) {
+      const bool ok = lane < sp && pidv >= 0 && pidv < n;
+      if (lane < kSmallMaxRows) s_pid[lane] = ok ? pidv : -1;
+      if (ok) s_pred[pidv] = 1;
+      lds_signal(&s_pdone);
+    }
+    static_assert(STEPS == 2, "two scoring steps: row lanes 0..7 and 8..15 hold their sums");
+    double acc[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      acc[s] = 0.0;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        float qs[4], lv[4], hv[4];
+        Unpack<T>::run(q2[j].x, qs);
+        Unpack<T>::run(q2[j].y, qs + 2);
+        if constexpr (LB16) {
+          Unpack<T>::run(lb[s][j].x, lv);
+          Unpack<T>::run(lb[s][j].y, lv + 2);
+          Unpack<T>::run(hb[s][j].x, hv);
+          Unpack<T>::run(hb[s][j].y, hv + 2);
+        } else {
+          lv[0] = lb[s][j].x; lv[1] = lb[s][j].y; lv[2] = lb[s][j].z; lv[3] = lb[s][j].w;
+          hv[0] = hb[s][j].x; hv[1] = hb[s][j].y; hv[2] = hb[s][j].z; hv[3] = hb[s][j].w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float b = qs[e] >= 0.f ? hv[e] : lv[e];   // lo where q < 0 or NaN
+          acc[s] = fma((double)qs[e], (double)b, acc[s]);
+        }
+      }
+    }
+    // the xor butterfly 8, 4, 2, 1 of both steps at once: row lanes 0..7
+    // hold step 0's sum, lanes 8..15 step 1's.  Blocks past N get key 0,
+    // below every score's key or equal to a NaN score's and at a higher
+    // index, so they never outrank a block
+    const double sum = score_rowsum<STEPS>(acc, l16);
+    if ((l16 & 7) == 0) {
+      const int nb = ((l16 >> 3) * SW + sw) * 4 + sub;
+      s_key[nb] = nb < n ? score_key(sum) : 0ull;
+    }
+    lds_signal(&s_kdone);
+    lds_wait(&s_kdone, SW);
+    // ---- ranks by (key, -index): wave sw compares every block (lane i)
+    // with blocks 8 sw .. 8 sw + 7 and adds its count
+    const uint64_t ki = s_key[lane];
+    int part = 0;
+#pragma unroll
+    for (int x = 0; x < kSmallMaxN / SW; ++x) {
+      const int j = sw * (kSmallMaxN / SW) + x;
+      const uint64_t kj = s_key[j];
+      part += (kj > ki) || (kj == ki && j < lane);
+    }
+    if (part) __hip_atomic_fetch_add(&s_rank[lane], part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    lds_signal(&s_rdone);
+    lds_wait(&s_rdone, SW);
+    // ---- every selection wave: the selection and the misses (selected, in
+    // no predicted slot) in ascending order.  Miss i is two tasks, its
+    // tokens 0..15 (task 2 i) and 16..31 (task 2 i + 1); wave sw takes tasks
+    // sw and sw + 8, both halves of the same parity
+    const int rk = s_rank[lane], pr = s_pred[lane];   // both read at once
+    const bool sel = (lane < n) & (rk < K);
+    const uint64_t selm = __ballot(sel);
+    const uint64_t mm = __ballot(sel & (pr == 0));
+    const int nmiss = __popcll(mm);
+    const int nt = 2 * nmiss;
+    const int t0 = 16 * (sw & 1);
+    const bool has0 = sw < nt, has1 = sw + SW < nt;
+    uint64_t mk = mm;   // miss sw / 2 at the lowest set bit, then miss sw / 2 + 4
+    for (int i = 0; i < (sw >> 1); ++i) mk &= mk - 1;
+    const int b0 = has0 ? __builtin_ctzll(mk) : 0;
+    for (int i = 0; i < SW / 2; ++i) mk &= mk - 1;
+    const int b1 = has1 ? __builtin_ctzll(mk) : 0;
+    TH th;
+    th.init();
+    uint32_t kw0[1][TH::QW], vw0[TH::CH][TH::VW], kw1[1][TH::QW], vw1[TH::CH][TH::VW];
+    if (has0) {
+      const size_t off = ((size_t)kv * n + b0) * blk_elems;
+      th.load(K_ + off, V_ + off, t0, kw0, vw0);
+    }
+    if (has1) {
+      const size_t off = ((size_t)kv * n + b1) * blk_elems;
+      th.load(K_ + off, V_ + off, t0, kw1, vw1);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // both halves requested before either is used
+    if (sw == 0) {
+      // while the tiles travel: the IDs out, and the rows the merge takes.
+      // Predicted slot p counts when valid and (union, or its block is
+      // selected and p is the highest slot holding it)
+      const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+      if (sel) a.ids[(size_t)h * K + __popcll(selm & below)] = lane;
+      if (lane < sp) {
+        const int b = s_pid[lane];
+        bool top = true;
+#pragma unroll
+        for (int p = 0; p < kSmallMaxRows; ++p)
+          top = top && !(p > lane && p < sp && s_pid[p] == b);
+        const bool bsel = b >= 0 && ((selm >> b) & 1ull);
+        s_on[lane] = b >= 0 && (a.uni != 0 || (bsel && top));
+      } else if (lane >= kSmallMaxRows && lane < kSmallMaxRows + nt) {
+        s_on[lane] = 1;
+      }
+    }
+    // the halves' states (row 8 + task)
+    if (has0) {
+      float m = -INFINITY, l = 0.f, acc[TH::DPL];
+#pragma unroll
+      for (int e = 0; e < TH::DPL; ++e) acc[e] = 0.f;
+      th.template update<false, false>(qw, kw0, vw0, t0, 32, scale, m, l, acc);
+      if (lane == 0) {
+        s_m[kSmallMaxRows + sw] = m;
+        s_l[kSmallMaxRows + sw] = l;
+      }
+      th.store(s_u[kSmallMaxRows + sw], acc);
+    }
+    if (has1) {
+      float m = -INFINITY, l = 0.f, acc[TH::DPL];
+#pragma unroll
+      for (int e = 0; e < TH::DPL; ++e) acc[e] = 0.f;
+      th.template update<false, false>(qw, kw1, vw1, t0, 32, scale, m, l, acc);
+      if (lane == 0) {
+        s_m[kSmallMaxRows + SW + sw] = m;
+        s_l[kSmallMaxRows + SW + sw] = l;
+      }
+      th.store(s_u[kSmallMaxRows + SW + sw], acc);
+    }
+  }
+  __syncthreads();
+  // ---- the LSE merge of the rows taken, by the selection role's first waves
+  // (the predicted role's waves may still have global stores in flight).
+  // Every row is read; rows not taken (LDS this launch never wrote) are left
+  // out by selection, not by a zero weight
+  const int dm = tid;
+  if (dm < D) {
+    float mr[R], ur[R], lr[R];
+    int on[R];
+#pragma unroll
+    for (int i = 0; i < R / 4; ++i) {
+      const float4 m4 = reinterpret_cast<const float4*>(s_m)[i];
+      const float4 l4 = reinterpret_cast<const float4*>(s_l)[i];
+      const int4 o4 = reinterpret_cast<const int4*>(s_on)[i];
+      mr[4 * i] = m4.x; mr[4 * i + 1] = m4.y; mr[4 * i + 2] = m4.z; mr[4 * i + 3] = m4.w;
+      lr[4 * i] = l4.x; lr[4 * i + 1] = l4.y; lr[4 * i + 2] = l4.z; lr[4 * i + 3] = l4.w;
+      on[4 * i] = o4.x; on[4 * i + 1] = o4.y; on[4 * i + 2] = o4.z; on[4 * i + 3] = o4.w;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) ur[r] = s_u[r][dm];
+    pin(ur);
+    float M = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < R; ++r) M = on[r] ? fmaxf(M, mr[r]) : M;
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float f = wexp(mr[r], M);
+      num = on[r] ? num + f * ur[r] : num;
+      den = on[r] ? den + f * lr[r] : den;
+    }
+    a.out[(size_t)h * D + dm] = num / den;
+  }
+}
+
+}  // namespace
+
+bool small_covers(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,
+                  int bounds_dtype, uintptr_t align) {
+  return (dtype == DT_BF16 || dtype == DT_F16) && hq % hkv == 0 && b == 32 &&
+         (d == 64 || d == 128) && n >= 1 && n <= kSmallMaxN && topk >= 1 &&
+         topk <= kSmallMaxRows && topk <= n && sp >= 1 && sp <= kSmallMaxRows &&
+         stk_bounds_ok(dtype, bounds_dtype) && (align & 15) == 0;
+}
+
+int launch_small(int dtype, const SmallArgs& a, int bounds_dtype, hipStream_t st) {
+  const dim3 grid(a.hq), block(kSmallThreads);
+  const bool lb16 = bounds_dtype != 0;
+#define STK_SMALL(T_, NCH_)                                                         \
+  do {                                                                              \
+    if (lb16) hipLaunchKernelGGL((k_step_small<T_, NCH_, true>), grid, block, 0, st, a); \
+    else hipLaunchKernelGGL((k_step_small<T_, NCH_, false>), grid, block, 0, st, a);     \
+  } while (0)
+  if (dtype == DT_BF16) {
+    if (a.d == 64) STK_SMALL(bf16s, 2);
+    else STK_SMALL(bf16s, 4);
+  } else {
+    if (a.d == 64) STK_SMALL(f16s, 2);
+    else STK_SMALL(f16s, 4);
+  }
+#undef STK_SMALL
+  return stk_check_launch("k_step_small");
+}
+
+}  // namespace stk

@@ -60,6 +60,7 @@ _SIGS = {
     "stk_speculative_step": (I, [P, P, P, I, I, I, I, I, I, P, P, I, I, P, I, I, I,
                                  P, P, P, P, P, P, Z, P]),
     "stk_step1_supported": (I, [I, I, I, I, I, I, I, I, I]),
+    "stk_step_small_supported": (I, [I, I, I, I, I, I, I, I, I, I]),
     "stk_step1_timeouts": (I, []),
     "stk_step1_test_hook": (I, [ctypes.c_ulonglong, I]),
     "stk_step_noalloc_max_keys": (Z, []),

@@ -73,6 +73,23 @@ def test_one_launch_support_matches_the_flag_slot(lib):
     assert L.stk_step_supported(2, 128, 32, 4096, 32, 64, 64, 64, 0) == 1
 
 
+def test_small_step_support_bounds(lib):
+    """stk_step_small_supported covers N <= 64, K and SP in [1, 8], B = 32,
+    D in {64, 128}, bf16 / fp16 K/V with FP32 or same-type bounds, int32
+    predictions, and nothing the fused step itself rejects."""
+    L = lib.lib()
+    ok = (2, 8, 2, 64, 32, 128, 8, 8, 0, 0)            # bf16, FP32 bounds
+    assert L.stk_step_small_supported(*ok) == 1
+    assert L.stk_step_small_supported(1, 4, 4, 1, 32, 64, 1, 1, 0, 1) == 1   # fp16, fp16 bounds
+    for i, bad in ((3, 65), (6, 9), (6, 0), (7, 9), (7, 0), (4, 64), (5, 256), (8, 1)):
+        args = list(ok)
+        args[i] = bad
+        assert L.stk_step_small_supported(*args) == 0, (i, bad)
+    assert L.stk_step_small_supported(2, 8, 2, 8, 32, 128, 9, 8, 0, 0) == 0    # K > N
+    assert L.stk_step_small_supported(2, 8, 3, 64, 32, 128, 8, 8, 0, 0) == 0   # Hq % Hkv
+    assert L.stk_step_small_supported(0, 8, 2, 64, 32, 128, 8, 8, 0, 0) == 0   # fp32 K/V
+
+
 def test_noalloc_step_rejects_oversized_key_rows(lib):
     """The allocation-free step refuses Hq * N above its fixed scratch before
     touching a device."""

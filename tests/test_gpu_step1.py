@@ -68,6 +68,15 @@ def _covered(q, k, topk, p):
                                           p.shape[1], _lib.id_code(p)) == 1
 
 
+def _small(q, k, topk, p, lo):
+    """True when the step would run in one workgroup per head instead."""
+    from strict_topk import _lib
+    hkv, n, b, d = k.shape
+    return _lib.lib().stk_step_small_supported(_lib.dtype_code(q), q.shape[0], hkv, n, b, d,
+                                               topk, p.shape[1], _lib.id_code(p),
+                                               _lib.bounds_code(lo, q)) == 1
+
+
 def _timeouts():
     from strict_topk import _lib
     torch.cuda.synchronize()
@@ -88,14 +97,14 @@ def _same(res, ref):
     (32, 8, 2048, 128, 64, 0.75, torch.bfloat16, False),   # c3, 16 misses per head
     (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, True),     # c3, repair_union
     (16, 8, 512, 128, 64, 0.9, torch.bfloat16, False),     # c2 (G = 2)
-    (4, 4, 64, 64, 8, 0.75, torch.float16, False),         # c1 (G = 1, D = 64)
+    (4, 4, 65, 64, 8, 0.75, torch.float16, False),         # c1-like (G = 1, D = 64), one block
+                                                           # past the one-workgroup-per-head shapes
     (12, 3, 4000, 64, 50, 0.5, torch.float16, False),      # eight keys per tail thread
     (8, 8, 7000, 128, 16, 0.9, torch.bfloat16, False),     # sixteen keys per tail thread
     (6, 2, 333, 128, 40, 0.6, torch.bfloat16, False),      # G = 3, N not a chunk multiple
     (4, 4, 64, 64, 64, 1.0, torch.float16, False),         # K = N: every block selected
-    (4, 2, 1, 128, 1, 1.0, torch.bfloat16, False),         # one block
     (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, "fp32"),   # c3 with the reference's FP32 bounds
-    (4, 4, 64, 64, 8, 0.75, torch.float16, "fp32"),        # c1 as the benchmark runs it
+    (4, 4, 65, 64, 8, 0.75, torch.float16, "fp32"),        # c1-like with FP32 bounds
 ])
 def test_step1_matches_two_launches(hq, hkv, n, d, topk, overlap, dtype, union):
     """The one launch against its two launches (bit-equal IDs, states and
@@ -109,7 +118,7 @@ def test_step1_matches_two_launches(hq, hkv, n, d, topk, overlap, dtype, union):
     if fp32:
         lo, hi = host[3].cuda(), host[4].cuda()
         assert lo.dtype == torch.float32
-    assert _covered(q, k, topk, p)
+    assert _covered(q, k, topk, p) and not _small(q, k, topk, p, lo)
     ref = _two_launches(q, k, v, lo, hi, p, topk, union)
     res = step.speculative_step(q, k, v, lo, hi, p, topk, union=union)
     assert res.selected.cpu().numpy().tolist() == ref_ids.tolist()
@@ -162,7 +171,7 @@ def test_step1_two_streams_and_shape_changes():
     from strict_topk import step
     a = _inputs(32, 8, 2048, 128, 64, 0.9, torch.bfloat16, 20261104)[1]
     b = _inputs(16, 8, 512, 128, 64, 0.75, torch.bfloat16, 20261105)[1]
-    c = _inputs(4, 4, 64, 64, 8, 0.75, torch.float16, 20261106)[1]
+    c = _inputs(4, 4, 65, 64, 8, 0.75, torch.float16, 20261106)[1]
     refs = {name: _two_launches(*t, topk, False) for name, t, topk in
             (("a", a, 64), ("b", b, 64), ("c", c, 8))}
     torch.cuda.synchronize()
