@@ -245,6 +245,22 @@ __device__ __forceinline__ float wave_max(float v) { return xor_reduce(v, 1, 32,
 
 __device__ __forceinline__ int wave_any(bool p) { return __any(p); }
 
+// Wave-wide max (MAX) or min of an unsigned word, returned in every lane.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_ext_u32(uint32_t v) {
+  const int id = MAX ? 0 : -1;
+  auto f = [&](uint32_t x, int y) {
+    return MAX ? (x > (uint32_t)y ? x : (uint32_t)y) : (x < (uint32_t)y ? x : (uint32_t)y);
+  };
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0xB1, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x4E, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x141, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x140, 0xf, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x142, 0xa, 0xf, false));
+  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x143, 0xc, 0xf, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Block-wide reductions for up to 1024 threads; `red` needs 32 floats.
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
@@ -457,6 +473,36 @@ __device__ __forceinline__ bool wait_flags(const uint32_t* flag, int cnt, uint32
     if (__all(ready)) return true;
     if (__builtin_amdgcn_s_memrealtime() - t0 > spin) {
       if (lane_id() == 0) atomicAdd(err, 1u);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// wait_flags for flags that carry a range of key high words, each
+// (max >> 16) << 16 | (min >> 16) of its chunk; also returns, in every lane,
+// [hmin, hmax] covering every chunk's range (after a time-out: an empty one).
+__device__ __forceinline__ bool wait_flags_range(const uint32_t* flag, int cnt, uint32_t* err,
+                                                 uint64_t spin, uint32_t& hmax, uint32_t& hmin) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (true) {
+    int ready = 1;
+    uint32_t mx = 0u, mn = 0xffffu;
+    for (int i = lane_id(); i < cnt; i += STK_WAVE) {
+      const uint32_t f = ld_agent(flag + i);
+      ready &= f != 0u;
+      mx = (f >> 16) > mx ? (f >> 16) : mx;
+      mn = (f & 0xffffu) < mn ? (f & 0xffffu) : mn;
+    }
+    if (__all(ready)) {
+      hmax = (wave_ext_u32<true>(mx) << 16) | 0xffffu;
+      hmin = wave_ext_u32<false>(mn) << 16;
+      return true;
+    }
+    if (__builtin_amdgcn_s_memrealtime() - t0 > spin) {
+      if (lane_id() == 0) atomicAdd(err, 1u);
+      hmax = 0u;
+      hmin = 0xffffffffu;
       return false;
     }
     __builtin_amdgcn_s_sleep(1);

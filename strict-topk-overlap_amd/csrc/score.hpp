@@ -51,7 +51,8 @@ struct ScoreArgs {
   int chunks;            // workgroups per KV head
   float* scores;         // optional FP32 [hq, n]
   uint64_t* keys;        // optional [hq, n]
-  uint32_t* sflag;       // SIG: [hq, chunks], set once a chunk's keys are published
+  uint32_t* sflag;       // SIG: [hq, chunks], set (to the chunk's key range, never 0)
+                         // once a chunk's keys are published
   int drop;              // SIG, tests only: publish no flag (the consumers time out)
 };
 
@@ -126,6 +127,7 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
   constexpr int QN = GT * 64 * P;         // staged query values
   __shared__ __align__(16) double s_q[QN];
   __shared__ __align__(16) uint32_t s_m[QN];
+  __shared__ uint32_t s_rng[SIG ? WV : 1][GT][2];   // SIG: per wave and head, key range
   const int G = a.hq / a.hkv;
   const int kv = wg / a.chunks;
   const int chunk = wg % a.chunks;
@@ -306,21 +308,50 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
     const int combo = l16 >> (4 - LOGC);
     const int gi = combo / STEPS, s = combo % STEPS;
     const int nb = wave_base + 4 * s + sub;
-    if ((l16 & ((16 >> LOGC) - 1)) == 0 && nb < nv && gb + gi < G) {
-      if (r == 0.0) r = 0.0;
+    const bool mine = (l16 & ((16 >> LOGC) - 1)) == 0 && nb < nv && gb + gi < G;
+    if (r == 0.0) r = 0.0;
+    const uint64_t key = (PG && ((dead >> s) & 1)) ? 0ull : score_key(r);
+    if (mine) {
       const size_t o = (size_t)(h0 + gb + gi) * a.n + nb;
       if (a.scores) a.scores[o] = (float)r;
-      const uint64_t key = (PG && ((dead >> s) & 1)) ? 0ull : score_key(r);
       if constexpr (SIG) st_agent(a.keys + o, key);
       else if (a.keys) a.keys[o] = key;
+    }
+    if constexpr (SIG) {
+      // while the keys' stores travel: this wave's range of the high words
+      // of its non-NaN keys, per query head (G <= GT: one stage)
+      const uint32_t hw = (uint32_t)(key >> 32);
+      const bool live = mine && key != 0ull;
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        const uint32_t mx = wave_ext_u32<true>(live && gi == g ? hw : 0u);
+        const uint32_t mn = wave_ext_u32<false>(live && gi == g ? hw : 0xffffffffu);
+        if (lane_id() == 0) {
+          s_rng[wave_id()][g][0] = mx;
+          s_rng[wave_id()][g][1] = mn;
+        }
+      }
     }
   }
   if constexpr (SIG) {
     // publish the chunk to every query head of the group
     wait_stores();
     __syncthreads();
-    if (!a.drop && (int)threadIdx.x < G)
-      st_agent(a.sflag + (size_t)(h0 + threadIdx.x) * a.chunks + chunk, 1u);
+    if (!a.drop && (int)threadIdx.x < G) {
+      // The flag carries the chunk's range of key high words rounded
+      // outward to 16 bits, (max >> 16) << 16 | (min >> 16), so that the
+      // tail's top-K starts from the row's range without computing it.  It
+      // is never 0: a non-NaN key's high word is at least 0x000FFFFF, and a
+      // chunk without one gives 0x0000FFFF.
+      uint32_t mx = 0u, mn = 0xffffffffu;
+#pragma unroll
+      for (int w = 0; w < WV; ++w) {
+        mx = s_rng[w][threadIdx.x][0] > mx ? s_rng[w][threadIdx.x][0] : mx;
+        mn = s_rng[w][threadIdx.x][1] < mn ? s_rng[w][threadIdx.x][1] : mn;
+      }
+      st_agent(a.sflag + (size_t)(h0 + threadIdx.x) * a.chunks + chunk,
+               ((mx >> 16) << 16) | (mn >> 16));
+    }
   }
 }
 

@@ -88,12 +88,20 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   uint32_t qw[TT::QW];
   t.load_q(reinterpret_cast<const T*>(a.kv.q) + (size_t)h * D, qw);
   for (int i = tid; i < n; i += kTailThreads) map[i] = 0;
+  // the top-K's histogram too: it starts at phase B, with the row's range
+  // from the scorers' flags
+  for (int i = tid; i < kBins; i += kTailThreads) tb.hist[i] = 0;
+  if (tid < kBins / 16) tb.grp[tid] = 0;
+  if (tid == 0) tb.ncand = 0;
   // every slot entry is written (-1 past sp): the sums below read entries
   // past sp, and LDS holds whatever an earlier workgroup left there
   if (tid < kTailMaxK) pids[tid] = pid;
   if (tid == 0) s_fail = 0;
-  // ---- this head's keys, once every chunk of its KV head is published
-  bool ok = wait_flags(sflag, chunks, A.err, A.spin);
+  __syncthreads();   // the clears before any use (the flags take far longer)
+  // ---- this head's keys and their range, once every chunk of its KV head
+  // is published
+  uint32_t hmax, hmin;
+  bool ok = wait_flags_range(sflag, chunks, A.err, A.spin, hmax, hmin);
   uint64_t key[KPT];
   {
     const uint64_t* rk = a.keys + (size_t)h * n;
@@ -107,10 +115,8 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   }
   // membership map: max predicted slot + 1 of each valid predicted block (a
   // valid block always has a state here: the states role computes every slot)
-  auto fill_map = [&] {
-    if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
-  };
-  const uint32_t flags = topk_bins_flags<KPT>(key, n, a.k, tb, fill_map);
+  if (tid < sp && pid >= 0 && pid < n) atomicMax(&map[pid], tid + 1);
+  const uint32_t flags = topk_bins_from<KPT>(key, n, a.k, tb, hmax, hmin);
   // ---- the state flags, requested now and read after the scan, so that
   // their round trip overlaps it (slots past SP read slot 0; SP <= 128 here)
   const int fl0 = lane_id(), fl1 = lane_id() + STK_WAVE;

@@ -18,6 +18,9 @@
 //   D  if bin t is taken whole, done; otherwise its keys (a few) are listed
 //      in LDS, wave 0 ranks them by (key, -index) and publishes the last one
 //      taken, two barriers.
+// A caller that knows a range covering the keys ahead (the one-launch
+// step's tails get it with the scorers' flags) enters at B
+// (topk_bins_from) and skips A's reductions and barrier.
 // The bin map is monotone non-decreasing in the key (every rounding step is
 // monotone, NaN keys, whose key is 0, go to bin 0), so the selection is the
 // exact one whatever the ranges and roundings are.  Rows whose range is
@@ -52,20 +55,9 @@ __device__ __forceinline__ float key_value(uint64_t key) {
   return (float)__longlong_as_double((long long)b);
 }
 
-template <bool MAX>
-__device__ __forceinline__ uint32_t wave_ext_u32(uint32_t v) {
-  const int id = MAX ? 0 : -1;
-  auto f = [&](uint32_t x, int y) {
-    return MAX ? (x > (uint32_t)y ? x : (uint32_t)y) : (x < (uint32_t)y ? x : (uint32_t)y);
-  };
-  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0xB1, 0xf, 0xf, false));
-  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x4E, 0xf, 0xf, false));
-  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x141, 0xf, 0xf, false));
-  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x140, 0xf, 0xf, false));
-  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x142, 0xa, 0xf, false));
-  v = f(v, __builtin_amdgcn_update_dpp(id, (int)v, 0x143, 0xc, 0xf, false));
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
+template <int KPT>
+__device__ __forceinline__ uint32_t topk_bins_from(const uint64_t (&key)[KPT], int n, int k,
+                                                   TopkBinsLds& L, uint32_t hmax, uint32_t hmin);
 
 // Phase A's LDS words must be free when it starts (a barrier since their
 // last use).  `between` runs after barrier A and before barrier B, for the
@@ -76,11 +68,6 @@ __device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], 
   const int nwaves = blockDim.x / STK_WAVE;
   const int base = threadIdx.x * KPT;
   const int lane = lane_id();
-  // Up to four keys per thread the 16-bin group sums are kept with LDS
-  // atomics during the histogram (phase C then reads one word per lane);
-  // with more keys those atomics, 64 words for the whole row, contend, and
-  // phase C sums its 16 bins from the histogram instead (four 16-byte reads).
-  constexpr bool kGroupAtomics = KPT <= 4;
   // ---- A: range of the finite-or-infinite, non-NaN keys (key 0 is NaN)
   uint32_t hmax = 0u, hmin = 0xffffffffu;
 #pragma unroll
@@ -107,6 +94,23 @@ __device__ __forceinline__ uint32_t topk_bins_flags(const uint64_t (&key)[KPT], 
     hmax = L.red[0][w] > hmax ? L.red[0][w] : hmax;
     hmin = L.red[1][w] < hmin ? L.red[1][w] : hmin;
   }
+  return topk_bins_from<KPT>(key, n, k, L, hmax, hmin);
+}
+
+// Phases B-D for a range [hmin, hmax] of the keys' high words known ahead
+// (any range gives the exact selection; one that covers the row's keys gives
+// the narrowest bins).  L.hist, L.grp and L.ncand must be zero, with a
+// barrier since they were cleared and since L's last use.
+template <int KPT>
+__device__ __forceinline__ uint32_t topk_bins_from(const uint64_t (&key)[KPT], int n, int k,
+                                                   TopkBinsLds& L, uint32_t hmax, uint32_t hmin) {
+  const int base = threadIdx.x * KPT;
+  const int lane = lane_id();
+  // Up to four keys per thread the 16-bin group sums are kept with LDS
+  // atomics during the histogram (phase C then reads one word per lane);
+  // with more keys those atomics, 64 words for the whole row, contend, and
+  // phase C sums its 16 bins from the histogram instead (four 16-byte reads).
+  constexpr bool kGroupAtomics = KPT <= 4;
   const float lo = key_value((uint64_t)hmin << 32);
   const float hi = key_value(((uint64_t)hmax << 32) | 0xffffffffull);
   const float range = hi - lo;
