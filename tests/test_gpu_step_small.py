@@ -145,3 +145,28 @@ def test_small_step_in_a_graph():
         assert torch.equal(out.selected, eager.selected)
         assert torch.equal(out.output, eager.output)
         assert torch.equal(out.state.u, eager.state.u)
+
+
+@pytest.mark.parametrize("n", [40, 80])   # one workgroup per head; past 64 blocks, the flag grid
+def test_step_nonfinite_bounds(n):
+    """-inf / +inf bounds and NaN scores through the fused step (its own FP64
+    scores and top-K): the selected IDs equal the oracle's, NaN ranking below
+    -inf and ties toward the lower index."""
+    from stk_harness.configs import make_qkv
+    from strict_topk import step
+    hq, hkv, d, topk = 4, 2, 64, 8
+    q, k, v, lo, hi = make_qkv(hq, hkv, d, 32, n, torch.float16, True, 4242 + n)
+    lo, hi = lo.clone(), hi.clone()
+    lo[0, 3] = float("-inf")
+    hi[1, 5] = float("inf")
+    lo[1, 7, 0] = float("nan")
+    hi[1, 7, 0] = float("nan")
+    lo[0, 9:12] = lo[0, 12]          # exact ties
+    hi[0, 9:12] = hi[0, 12]
+    ref = O.select_blocks(C.f64(q), lo.double().numpy(), hi.double().numpy(), topk)
+    p = torch.from_numpy(ref[:, :topk].copy()).to(torch.int32)
+    qd, kd, vd, lod, hid, pd = (t.cuda() for t in (q, k, v, lo, hi, p))
+    assert _small(qd, kd, topk, topk, lod) == (n <= 64)
+    res = step.speculative_step(qd, kd, vd, lod, hid, pd, topk)
+    torch.cuda.synchronize()
+    assert res.selected.cpu().numpy().tolist() == ref.tolist()
