@@ -6,17 +6,18 @@
 // kernels.repair or gqa.repair_union) is, per query head, the bound scores of
 // its KV head's blocks (selector.py:8-20), their top-K, the predicted blocks'
 // softmax states (kernels.py:42-71) and the strict repair's LSE merge
-// (kernels.py:120-247).  When a head has at most 64 blocks and at most eight
+// (kernels.py:120-247).  When a head has at most 128 blocks and at most eight
 // selected and eight predicted rows, one workgroup of sixteen waves holds all
 // of it, in two roles that meet only in LDS:
 //   * selection, waves 0..7 (launched first): wave 0 requests the predicted
 //     IDs ahead of everything and publishes them as soon as they arrive;
-//     every wave requests the bounds of eight blocks and the query, scores
-//     them in FP64, publishes the keys, adds its partial ranks (its eight
-//     blocks against all 64), and once every rank is in, each wave finds the
-//     selection and the misses by ballot and requests its miss half-tiles
-//     (a miss is split in two 16-token halves, so up to sixteen halves run
-//     on eight waves); wave 0 writes the IDs while those tiles travel;
+//     every wave requests the bounds of N / 8 blocks (8 or 16) and the
+//     query, scores them in FP64, publishes the keys, adds its partial ranks
+//     (its blocks against all of them; past 64 blocks a lane ranks two), and
+//     once every rank is in, each wave finds the selection and the misses by
+//     ballot and requests its miss half-tiles (a miss is split in two
+//     16-token halves, so up to sixteen halves run on eight waves); wave 0
+//     writes the IDs while those tiles travel;
 //   * prediction, waves 8..15: wave 8 + p waits for the IDs, requests slot
 //     p's tile and computes and stores its softmax state.
 // The merge after the one barrier reads every row (predicted states, miss
@@ -65,21 +66,25 @@ __device__ __forceinline__ void pin(float (&x)[N]) {
                  "+v"(x[i + 4]), "+v"(x[i + 5]), "+v"(x[i + 6]), "+v"(x[i + 7]));
 }
 
-template <typename T, int NCH, bool LB16>
+// KB: blocks per lane of the rank (MAXN = 64 KB blocks per KV head at most).
+template <typename T, int NCH, bool LB16, int KB>
 __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
   using TT = TokTile<T, NCH, 2>;   // 32 tokens: one block per chunk
   using TH = TokTile<T, NCH, 1>;   // 16 tokens: half a block (the misses)
   constexpr int D = TT::D;
   constexpr int P = D / 64;         // 64-dim scoring passes
   constexpr int SW = kSmallRoleWaves;
-  constexpr int STEPS = kSmallMaxN / (SW * 4);   // 4-block scoring steps per wave
+  constexpr int MAXN = STK_WAVE * KB;
+  static_assert(KB == 1 || KB == 2, "one or two blocks per lane");
+  constexpr int STEPS = MAXN / (SW * 4);         // 4-block scoring steps per wave
+  constexpr int JW = MAXN / SW;                  // blocks per wave in the rank
   constexpr int RM = 2 * kSmallMaxRows;          // the misses' half-block rows
   constexpr int R = kSmallMaxRows + RM;          // merged rows: predicted | miss halves
   static_assert(R % 8 == 0 && TH::QW == TT::QW && TH::DPL == TT::DPL,
                 "rows read as 4-wide vectors; the half tile shares the query layout");
-  __shared__ uint64_t s_key[kSmallMaxN];
-  __shared__ int s_rank[kSmallMaxN];
-  __shared__ int s_pred[kSmallMaxN];   // 1: some predicted slot holds the block
+  __shared__ uint64_t s_key[MAXN];
+  __shared__ int s_rank[MAXN];
+  __shared__ int s_pred[MAXN];   // 1: some predicted slot holds the block
   __shared__ int s_pid[kSmallMaxRows];
   __shared__ __align__(16) int s_on[R];
   __shared__ int s_kdone, s_rdone, s_pdone;
@@ -94,7 +99,7 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
   const size_t blk_elems = (size_t)32 * D;
   const T* qrow = reinterpret_cast<const T*>(a.q) + (size_t)h * D;
   const float scale = 1.0f / sqrtf((float)D);
-  if (tid < kSmallMaxN) {
+  if (tid < MAXN) {
     s_rank[tid] = 0;
     s_pred[tid] = 0;
   }
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
       if (ok) s_pred[pidv] = 1;
       lds_signal(&s_pdone);
     }
-    static_assert(STEPS == 2, "two scoring steps: row lanes 0..7 and 8..15 hold their sums");
+    static_assert(STEPS == 2 || STEPS == 4, "two or four scoring steps");
     double acc[STEPS];
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
@@ -197,47 +202,65 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
         }
       }
     }
-    // the xor butterfly 8, 4, 2, 1 of both steps at once: row lanes 0..7
-    // hold step 0's sum, lanes 8..15 step 1's.  Blocks past N get key 0,
-    // below every score's key or equal to a NaN score's and at a higher
-    // index, so they never outrank a block
+    // the xor butterfly 8, 4, 2, 1 of every step at once: row lane l16
+    // holds step l16 / (16 / STEPS)'s sum.  Blocks past N get key 0, below
+    // every score's key or equal to a NaN score's and at a higher index, so
+    // they never outrank a block
     const double sum = score_rowsum<STEPS>(acc, l16);
-    if ((l16 & 7) == 0) {
-      const int nb = ((l16 >> 3) * SW + sw) * 4 + sub;
+    constexpr int LPS = 16 / STEPS;   // row lanes per step
+    if ((l16 & (LPS - 1)) == 0) {
+      const int nb = ((l16 / LPS) * SW + sw) * 4 + sub;
       s_key[nb] = nb < n ? score_key(sum) : 0ull;
     }
     lds_signal(&s_kdone);
     lds_wait(&s_kdone, SW);
-    // ---- ranks by (key, -index): wave sw compares every block (lane i)
-    // with blocks 8 sw .. 8 sw + 7 and adds its count
-    const uint64_t ki = s_key[lane];
-    int part = 0;
+    // ---- ranks by (key, -index): wave sw compares every block (lane i
+    // holds blocks i and, KB = 2, i + 64) with blocks JW sw .. JW sw + JW - 1
+    // and adds its counts
 #pragma unroll
-    for (int x = 0; x < kSmallMaxN / SW; ++x) {
-      const int j = sw * (kSmallMaxN / SW) + x;
-      const uint64_t kj = s_key[j];
-      part += (kj > ki) || (kj == ki && j < lane);
+    for (int kb = 0; kb < KB; ++kb) {
+      const int i = lane + STK_WAVE * kb;
+      const uint64_t ki = s_key[i];
+      int part = 0;
+#pragma unroll
+      for (int x = 0; x < JW; ++x) {
+        const int j = sw * JW + x;
+        const uint64_t kj = s_key[j];
+        part += (kj > ki) || (kj == ki && j < i);
+      }
+      if (part) __hip_atomic_fetch_add(&s_rank[i], part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    if (part) __hip_atomic_fetch_add(&s_rank[lane], part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     lds_signal(&s_rdone);
     lds_wait(&s_rdone, SW);
     // ---- every selection wave: the selection and the misses (selected, in
     // no predicted slot) in ascending order.  Miss i is two tasks, its
     // tokens 0..15 (task 2 i) and 16..31 (task 2 i + 1); wave sw takes tasks
     // sw and sw + 8, both halves of the same parity
-    const int rk = s_rank[lane], pr = s_pred[lane];   // both read at once
-    const bool sel = (lane < n) & (rk < K);
-    const uint64_t selm = __ballot(sel);
-    const uint64_t mm = __ballot(sel & (pr == 0));
-    const int nmiss = __popcll(mm);
+    // (selm / mm word kb: blocks 64 kb .. 64 kb + 63)
+    bool sel[KB];
+    uint64_t selm[2] = {0ull, 0ull}, mm[2] = {0ull, 0ull};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int i = lane + STK_WAVE * kb;
+      const int rk = s_rank[i], pr = s_pred[i];   // both read at once
+      sel[kb] = (i < n) & (rk < K);
+      selm[kb] = __ballot(sel[kb]);
+      mm[kb] = __ballot(sel[kb] & (pr == 0));
+    }
+    const int nm0 = __popcll(mm[0]);
+    const int nmiss = nm0 + __popcll(mm[1]);
     const int nt = 2 * nmiss;
     const int t0 = 16 * (sw & 1);
     const bool has0 = sw < nt, has1 = sw + SW < nt;
-    uint64_t mk = mm;   // miss sw / 2 at the lowest set bit, then miss sw / 2 + 4
-    for (int i = 0; i < (sw >> 1); ++i) mk &= mk - 1;
-    const int b0 = has0 ? __builtin_ctzll(mk) : 0;
-    for (int i = 0; i < SW / 2; ++i) mk &= mk - 1;
-    const int b1 = has1 ? __builtin_ctzll(mk) : 0;
+    // block of miss mi (ascending order): the mi-th set bit of mm
+    auto miss_block = [&](int mi) {
+      const int word = mi < nm0 ? 0 : 1;
+      uint64_t x = mm[word];
+      for (int i = word ? mi - nm0 : mi; i > 0; --i) x &= x - 1;
+      return STK_WAVE * word + __builtin_ctzll(x);
+    };
+    const int b0 = has0 ? miss_block(sw >> 1) : 0;
+    const int b1 = has1 ? miss_block((sw >> 1) + SW / 2) : 0;
     TH th;
     th.init();
     uint32_t kw0[1][TH::QW], vw0[TH::CH][TH::VW], kw1[1][TH::QW], vw1[TH::CH][TH::VW];
@@ -255,14 +278,18 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
       // Predicted slot p counts when valid and (union, or its block is
       // selected and p is the highest slot holding it)
       const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-      if (sel) a.ids[(size_t)h * K + __popcll(selm & below)] = lane;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+        if (sel[kb])
+          a.ids[(size_t)h * K + (kb ? __popcll(selm[0]) : 0) + __popcll(selm[kb] & below)] =
+              lane + STK_WAVE * kb;
       if (lane < sp) {
         const int b = s_pid[lane];
         bool top = true;
 #pragma unroll
         for (int p = 0; p < kSmallMaxRows; ++p)
           top = top && !(p > lane && p < sp && s_pid[p] == b);
-        const bool bsel = b >= 0 && ((selm >> b) & 1ull);
+        const bool bsel = b >= 0 && ((selm[b >> 6] >> (b & 63)) & 1ull);
         s_on[lane] = b >= 0 && (a.uni != 0 || (bsel && top));
       } else if (lane >= kSmallMaxRows && lane < kSmallMaxRows + nt) {
         s_on[lane] = 1;
@@ -340,10 +367,15 @@ bool small_covers(int dtype, int hq, int hkv, int n, int b, int d, int topk, int
 int launch_small(int dtype, const SmallArgs& a, int bounds_dtype, hipStream_t st) {
   const dim3 grid(a.hq), block(kSmallThreads);
   const bool lb16 = bounds_dtype != 0;
-#define STK_SMALL(T_, NCH_)                                                         \
-  do {                                                                              \
-    if (lb16) hipLaunchKernelGGL((k_step_small<T_, NCH_, true>), grid, block, 0, st, a); \
-    else hipLaunchKernelGGL((k_step_small<T_, NCH_, false>), grid, block, 0, st, a);     \
+#define STK_SMALL_KB(T_, NCH_, KB_)                                                    \
+  do {                                                                                 \
+    if (lb16) hipLaunchKernelGGL((k_step_small<T_, NCH_, true, KB_>), grid, block, 0, st, a); \
+    else hipLaunchKernelGGL((k_step_small<T_, NCH_, false, KB_>), grid, block, 0, st, a);     \
+  } while (0)
+#define STK_SMALL(T_, NCH_)                      \
+  do {                                           \
+    if (a.n > STK_WAVE) STK_SMALL_KB(T_, NCH_, 2); \
+    else STK_SMALL_KB(T_, NCH_, 1);              \
   } while (0)
   if (dtype == DT_BF16) {
     if (a.d == 64) STK_SMALL(bf16s, 2);
@@ -353,6 +385,7 @@ int launch_small(int dtype, const SmallArgs& a, int bounds_dtype, hipStream_t st
     else STK_SMALL(f16s, 4);
   }
 #undef STK_SMALL
+#undef STK_SMALL_KB
   return stk_check_launch("k_step_small");
 }
 

@@ -1,5 +1,5 @@
 // The speculative step for small shapes in one launch (k_step_small,
-// step_small.hip): one workgroup per query head for up to 64 blocks per KV
+// step_small.hip): one workgroup per query head for up to 128 blocks per KV
 // head and up to eight selected and eight predicted rows per head.  Its
 // sixteen waves split in two roles (step_small.hip).
 #pragma once
@@ -10,7 +10,7 @@ namespace stk {
 
 constexpr int kSmallThreads = 1024;
 constexpr int kSmallRoleWaves = 8;   // waves per role: predicted tiles | selection and misses
-constexpr int kSmallMaxN = 64;      // blocks per KV head: one per lane of the top-K wave
+constexpr int kSmallMaxN = 128;     // blocks per KV head: up to two per lane of the rank
 constexpr int kSmallMaxRows = 8;    // selected and predicted rows: one tile per wave each
 
 struct SmallArgs {
@@ -26,7 +26,7 @@ struct SmallArgs {
 };
 
 // True when k_step_small covers the fused step's shape: bf16 / fp16 K/V,
-// B = 32, D in {64, 128}, N <= 64, TOPK and SP in [1, 8], bounds FP32 or of
+// B = 32, D in {64, 128}, N <= 128, TOPK and SP in [1, 8], bounds FP32 or of
 // the K/V type, and 16-byte aligned q / k / v / lo / hi (`align`: the OR of
 // their addresses).
 bool small_covers(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,

@@ -97,14 +97,14 @@ def _same(res, ref):
     (32, 8, 2048, 128, 64, 0.75, torch.bfloat16, False),   # c3, 16 misses per head
     (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, True),     # c3, repair_union
     (16, 8, 512, 128, 64, 0.9, torch.bfloat16, False),     # c2 (G = 2)
-    (4, 4, 65, 64, 8, 0.75, torch.float16, False),         # c1-like (G = 1, D = 64), one block
+    (4, 4, 130, 64, 8, 0.75, torch.float16, False),        # c1-like (G = 1, D = 64), past the small step
                                                            # past the one-workgroup-per-head shapes
     (12, 3, 4000, 64, 50, 0.5, torch.float16, False),      # eight keys per tail thread
     (8, 8, 7000, 128, 16, 0.9, torch.bfloat16, False),     # sixteen keys per tail thread
     (6, 2, 333, 128, 40, 0.6, torch.bfloat16, False),      # G = 3, N not a chunk multiple
     (4, 4, 64, 64, 64, 1.0, torch.float16, False),         # K = N: every block selected
     (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, "fp32"),   # c3 with the reference's FP32 bounds
-    (4, 4, 65, 64, 8, 0.75, torch.float16, "fp32"),        # c1-like with FP32 bounds
+    (4, 4, 130, 64, 8, 0.75, torch.float16, "fp32"),       # c1-like with FP32 bounds
 ])
 def test_step1_matches_two_launches(hq, hkv, n, d, topk, overlap, dtype, union):
     """The one launch against its two launches (bit-equal IDs, states and
@@ -171,7 +171,7 @@ def test_step1_two_streams_and_shape_changes():
     from strict_topk import step
     a = _inputs(32, 8, 2048, 128, 64, 0.9, torch.bfloat16, 20261104)[1]
     b = _inputs(16, 8, 512, 128, 64, 0.75, torch.bfloat16, 20261105)[1]
-    c = _inputs(4, 4, 65, 64, 8, 0.75, torch.float16, 20261106)[1]
+    c = _inputs(4, 4, 130, 64, 8, 0.75, torch.float16, 20261106)[1]
     refs = {name: _two_launches(*t, topk, False) for name, t, topk in
             (("a", a, 64), ("b", b, 64), ("c", c, 8))}
     torch.cuda.synchronize()

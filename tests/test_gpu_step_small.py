@@ -1,6 +1,6 @@
 """GPU parity of the small-shape step (one workgroup per query head).
 
-stk_speculative_step runs shapes with at most 64 blocks per KV head and at
+stk_speculative_step runs shapes with at most 128 blocks per KV head and at
 most eight selected and eight predicted rows per head in one workgroup per
 query head (k_step_small).  Bars, as for the other fused paths: selected IDs
 bit-exact against the FP64 oracle (ties toward the lower index, ascending);
@@ -66,6 +66,9 @@ def _check(res, host, p_host, topk, union, what):
     (6, 3, 17, 64, 3, 0.6, torch.bfloat16, "k", False),      # small K
     (4, 2, 1, 128, 1, 1.0, torch.bfloat16, "k", False),      # one block
     (4, 4, 8, 64, 8, 1.0, torch.float16, "k", False),        # K = N
+    (4, 4, 128, 64, 8, 0.75, torch.float16, "fp32", False),  # two blocks per lane of the rank
+    (8, 2, 100, 128, 8, 0.5, torch.bfloat16, "k", True),     # N between 64 and 128, union
+    (6, 3, 65, 128, 5, 0.0, torch.bfloat16, "fp32", False),  # one block past 64, every block missed
 ])
 def test_small_step(hq, hkv, n, d, topk, overlap, dtype, bounds, union):
     from stk_harness.configs import make_qkv, perturb
@@ -104,12 +107,13 @@ def test_small_step_predictions_with_invalid_and_repeated_ids():
 
 
 def test_small_step_not_covered():
-    """Past 64 blocks, 8 selected or 8 predicted rows, other block sizes and
+    """Past 128 blocks, 8 selected or 8 predicted rows, other block sizes and
     head dims, the step takes the other paths."""
     from strict_topk import _lib
     L = _lib.lib()
     assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 8, 8, 0, 0) == 1
-    assert L.stk_step_small_supported(1, 4, 4, 65, 32, 64, 8, 8, 0, 0) == 0   # N
+    assert L.stk_step_small_supported(1, 4, 4, 128, 32, 64, 8, 8, 0, 0) == 1
+    assert L.stk_step_small_supported(1, 4, 4, 129, 32, 64, 8, 8, 0, 0) == 0  # N
     assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 9, 8, 0, 0) == 0   # TOPK
     assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 8, 9, 0, 0) == 0   # SP
     assert L.stk_step_small_supported(1, 4, 4, 64, 16, 64, 8, 8, 0, 0) == 0   # B
@@ -147,7 +151,7 @@ def test_small_step_in_a_graph():
         assert torch.equal(out.state.u, eager.state.u)
 
 
-@pytest.mark.parametrize("n", [40, 80])   # one workgroup per head; past 64 blocks, the flag grid
+@pytest.mark.parametrize("n", [40, 100, 130])   # one workgroup per head (up to 128 blocks); the flag grid
 def test_step_nonfinite_bounds(n):
     """-inf / +inf bounds and NaN scores through the fused step (its own FP64
     scores and top-K): the selected IDs equal the oracle's, NaN ranking below
@@ -166,7 +170,7 @@ def test_step_nonfinite_bounds(n):
     ref = O.select_blocks(C.f64(q), lo.double().numpy(), hi.double().numpy(), topk)
     p = torch.from_numpy(ref[:, :topk].copy()).to(torch.int32)
     qd, kd, vd, lod, hid, pd = (t.cuda() for t in (q, k, v, lo, hi, p))
-    assert _small(qd, kd, topk, topk, lod) == (n <= 64)
+    assert _small(qd, kd, topk, topk, lod) == (n <= 128)
     res = step.speculative_step(qd, kd, vd, lod, hid, pd, topk)
     torch.cuda.synchronize()
     assert res.selected.cpu().numpy().tolist() == ref.tolist()
