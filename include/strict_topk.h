@@ -286,7 +286,7 @@ int stk_step1_supported(int dtype, int hq, int hkv, int n, int b, int d, int top
 /* 1 when stk_speculative_step (and stk_speculative_step_noalloc) run the
  * shape in one workgroup per query head, with no hand-off between
  * workgroups: bf16/fp16, B = 32, D in {64, 128}, N <= 128, TOPK and SP in
- * [1, 8], int32 predicted IDs, bounds FP32 or of the K/V type (16-byte
+ * [1, 16], int32 predicted IDs, bounds FP32 or of the K/V type (16-byte
  * aligned pointers assumed; others take the paths above).  Such a head's
  * bounds, then its misses' tiles, are two dependent memory round trips of
  * its own workgroup; its predicted tiles travel beside them.  The selected

@@ -6,9 +6,9 @@
 // kernels.repair or gqa.repair_union) is, per query head, the bound scores of
 // its KV head's blocks (selector.py:8-20), their top-K, the predicted blocks'
 // softmax states (kernels.py:42-71) and the strict repair's LSE merge
-// (kernels.py:120-247).  When a head has at most 128 blocks and at most eight
-// selected and eight predicted rows, one workgroup of sixteen waves holds all
-// of it, in two roles that meet only in LDS:
+// (kernels.py:120-247).  When a head has at most 128 blocks and at most
+// sixteen selected and sixteen predicted rows, one workgroup of sixteen waves
+// holds all of it, in two roles that meet only in LDS:
 //   * selection, waves 0..7 (launched first): wave 0 requests the predicted
 //     IDs ahead of everything and publishes them as soon as they arrive;
 //     every wave requests the bounds of N / 8 blocks (8 or 16) and the
@@ -16,10 +16,12 @@
 //     (its blocks against all of them; past 64 blocks a lane ranks two), and
 //     once every rank is in, each wave finds the selection and the misses by
 //     ballot and requests its miss half-tiles (a miss is split in two
-//     16-token halves, so up to sixteen halves run on eight waves); wave 0
-//     writes the IDs while those tiles travel;
-//   * prediction, waves 8..15: wave 8 + p waits for the IDs, requests slot
-//     p's tile and computes and stores its softmax state.
+//     16-token halves, two per wave in flight, in one round up to eight
+//     misses and two up to sixteen); wave 0 writes the IDs while those tiles
+//     travel;
+//   * prediction, waves 8..15: wave 8 + p waits for the IDs, then for slot
+//     p and (past eight rows) slot p + 8 in turn requests the tile and
+//     computes and stores its softmax state.
 // The merge after the one barrier reads every row (predicted states, miss
 // halves) from LDS.  Critical path: two dependent memory round trips (the
 // bounds, then the miss tiles) and two LDS hand-offs (keys, ranks).  The
@@ -66,8 +68,9 @@ __device__ __forceinline__ void pin(float (&x)[N]) {
                  "+v"(x[i + 4]), "+v"(x[i + 5]), "+v"(x[i + 6]), "+v"(x[i + 7]));
 }
 
-// KB: blocks per lane of the rank (MAXN = 64 KB blocks per KV head at most).
-template <typename T, int NCH, bool LB16, int KB>
+// KB: blocks per lane of the rank (MAXN = 64 KB blocks per KV head at most);
+// ROWS: the most selected and the most predicted rows per head (8 or 16).
+template <typename T, int NCH, bool LB16, int KB, int ROWS>
 __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
   using TT = TokTile<T, NCH, 2>;   // 32 tokens: one block per chunk
   using TH = TokTile<T, NCH, 1>;   // 16 tokens: half a block (the misses)
@@ -78,14 +81,16 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
   static_assert(KB == 1 || KB == 2, "one or two blocks per lane");
   constexpr int STEPS = MAXN / (SW * 4);         // 4-block scoring steps per wave
   constexpr int JW = MAXN / SW;                  // blocks per wave in the rank
-  constexpr int RM = 2 * kSmallMaxRows;          // the misses' half-block rows
-  constexpr int R = kSmallMaxRows + RM;          // merged rows: predicted | miss halves
-  static_assert(R % 8 == 0 && TH::QW == TT::QW && TH::DPL == TT::DPL,
-                "rows read as 4-wide vectors; the half tile shares the query layout");
+  static_assert(ROWS == 8 || ROWS == 16, "eight or sixteen rows");
+  constexpr int RM = 2 * ROWS;                   // the misses' half-block rows
+  constexpr int R = ROWS + RM;                   // merged rows: predicted | miss halves
+  constexpr int RC = 24;                         // rows per merge chunk
+  static_assert(R % RC == 0 && RC % 8 == 0 && TH::QW == TT::QW && TH::DPL == TT::DPL,
+                "rows merged in chunks of 24; the half tile shares the query layout");
   __shared__ uint64_t s_key[MAXN];
   __shared__ int s_rank[MAXN];
   __shared__ int s_pred[MAXN];   // 1: some predicted slot holds the block
-  __shared__ int s_pid[kSmallMaxRows];
+  __shared__ int s_pid[ROWS];
   __shared__ __align__(16) int s_on[R];
   __shared__ int s_kdone, s_rdone, s_pdone;
   __shared__ __align__(16) float s_m[R];
@@ -110,13 +115,14 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
   t.init();
   uint32_t qw[TT::QW];
   if (w >= SW) {
-    // ---- predicted role, wave SW + ps (ps < SP): slot ps's ID (published
-    // by wave 0), then its tile, then its state (an invalid ID reads block 0
-    // and keeps the empty state)
-    const int ps = w - SW;
-    if (ps < sp) {
+    // ---- predicted role, wave SW + q: slots q and (ROWS = 16) q + 8 in
+    // turn, each its ID (published by wave 0), then its tile, then its state
+    // (an invalid ID reads block 0 and keeps the empty state)
+    if (w - SW < sp) {
       t.load_q(qrow, qw);
       lds_wait(&s_pdone, 1);
+    }
+    for (int ps = w - SW; ps < sp && ps < ROWS; ps += SW) {
       const int pid = s_pid[ps];
       const bool pvalid = pid >= 0;
       uint32_t kw[2][TT::QW], vw[TT::CH][TT::VW];
@@ -172,7 +178,7 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     if (sw == 0) {
       const bool ok = lane < sp && pidv >= 0 && pidv < n;
-      if (lane < kSmallMaxRows) s_pid[lane] = ok ? pidv : -1;
+      if (lane < ROWS) s_pid[lane] = ok ? pidv : -1;
       if (ok) s_pred[pidv] = 1;
       lds_signal(&s_pdone);
     }
@@ -235,7 +241,7 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
     // ---- every selection wave: the selection and the misses (selected, in
     // no predicted slot) in ascending order.  Miss i is two tasks, its
     // tokens 0..15 (task 2 i) and 16..31 (task 2 i + 1); wave sw takes tasks
-    // sw and sw + 8, both halves of the same parity
+    // sw + 16 r and sw + 16 r + 8 in round r, all of the same parity
     // (selm / mm word kb: blocks 64 kb .. 64 kb + 63)
     bool sel[KB];
     uint64_t selm[2] = {0ull, 0ull}, mm[2] = {0ull, 0ull};
@@ -251,7 +257,6 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
     const int nmiss = nm0 + __popcll(mm[1]);
     const int nt = 2 * nmiss;
     const int t0 = 16 * (sw & 1);
-    const bool has0 = sw < nt, has1 = sw + SW < nt;
     // block of miss mi (ascending order): the mi-th set bit of mm
     auto miss_block = [&](int mi) {
       const int word = mi < nm0 ? 0 : 1;
@@ -259,64 +264,67 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
       for (int i = word ? mi - nm0 : mi; i > 0; --i) x &= x - 1;
       return STK_WAVE * word + __builtin_ctzll(x);
     };
-    const int b0 = has0 ? miss_block(sw >> 1) : 0;
-    const int b1 = has1 ? miss_block((sw >> 1) + SW / 2) : 0;
     TH th;
     th.init();
-    uint32_t kw0[1][TH::QW], vw0[TH::CH][TH::VW], kw1[1][TH::QW], vw1[TH::CH][TH::VW];
-    if (has0) {
-      const size_t off = ((size_t)kv * n + b0) * blk_elems;
-      th.load(K_ + off, V_ + off, t0, kw0, vw0);
-    }
-    if (has1) {
-      const size_t off = ((size_t)kv * n + b1) * blk_elems;
-      th.load(K_ + off, V_ + off, t0, kw1, vw1);
-    }
-    __builtin_amdgcn_sched_barrier(0);   // both halves requested before either is used
-    if (sw == 0) {
-      // while the tiles travel: the IDs out, and the rows the merge takes.
-      // Predicted slot p counts when valid and (union, or its block is
-      // selected and p is the highest slot holding it)
-      const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-        if (sel[kb])
-          a.ids[(size_t)h * K + (kb ? __popcll(selm[0]) : 0) + __popcll(selm[kb] & below)] =
-              lane + STK_WAVE * kb;
-      if (lane < sp) {
-        const int b = s_pid[lane];
-        bool top = true;
-#pragma unroll
-        for (int p = 0; p < kSmallMaxRows; ++p)
-          top = top && !(p > lane && p < sp && s_pid[p] == b);
-        const bool bsel = b >= 0 && ((selm[b >> 6] >> (b & 63)) & 1ull);
-        s_on[lane] = b >= 0 && (a.uni != 0 || (bsel && top));
-      } else if (lane >= kSmallMaxRows && lane < kSmallMaxRows + nt) {
-        s_on[lane] = 1;
+    for (int r = 0; r < ROWS / 8; ++r) {
+      const int ta = sw + 2 * SW * r, tb = ta + SW;
+      const bool has_a = ta < nt, has_b = tb < nt;
+      uint32_t kwa[1][TH::QW], vwa[TH::CH][TH::VW], kwb[1][TH::QW], vwb[TH::CH][TH::VW];
+      if (has_a) {
+        const size_t off = ((size_t)kv * n + miss_block(ta >> 1)) * blk_elems;
+        th.load(K_ + off, V_ + off, t0, kwa, vwa);
       }
-    }
-    // the halves' states (row 8 + task)
-    if (has0) {
-      float m = -INFINITY, l = 0.f, acc[TH::DPL];
-#pragma unroll
-      for (int e = 0; e < TH::DPL; ++e) acc[e] = 0.f;
-      th.template update<false, false>(qw, kw0, vw0, t0, 32, scale, m, l, acc);
-      if (lane == 0) {
-        s_m[kSmallMaxRows + sw] = m;
-        s_l[kSmallMaxRows + sw] = l;
+      if (has_b) {
+        const size_t off = ((size_t)kv * n + miss_block(tb >> 1)) * blk_elems;
+        th.load(K_ + off, V_ + off, t0, kwb, vwb);
       }
-      th.store(s_u[kSmallMaxRows + sw], acc);
-    }
-    if (has1) {
-      float m = -INFINITY, l = 0.f, acc[TH::DPL];
+      __builtin_amdgcn_sched_barrier(0);   // both halves requested before either is used
+      if (r == 0 && sw == 0) {
+        // while the tiles travel: the IDs out, and the rows the merge takes.
+        // Predicted slot p counts when valid and (union, or its block is
+        // selected and p is the highest slot holding it)
+        const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
 #pragma unroll
-      for (int e = 0; e < TH::DPL; ++e) acc[e] = 0.f;
-      th.template update<false, false>(qw, kw1, vw1, t0, 32, scale, m, l, acc);
-      if (lane == 0) {
-        s_m[kSmallMaxRows + SW + sw] = m;
-        s_l[kSmallMaxRows + SW + sw] = l;
+        for (int kb = 0; kb < KB; ++kb)
+          if (sel[kb])
+            a.ids[(size_t)h * K + (kb ? __popcll(selm[0]) : 0) + __popcll(selm[kb] & below)] =
+                lane + STK_WAVE * kb;
+        if (lane < sp) {
+          const int b = s_pid[lane];
+          bool top = true;
+#pragma unroll
+          for (int p = 0; p < ROWS; ++p)
+            top = top && !(p > lane && p < sp && s_pid[p] == b);
+          const bool bsel = b >= 0 && ((selm[b >> 6] >> (b & 63)) & 1ull);
+          s_on[lane] = b >= 0 && (a.uni != 0 || (bsel && top));
+        } else if (lane >= ROWS && lane < ROWS + nt) {
+          s_on[lane] = 1;
+        }
       }
-      th.store(s_u[kSmallMaxRows + SW + sw], acc);
+      // the halves' states (row ROWS + task)
+      if (has_a) {
+        float m = -INFINITY, l = 0.f, acc[TH::DPL];
+#pragma unroll
+        for (int e = 0; e < TH::DPL; ++e) acc[e] = 0.f;
+        th.template update<false, false>(qw, kwa, vwa, t0, 32, scale, m, l, acc);
+        if (lane == 0) {
+          s_m[ROWS + ta] = m;
+          s_l[ROWS + ta] = l;
+        }
+        th.store(s_u[ROWS + ta], acc);
+      }
+      if (has_b) {
+        float m = -INFINITY, l = 0.f, acc[TH::DPL];
+#pragma unroll
+        for (int e = 0; e < TH::DPL; ++e) acc[e] = 0.f;
+        th.template update<false, false>(qw, kwb, vwb, t0, 32, scale, m, l, acc);
+        if (lane == 0) {
+          s_m[ROWS + tb] = m;
+          s_l[ROWS + tb] = l;
+        }
+        th.store(s_u[ROWS + tb], acc);
+      }
     }
   }
   __syncthreads();
@@ -326,29 +334,41 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
   // out by selection, not by a zero weight
   const int dm = tid;
   if (dm < D) {
-    float mr[R], ur[R], lr[R];
-    int on[R];
+    // chunks of RC rows: their m, l and flags as 4-wide vectors and their u
+    // column entries all requested before any is used
+    auto chunk = [&](int c0, float (&mr)[RC], float (&lr)[RC], float (&ur)[RC], int (&on)[RC]) {
 #pragma unroll
-    for (int i = 0; i < R / 4; ++i) {
-      const float4 m4 = reinterpret_cast<const float4*>(s_m)[i];
-      const float4 l4 = reinterpret_cast<const float4*>(s_l)[i];
-      const int4 o4 = reinterpret_cast<const int4*>(s_on)[i];
-      mr[4 * i] = m4.x; mr[4 * i + 1] = m4.y; mr[4 * i + 2] = m4.z; mr[4 * i + 3] = m4.w;
-      lr[4 * i] = l4.x; lr[4 * i + 1] = l4.y; lr[4 * i + 2] = l4.z; lr[4 * i + 3] = l4.w;
-      on[4 * i] = o4.x; on[4 * i + 1] = o4.y; on[4 * i + 2] = o4.z; on[4 * i + 3] = o4.w;
-    }
+      for (int i = 0; i < RC / 4; ++i) {
+        const float4 m4 = reinterpret_cast<const float4*>(s_m + c0)[i];
+        const float4 l4 = reinterpret_cast<const float4*>(s_l + c0)[i];
+        const int4 o4 = reinterpret_cast<const int4*>(s_on + c0)[i];
+        mr[4 * i] = m4.x; mr[4 * i + 1] = m4.y; mr[4 * i + 2] = m4.z; mr[4 * i + 3] = m4.w;
+        lr[4 * i] = l4.x; lr[4 * i + 1] = l4.y; lr[4 * i + 2] = l4.z; lr[4 * i + 3] = l4.w;
+        on[4 * i] = o4.x; on[4 * i + 1] = o4.y; on[4 * i + 2] = o4.z; on[4 * i + 3] = o4.w;
+      }
 #pragma unroll
-    for (int r = 0; r < R; ++r) ur[r] = s_u[r][dm];
-    pin(ur);
+      for (int r = 0; r < RC; ++r) ur[r] = s_u[c0 + r][dm];
+      pin(ur);
+    };
+    float mr[RC], ur[RC], lr[RC];
+    int on[RC];
     float M = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < R; ++r) M = on[r] ? fmaxf(M, mr[r]) : M;
+    for (int c0 = 0; c0 < R; c0 += RC) {
+      if (R > RC || c0 == 0) chunk(c0, mr, lr, ur, on);
+#pragma unroll
+      for (int r = 0; r < RC; ++r) M = on[r] ? fmaxf(M, mr[r]) : M;
+    }
     float num = 0.f, den = 0.f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float f = wexp(mr[r], M);
-      num = on[r] ? num + f * ur[r] : num;
-      den = on[r] ? den + f * lr[r] : den;
+    for (int c0 = 0; c0 < R; c0 += RC) {
+      if (R > RC) chunk(c0, mr, lr, ur, on);   // one chunk: still in registers
+#pragma unroll
+      for (int r = 0; r < RC; ++r) {
+        const float f = wexp(mr[r], M);
+        num = on[r] ? num + f * ur[r] : num;
+        den = on[r] ? den + f * lr[r] : den;
+      }
     }
     a.out[(size_t)h * D + dm] = num / den;
   }
@@ -367,10 +387,15 @@ bool small_covers(int dtype, int hq, int hkv, int n, int b, int d, int topk, int
 int launch_small(int dtype, const SmallArgs& a, int bounds_dtype, hipStream_t st) {
   const dim3 grid(a.hq), block(kSmallThreads);
   const bool lb16 = bounds_dtype != 0;
-#define STK_SMALL_KB(T_, NCH_, KB_)                                                    \
-  do {                                                                                 \
-    if (lb16) hipLaunchKernelGGL((k_step_small<T_, NCH_, true, KB_>), grid, block, 0, st, a); \
-    else hipLaunchKernelGGL((k_step_small<T_, NCH_, false, KB_>), grid, block, 0, st, a);     \
+#define STK_SMALL_R(T_, NCH_, KB_, R_)                                                       \
+  do {                                                                                      \
+    if (lb16) hipLaunchKernelGGL((k_step_small<T_, NCH_, true, KB_, R_>), grid, block, 0, st, a); \
+    else hipLaunchKernelGGL((k_step_small<T_, NCH_, false, KB_, R_>), grid, block, 0, st, a);     \
+  } while (0)
+#define STK_SMALL_KB(T_, NCH_, KB_)                              \
+  do {                                                           \
+    if (a.k > 8 || a.sp > 8) STK_SMALL_R(T_, NCH_, KB_, 16);     \
+    else STK_SMALL_R(T_, NCH_, KB_, 8);                          \
   } while (0)
 #define STK_SMALL(T_, NCH_)                      \
   do {                                           \
@@ -386,6 +411,7 @@ int launch_small(int dtype, const SmallArgs& a, int bounds_dtype, hipStream_t st
   }
 #undef STK_SMALL
 #undef STK_SMALL_KB
+#undef STK_SMALL_R
   return stk_check_launch("k_step_small");
 }
 

@@ -1,6 +1,6 @@
 // The speculative step for small shapes in one launch (k_step_small,
 // step_small.hip): one workgroup per query head for up to 128 blocks per KV
-// head and up to eight selected and eight predicted rows per head.  Its
+// head and up to sixteen selected and sixteen predicted rows per head.  Its
 // sixteen waves split in two roles (step_small.hip).
 #pragma once
 
@@ -11,7 +11,7 @@ namespace stk {
 constexpr int kSmallThreads = 1024;
 constexpr int kSmallRoleWaves = 8;   // waves per role: predicted tiles | selection and misses
 constexpr int kSmallMaxN = 128;     // blocks per KV head: up to two per lane of the rank
-constexpr int kSmallMaxRows = 8;    // selected and predicted rows: one tile per wave each
+constexpr int kSmallMaxRows = 16;   // selected and predicted rows: up to two tiles per wave each
 
 struct SmallArgs {
   const void* q; const void* kk; const void* vv;   // q [hq, d], k / v [hkv, n, 32, d]
@@ -26,7 +26,7 @@ struct SmallArgs {
 };
 
 // True when k_step_small covers the fused step's shape: bf16 / fp16 K/V,
-// B = 32, D in {64, 128}, N <= 128, TOPK and SP in [1, 8], bounds FP32 or of
+// B = 32, D in {64, 128}, N <= 128, TOPK and SP in [1, 16], bounds FP32 or of
 // the K/V type, and 16-byte aligned q / k / v / lo / hi (`align`: the OR of
 // their addresses).
 bool small_covers(int dtype, int hq, int hkv, int n, int b, int d, int topk, int sp,

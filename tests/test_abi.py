@@ -74,14 +74,15 @@ def test_one_launch_support_matches_the_flag_slot(lib):
 
 
 def test_small_step_support_bounds(lib):
-    """stk_step_small_supported covers N <= 128, K and SP in [1, 8], B = 32,
+    """stk_step_small_supported covers N <= 128, K and SP in [1, 16], B = 32,
     D in {64, 128}, bf16 / fp16 K/V with FP32 or same-type bounds, int32
     predictions, and nothing the fused step itself rejects."""
     L = lib.lib()
     ok = (2, 8, 2, 64, 32, 128, 8, 8, 0, 0)            # bf16, FP32 bounds
     assert L.stk_step_small_supported(*ok) == 1
     assert L.stk_step_small_supported(1, 4, 4, 1, 32, 64, 1, 1, 0, 1) == 1   # fp16, fp16 bounds
-    for i, bad in ((3, 129), (6, 9), (6, 0), (7, 9), (7, 0), (4, 64), (5, 256), (8, 1)):
+    assert L.stk_step_small_supported(2, 8, 2, 128, 32, 128, 16, 16, 0, 0) == 1   # the largest
+    for i, bad in ((3, 129), (6, 17), (6, 0), (7, 17), (7, 0), (4, 64), (5, 256), (8, 1)):
         args = list(ok)
         args[i] = bad
         assert L.stk_step_small_supported(*args) == 0, (i, bad)

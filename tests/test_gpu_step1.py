@@ -98,7 +98,6 @@ def _same(res, ref):
     (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, True),     # c3, repair_union
     (16, 8, 512, 128, 64, 0.9, torch.bfloat16, False),     # c2 (G = 2)
     (4, 4, 130, 64, 8, 0.75, torch.float16, False),        # c1-like (G = 1, D = 64), past the small step
-                                                           # past the one-workgroup-per-head shapes
     (12, 3, 4000, 64, 50, 0.5, torch.float16, False),      # eight keys per tail thread
     (8, 8, 7000, 128, 16, 0.9, torch.bfloat16, False),     # sixteen keys per tail thread
     (6, 2, 333, 128, 40, 0.6, torch.bfloat16, False),      # G = 3, N not a chunk multiple

@@ -1,7 +1,7 @@
 """GPU parity of the small-shape step (one workgroup per query head).
 
 stk_speculative_step runs shapes with at most 128 blocks per KV head and at
-most eight selected and eight predicted rows per head in one workgroup per
+most sixteen selected and sixteen predicted rows per head in one workgroup per
 query head (k_step_small).  Bars, as for the other fused paths: selected IDs
 bit-exact against the FP64 oracle (ties toward the lower index, ascending);
 the prediction's block states and the output within the reference tolerance
@@ -69,6 +69,10 @@ def _check(res, host, p_host, topk, union, what):
     (4, 4, 128, 64, 8, 0.75, torch.float16, "fp32", False),  # two blocks per lane of the rank
     (8, 2, 100, 128, 8, 0.5, torch.bfloat16, "k", True),     # N between 64 and 128, union
     (6, 3, 65, 128, 5, 0.0, torch.bfloat16, "fp32", False),  # one block past 64, every block missed
+    (4, 4, 128, 64, 16, 0.75, torch.float16, "fp32", False), # sixteen rows: two slots per wave
+    (8, 2, 100, 128, 12, 0.5, torch.bfloat16, "k", True),    # twelve rows, union
+    (4, 4, 64, 64, 16, 0.0, torch.float16, "k", False),      # sixteen misses: two rounds of halves
+    (4, 2, 40, 128, 9, 0.6, torch.bfloat16, "fp32", False),  # nine rows
 ])
 def test_small_step(hq, hkv, n, d, topk, overlap, dtype, bounds, union):
     from stk_harness.configs import make_qkv, perturb
@@ -107,15 +111,16 @@ def test_small_step_predictions_with_invalid_and_repeated_ids():
 
 
 def test_small_step_not_covered():
-    """Past 128 blocks, 8 selected or 8 predicted rows, other block sizes and
+    """Past 128 blocks, 16 selected or 16 predicted rows, other block sizes and
     head dims, the step takes the other paths."""
     from strict_topk import _lib
     L = _lib.lib()
     assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 8, 8, 0, 0) == 1
     assert L.stk_step_small_supported(1, 4, 4, 128, 32, 64, 8, 8, 0, 0) == 1
     assert L.stk_step_small_supported(1, 4, 4, 129, 32, 64, 8, 8, 0, 0) == 0  # N
-    assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 9, 8, 0, 0) == 0   # TOPK
-    assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 8, 9, 0, 0) == 0   # SP
+    assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 16, 16, 0, 0) == 1
+    assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 17, 8, 0, 0) == 0  # TOPK
+    assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 8, 17, 0, 0) == 0  # SP
     assert L.stk_step_small_supported(1, 4, 4, 64, 16, 64, 8, 8, 0, 0) == 0   # B
     assert L.stk_step_small_supported(2, 4, 4, 64, 32, 256, 8, 8, 0, 2) == 0  # D
     assert L.stk_step_small_supported(0, 4, 4, 64, 32, 64, 8, 8, 0, 0) == 0   # fp32 K/V
@@ -174,3 +179,22 @@ def test_step_nonfinite_bounds(n):
     res = step.speculative_step(qd, kd, vd, lod, hid, pd, topk)
     torch.cuda.synchronize()
     assert res.selected.cpu().numpy().tolist() == ref.tolist()
+
+
+@pytest.mark.parametrize("n,topk,sp,union", [(64, 6, 12, False), (100, 14, 5, True),
+                                            (128, 16, 16, True), (30, 3, 16, False)])
+def test_small_step_rows_differ(n, topk, sp, union):
+    """Predicted rows of a width other than K (SP above and below 8, both
+    row counts of the kernel): IDs, states and output against the oracle."""
+    from stk_harness.configs import make_qkv, perturb
+    from strict_topk import step
+    hq, hkv, d = 8, 4, 64
+    q, k, v, lo, hi = make_qkv(hq, hkv, d, 32, n, torch.bfloat16, True, 31 + n + sp)
+    ids = O.select_blocks(C.f64(q), lo.numpy(), hi.numpy(), topk)
+    p = perturb(torch.from_numpy(ids), n, sp, 0.6, n + sp)
+    assert p.shape == (hq, sp)
+    qd, kd, vd, lod, hid, pd = (t.cuda() for t in (q, k, v, lo, hi, p))
+    assert _small(qd, kd, topk, sp, lod)
+    res = step.speculative_step(qd, kd, vd, lod, hid, pd, topk, union=union)
+    torch.cuda.synchronize()
+    _check(res, (q, k, v, lo, hi), p, topk, union, (n, topk, sp, union))
