@@ -145,19 +145,20 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
     if ((mflags >> i) & 1u) miss[mpos++] = idx;
   }
   __syncthreads();
-  // ---- every state published (or, rarely, a wait for the last ones), then
-  // each wave's first missed tile and the state rows together.  The wait
-  // comes first: a wait issued after the tile's loads would wait for the tile
-  // too (loads return in order)
+  // ---- each wave's first missed tile (it needs no state), then every state
+  // published, then the state rows.  Checking the flag values requested
+  // before the scan waits for them only (loads return in order, and the
+  // tile's went out after them); only the rare wait for the last flags also
+  // waits behind the tile
   const int kvh = h / G;
   const float scale = 1.0f / sqrtf((float)D);
   const T* K = reinterpret_cast<const T*>(a.kv.k);
   const T* V = reinterpret_cast<const T*>(a.kv.v);
   auto tile = [&](int x) { return (((size_t)kvh * n + miss[x]) * a.kv.b) * D; };
   uint32_t kw[2][TT::QW], vw[TT::CH][TT::VW];
+  if (w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
   if (!__all((fv0 != 0u || fl0 >= sp) && (fv1 != 0u || fl1 >= sp)))
     ok = wait_flags(tflag, sp, A.err, A.spin) && ok;
-  if (w < nm) t.load(K + tile(w), V + tile(w), 0, kw, vw);
   // ---- this head's prediction states (thread (rg, c4): columns 4 c4 .. +3
   // of rows rg + RG j)
   const int c4 = tid % TPR, rg = tid / TPR;
