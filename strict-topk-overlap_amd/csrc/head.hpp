@@ -54,8 +54,24 @@ __device__ __forceinline__ void membership(HeadLds& s, int sp, int sa) {
   __syncthreads();
 }
 
+// Keeps N loaded values live at one point (groups of eight), so that the
+// compiler moves none of their loads under a later branch and waits for them
+// once.
+template <int N>
+__device__ __forceinline__ void hold_all(float (&x)[N]) {
+  static_assert(N % 8 == 0, "groups of eight");
+#pragma unroll
+  for (int i = 0; i < N; i += 8)
+    asm volatile("" : "+v"(x[i]), "+v"(x[i + 1]), "+v"(x[i + 2]), "+v"(x[i + 3]),
+                 "+v"(x[i + 4]), "+v"(x[i + 5]), "+v"(x[i + 6]), "+v"(x[i + 7]));
+}
+
 // Weighted sum over rows j < count of (l[j], u[j,:]) with weight w(j)
 // (rows with w == 0 are skipped).  Result: returned z, vector in out[D].
+// A thread takes its rows four at a time: the four rows' weights, l and u
+// columns are all requested before any is used (one round trip per four
+// rows instead of two per row), and the sums run in the same order as one
+// row at a time, so the result is the same bits.
 template <typename W, typename L, typename UR>
 __device__ __forceinline__ float sum_states(HeadLds& s, int count, int d, W weight, L lval,
                                             UR urow, float* out) {
@@ -65,15 +81,32 @@ __device__ __forceinline__ float sum_states(HeadLds& s, int count, int d, W weig
   int tr = threadIdx.x / dt, td = threadIdx.x % dt;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   float z = 0.f;
-  for (int j = tr; j < count; j += rg) {
-    float w = weight(j);
-    if (w == 0.f) continue;
-    if (td == 0) z += w * lval(j);
-    const float* ur = urow(j);
+  constexpr int UB = 4;   // rows per batch
+  for (int j0 = tr; j0 < count; j0 += UB * rg) {
+    float w[UB * 2], uv[UB * 4];   // w[u] weight, w[UB + u] l
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      int dd = td + c * dt;
-      if (dd < d) acc[c] += w * ur[dd];
+    for (int u = 0; u < UB; ++u) {
+      const int j = j0 + u * rg;
+      const int jc = j < count ? j : j0;   // rows past count read row j0, weight 0
+      const float wj = weight(jc);
+      w[u] = j < count ? wj : 0.f;
+      w[UB + u] = lval(jc);
+      const float* ur = urow(jc);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        // columns past D read column 0; their accumulators are never read
+        const int dd = td + c * dt;
+        uv[4 * u + c] = ur[dd < d ? dd : 0];
+      }
+    }
+    hold_all(w);
+    hold_all(uv);
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      if (w[u] == 0.f) continue;   // a skipped row's l and u add nothing, NaN included
+      if (td == 0) z += w[u] * w[UB + u];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] += w[u] * uv[4 * u + c];
     }
   }
   z = block_sum(z, s.red);
