@@ -127,29 +127,31 @@ def test_small_step_not_covered():
     assert L.stk_step_small_supported(1, 4, 4, 64, 32, 64, 8, 8, 1, 0) == 0   # int64 IDs
 
 
-def test_small_step_in_a_graph():
+@pytest.mark.parametrize("n,topk", [(64, 8), (120, 16)])   # eight rows; two keys per lane, sixteen rows
+def test_small_step_in_a_graph(n, topk):
     """Captured in a graph and replayed while the query changes in place:
     every replay equals the eager step on the same inputs."""
     from stk_harness.configs import make_qkv, perturb
     from strict_topk import step
-    q, k, v, lo, hi = make_qkv(4, 4, 64, 32, 64, torch.float16, True, 5)
-    ids = O.select_blocks(C.f64(q), lo.numpy(), hi.numpy(), 8)
-    p = perturb(torch.from_numpy(ids), 64, 8, 0.75, 5)
+    q, k, v, lo, hi = make_qkv(4, 4, 64, 32, n, torch.float16, True, 5)
+    ids = O.select_blocks(C.f64(q), lo.numpy(), hi.numpy(), topk)
+    p = perturb(torch.from_numpy(ids), n, topk, 0.75, 5)
     qd, kd, vd, lod, hid, pd = (t.cuda() for t in (q, k, v, lo, hi, p))
-    step.speculative_step(qd, kd, vd, lod, hid, pd, 8)
+    assert _small(qd, kd, topk, topk, lod)
+    step.speculative_step(qd, kd, vd, lod, hid, pd, topk)
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
-            out = step.speculative_step(qd, kd, vd, lod, hid, pd, 8)
+            out = step.speculative_step(qd, kd, vd, lod, hid, pd, topk)
     torch.cuda.current_stream().wait_stream(s)
     gen = torch.Generator().manual_seed(3)
     for _ in range(3):
         qd.copy_(torch.randn((4, 64), generator=gen).to(torch.float16))
         g.replay()
         torch.cuda.synchronize()
-        eager = step.speculative_step(qd, kd, vd, lod, hid, pd, 8)
+        eager = step.speculative_step(qd, kd, vd, lod, hid, pd, topk)
         torch.cuda.synchronize()
         assert torch.equal(out.selected, eager.selected)
         assert torch.equal(out.output, eager.output)

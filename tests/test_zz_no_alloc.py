@@ -58,7 +58,8 @@ def _same(ref, sel, st, out):
 def test_noalloc_matches_workspace_step(union):
     from strict_topk import step
     shapes = [(32, 8, 2048, 32, 128, 64, torch.bfloat16, 0.9),   # c3
-              (8, 2, 300, 16, 64, 20, torch.float16, 0.75)]     # smaller, second
+              (8, 2, 300, 16, 64, 20, torch.float16, 0.75),     # smaller, second
+              (4, 4, 100, 32, 64, 12, torch.float16, 0.75)]     # one workgroup per head
     for i, (hq, hkv, n, b, d, topk, dt, ov) in enumerate(shapes):
         print(f"noalloc call {i}: hq={hq} n={n} d={d} union={union}", flush=True)
         (q, k, v, lo, hi, p), (qh, kh, vh, ids) = _inputs(hq, hkv, n, b, d, topk, dt,
