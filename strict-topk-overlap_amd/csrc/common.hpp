@@ -245,6 +245,18 @@ __device__ __forceinline__ float wave_max(float v) { return xor_reduce(v, 1, 32,
 
 __device__ __forceinline__ int wave_any(bool p) { return __any(p); }
 
+// Keeps N loaded values live at one point (groups of eight), so that the
+// compiler moves none of their loads under a later branch and waits for them
+// once.
+template <int N>
+__device__ __forceinline__ void hold_all(float (&x)[N]) {
+  static_assert(N % 8 == 0, "groups of eight");
+#pragma unroll
+  for (int i = 0; i < N; i += 8)
+    asm volatile("" : "+v"(x[i]), "+v"(x[i + 1]), "+v"(x[i + 2]), "+v"(x[i + 3]),
+                 "+v"(x[i + 4]), "+v"(x[i + 5]), "+v"(x[i + 6]), "+v"(x[i + 7]));
+}
+
 // Wave-wide max (MAX) or min of an unsigned word, returned in every lane.
 template <bool MAX>
 __device__ __forceinline__ uint32_t wave_ext_u32(uint32_t v) {

@@ -54,18 +54,6 @@ __device__ __forceinline__ void membership(HeadLds& s, int sp, int sa) {
   __syncthreads();
 }
 
-// Keeps N loaded values live at one point (groups of eight), so that the
-// compiler moves none of their loads under a later branch and waits for them
-// once.
-template <int N>
-__device__ __forceinline__ void hold_all(float (&x)[N]) {
-  static_assert(N % 8 == 0, "groups of eight");
-#pragma unroll
-  for (int i = 0; i < N; i += 8)
-    asm volatile("" : "+v"(x[i]), "+v"(x[i + 1]), "+v"(x[i + 2]), "+v"(x[i + 3]),
-                 "+v"(x[i + 4]), "+v"(x[i + 5]), "+v"(x[i + 6]), "+v"(x[i + 7]));
-}
-
 // Weighted sum over rows j < count of (l[j], u[j,:]) with weight w(j)
 // (rows with w == 0 are skipped).  Result: returned z, vector in out[D].
 // A thread takes its rows four at a time: the four rows' weights, l and u

@@ -249,15 +249,29 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   if (tid < sp) st_agent(tflag + tid, 0u);
   // ---- one LSE merge of the hits' partials and the waves' miss states
   if (tid < D) {
+    // every LDS value the merge reads is requested before any is used
+    float hm[kTailWaves], wm[kTailWaves], hl[kTailWaves], wl[kTailWaves];
+    float hu[kTailWaves], wu[kTailWaves];
+#pragma unroll
+    for (int x = 0; x < kTailWaves; ++x) {
+      hm[x] = s_hmax[x];
+      wm[x] = s_wm[x];
+      hl[x] = s_hl[x];
+      wl[x] = s_wl[x];
+      hu[x] = s_hu[x][tid];
+      wu[x] = s_wu[x][tid];
+    }
+    hold_all(hu);
+    hold_all(wu);
     float M = -INFINITY;
 #pragma unroll
-    for (int x = 0; x < kTailWaves; ++x) M = fmaxf(M, fmaxf(s_hmax[x], s_wm[x]));
+    for (int x = 0; x < kTailWaves; ++x) M = fmaxf(M, fmaxf(hm[x], wm[x]));
     float num = 0.f, den = 0.f;
 #pragma unroll
     for (int x = 0; x < kTailWaves; ++x) {
-      const float fh = wexp(s_hmax[x], M), f = wexp(s_wm[x], M);
-      num += fh * s_hu[x][tid] + f * s_wu[x][tid];
-      den += fh * s_hl[x] + f * s_wl[x];
+      const float fh = wexp(hm[x], M), f = wexp(wm[x], M);
+      num += fh * hu[x] + f * wu[x];
+      den += fh * hl[x] + f * wl[x];
     }
     a.out[(size_t)h * D + tid] = fail ? __builtin_nanf("") : num / den;
   }

@@ -56,18 +56,6 @@ __device__ __forceinline__ void lds_wait(int* c, int v) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Keeps loaded values live at one point, so that the compiler sinks none of
-// their LDS reads into a branch (a select on a loaded value can otherwise
-// become a branch around the read) and issues them all before the first use.
-template <int N>
-__device__ __forceinline__ void pin(float (&x)[N]) {
-  static_assert(N % 8 == 0, "groups of eight");
-#pragma unroll
-  for (int i = 0; i < N; i += 8)
-    asm volatile("" : "+v"(x[i]), "+v"(x[i + 1]), "+v"(x[i + 2]), "+v"(x[i + 3]),
-                 "+v"(x[i + 4]), "+v"(x[i + 5]), "+v"(x[i + 6]), "+v"(x[i + 7]));
-}
-
 // KB: blocks per lane of the rank (MAXN = 64 KB blocks per KV head at most);
 // ROWS: the most selected and the most predicted rows per head (8 or 16).
 template <typename T, int NCH, bool LB16, int KB, int ROWS>
@@ -348,7 +336,7 @@ __global__ __launch_bounds__(kSmallThreads) void k_step_small(SmallArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < RC; ++r) ur[r] = s_u[c0 + r][dm];
-      pin(ur);
+      hold_all(ur);
     };
     float mr[RC], ur[RC], lr[RC];
     int on[RC];
