@@ -99,9 +99,22 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   if (tid == 0) s_fail = 0;
   __syncthreads();   // the clears before any use (the flags take far longer)
   // ---- this head's keys and their range, once every chunk of its KV head
-  // is published
-  uint32_t hmax, hmin;
-  bool ok = wait_flags_range(sflag, chunks, A.err, A.spin, hmax, hmin);
+  // is published.  Wave 0 polls the flags and the others wait at a barrier:
+  // eight waves polling on their own phases would start the top-K with the
+  // last of eight sightings
+  __shared__ uint32_t s_rng[3];
+  if (w == 0) {
+    uint32_t mx, mn;
+    const bool got = wait_flags_range(sflag, chunks, A.err, A.spin, mx, mn);
+    if (lane_id() == 0) {
+      s_rng[0] = mx;
+      s_rng[1] = mn;
+      s_rng[2] = got;
+    }
+  }
+  __syncthreads();
+  const uint32_t hmax = s_rng[0], hmin = s_rng[1];
+  bool ok = s_rng[2] != 0u;
   uint64_t key[KPT];
   {
     const uint64_t* rk = a.keys + (size_t)h * n;
