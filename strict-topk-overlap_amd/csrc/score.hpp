@@ -51,8 +51,9 @@ struct ScoreArgs {
   int chunks;            // workgroups per KV head
   float* scores;         // optional FP32 [hq, n]
   uint64_t* keys;        // optional [hq, n]
-  uint32_t* sflag;       // SIG: [hq, chunks], set (to the chunk's key range, never 0)
-                         // once a chunk's keys are published
+  uint32_t* sflag;       // SIG: [hq, fstride], entry chunk set (to the chunk's key
+                         // range, never 0) once the chunk's keys are published
+  int fstride;           // SIG: flag words per query head (>= chunks)
   int drop;              // SIG, tests only: publish no flag (the consumers time out)
 };
 
@@ -349,7 +350,7 @@ __device__ __forceinline__ void score_wg(const ScoreArgs& a, int wg,
         mx = s_rng[w][threadIdx.x][0] > mx ? s_rng[w][threadIdx.x][0] : mx;
         mn = s_rng[w][threadIdx.x][1] < mn ? s_rng[w][threadIdx.x][1] : mn;
       }
-      st_agent(a.sflag + (size_t)(h0 + threadIdx.x) * a.chunks + chunk,
+      st_agent(a.sflag + (size_t)(h0 + threadIdx.x) * a.fstride + chunk,
                ((mx >> 16) << 16) | (mn >> 16));
     }
   }

@@ -210,8 +210,8 @@ static int step_call(const void* q, const void* k, const void* v, int dtype, int
     const int rc = ctl_slot(st, step1_ctl_words(hq, n, sp), &ctl);
     if (rc) return rc;
     if (ctl)
-      return launch_step1(dtype, f, t, s, ctl, ctl + kCtlSlotWords - 1, g_step1_spin.load(),
-                          g_step1_drop.load(), st);
+      return launch_step1(dtype, f, t, s, ctl, kCtlSlotWords - 1, ctl + kCtlSlotWords - 1,
+                          g_step1_spin.load(), g_step1_drop.load(), st);
   }
   if (front) {
     const int rc = launch_front(dtype, f, s, st);

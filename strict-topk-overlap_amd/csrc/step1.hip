@@ -24,7 +24,8 @@ int launch_t(const Step1Args& a, const StepShape& s, hipStream_t st) {
 }  // namespace
 
 int launch_step1(int dtype, const FrontArgs& f, const TailArgs& t, const StepShape& s,
-                 uint32_t* ctl, uint32_t* err, uint64_t spin, int drop, hipStream_t st) {
+                 uint32_t* ctl, size_t cap, uint32_t* err, uint64_t spin, int drop,
+                 hipStream_t st) {
   if (!step1_covers(dtype, t.kv.hq, t.kv.hkv, t.kv.b, t.kv.d, s)) return 1;
   Step1Args a{};
   a.f = f;
@@ -34,8 +35,12 @@ int launch_step1(int dtype, const FrontArgs& f, const TailArgs& t, const StepSha
   a.S = t.kv.hkv * a.f.sc.chunks;
   a.T = (int)(((int64_t)hq * t.sp + kStep1Waves - 1) / kStep1Waves);
   a.H = hq;
+  // each head's chunk flags on a 128-byte line of their own when the slot
+  // holds that layout, else packed
+  const int line = (a.f.sc.chunks + 31) & ~31;
+  a.f.sc.fstride = (size_t)hq * (line + t.sp) <= cap ? line : a.f.sc.chunks;
   a.f.sc.sflag = ctl;
-  a.f.st.tflag = ctl + (size_t)hq * a.f.sc.chunks;
+  a.f.st.tflag = ctl + (size_t)hq * a.f.sc.fstride;
   a.err = err;
   a.spin = spin;
   a.f.sc.drop = a.f.st.drop = drop;

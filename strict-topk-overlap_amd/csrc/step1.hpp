@@ -44,15 +44,15 @@ constexpr int kStep1Waves = kStep1Threads / STK_WAVE;
 constexpr int kStep1Blocks = kStep1Waves * 4 * 2;   // blocks per scoring chunk
 
 struct Step1Args {
-  FrontArgs f;       // f.sc.sflag [hq, chunks], f.st.tflag [hq * sp]
+  FrontArgs f;       // f.sc.sflag [hq, fstride], f.st.tflag [hq * sp]
   TailArgs t;
   uint32_t* err;     // counts timed-out waits
   uint64_t spin;     // longest wait, in ticks of the 100 MHz real-time counter
   int S, T, H;       // workgroups per role: scoring, states, tails
 };
 
-// The flag array's words: one per (query head, chunk) and per (query head,
-// slot).
+// The flag array's fewest words: one per (query head, chunk) and per (query
+// head, slot).
 inline size_t step1_ctl_words(int hq, int n, int sp) {
   const size_t chunks = ((size_t)n + kStep1Blocks - 1) / kStep1Blocks;
   return (size_t)hq * chunks + (size_t)hq * sp;
@@ -79,7 +79,7 @@ __device__ __forceinline__ void step1_tail(const Step1Args& A, int h) {
   const int tid = threadIdx.x, w = wave_id();
   const int G = a.kv.hq / a.kv.hkv;
   const int chunks = A.f.sc.chunks;
-  uint32_t* sflag = A.f.sc.sflag + (size_t)h * chunks;
+  uint32_t* sflag = A.f.sc.sflag + (size_t)h * A.f.sc.fstride;
   uint32_t* tflag = A.f.st.tflag + (size_t)h * sp;
   // ---- what depends on nothing: the predicted row and the query row
   const int pid = (int)ld_or(a.p, (int64_t)h * sp + tid, tid < sp, (int32_t)-1);
@@ -320,11 +320,13 @@ __global__ __launch_bounds__(kStep1Threads, 4) void k_step1(Step1Args a) {
 bool step1_covers(int dtype, int hq, int hkv, int b, int d, const StepShape& s);
 
 // Launch k_step1 when step1_covers the shape (returns 1 otherwise, with
-// nothing launched).  ctl: step1_ctl_words(hq, n, sp) zero words (left
-// zero); err: a word incremented for every timed-out wait; spin: the longest
+// nothing launched).  ctl: `cap` >= step1_ctl_words(hq, n, sp) zero words
+// (left zero; when they fit, each head's chunk flags start a 128-byte line of
+// their own, so that no two heads' pollers share one); err: a word incremented for every timed-out wait; spin: the longest
 // wait in ticks; drop (tests only): the producers publish no flag, so every
 // wait times out.
 int launch_step1(int dtype, const FrontArgs& f, const TailArgs& t, const StepShape& s,
-                 uint32_t* ctl, uint32_t* err, uint64_t spin, int drop, hipStream_t st);
+                 uint32_t* ctl, size_t cap, uint32_t* err, uint64_t spin, int drop,
+                 hipStream_t st);
 
 }  // namespace stk
