@@ -102,6 +102,9 @@ def _same(res, ref):
     (8, 8, 7000, 128, 16, 0.9, torch.bfloat16, False),     # sixteen keys per tail thread
     (6, 2, 333, 128, 40, 0.6, torch.bfloat16, False),      # G = 3, N not a chunk multiple
     (4, 4, 64, 64, 64, 1.0, torch.float16, False),         # K = N: every block selected
+    # 128 heads * (64 + 64) flag words would fill the slot: each head's 33
+    # chunk flags packed after the previous head's (128 * (33 + 64) words)
+    (128, 32, 2112, 64, 64, 0.9, torch.float16, False),
     (32, 8, 2048, 128, 64, 0.9, torch.bfloat16, "fp32"),   # c3 with the reference's FP32 bounds
     (4, 4, 130, 64, 8, 0.75, torch.float16, "fp32"),       # c1-like with FP32 bounds
 ])
